@@ -1,0 +1,231 @@
+/*
+ * mlx_nufft_amd.h -- C-ABI of the MI355X NUFFT engine (libmlxnufft_amd.so).
+ *
+ * Every entry point is asynchronous on the HIP stream it is given (the
+ * caller's stream; from PyTorch, torch.cuda.current_stream().cuda_stream),
+ * takes plain device pointers and sizes, and returns an int status:
+ *   MN_OK (0), MN_EINVAL (-1, bad argument), MN_ERUNTIME (-2, HIP/rocFFT
+ *   failure), MN_ENOTIMPL (-3, unsupported combination).
+ * On a non-zero status, mn_last_error() returns a message for the calling
+ * thread. The library owns no caller data; it keeps only a mutex-guarded
+ * rocFFT plan cache (plus the plans' work buffers).
+ *
+ * Complex data are interleaved complex64 (float re, float im) -- the
+ * layout of numpy/torch complex64. Grids are C-ordered (last dim fastest).
+ *
+ * Citations "ref:" name the reference (mlx-nufft) code each entry point
+ * replaces; the reference's kernels are Metal source strings built per plan
+ * and launched through mx.fast.metal_kernel, so the citations point at
+ * those builders and launches.
+ */
+#ifndef MLX_NUFFT_AMD_H
+#define MLX_NUFFT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MN_OK 0
+#define MN_EINVAL (-1)
+#define MN_ERUNTIME (-2)
+#define MN_ENOTIMPL (-3)
+
+typedef void *mn_stream_t; /* a hipStream_t; NULL = the default stream */
+
+/*
+ * Fine-grid bin geometry shared by setpts, sort, spread and interp.
+ * dim in {1,2,3}; w = ES kernel width (2..16); n[d] = fine-grid size along
+ * dim d (1 for d >= dim); m[d] = bin size (cells) along d; nb[d] = number
+ * of bins along d = ceil(n[d]/m[d]). A point with cell index i1 (leftmost
+ * tap) lies in bin b[d] = ((i1[d] + w/2) mod n[d]) / m[d]; its bin key is
+ * the row-major index of b over nb. The padded tile of a bin has
+ * p[d] = m[d] + w - 1 cells and origin b[d]*m[d] - w/2.
+ * ref: nd.py:282-296 (_od_tile_dims), nd.py:298-320 (_od_prepare key).
+ */
+typedef struct mn_bins {
+    int32_t dim;
+    int32_t w;
+    int64_t n[3];
+    int32_t m[3];
+    int32_t nb[3];
+} mn_bins;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *mn_last_error(void);
+/* ABI version (major*10000 + minor*100 + patch). */
+int mn_version(void);
+
+/*
+ * Type-1/2 point setup ("crit64"): per point and dim, r = x mod 2pi with
+ * numpy's np.mod semantics, xi = r / h (h = 2pi/n[d], fp64 division),
+ * i1 = ceil(xi - w/2) (int32), fr = (float)(xi - i1), and the bin key.
+ * prec64 = 1 reproduces the fp64 path bit for bit; prec64 = 0 the "fp32"
+ * path (r and h rounded to fp32, fp32 divide).
+ * ref: nd.py:152-165 (_compute_cells), nd.py:43-91 + nd.py:191-222
+ * (df64 GPU re-point), nd.py:308-313 (bin key).
+ */
+int mn_setpts_t12(const mn_bins *g, int64_t P, const double *const x[3],
+                  int prec64, int32_t *const i1[3], float *const fr[3],
+                  uint32_t *key, mn_stream_t stream);
+
+/*
+ * Stable LSD radix sort of P uint32 keys (key_bits significant bits):
+ * perm_out = argsort(key_in, stable), key_out = key_in[perm_out].
+ * ws must hold mn_sort_workspace_bytes(P) bytes of device memory.
+ * ref: nd.py:314 (np.argsort(key, kind="stable")), nd.py:338 (mx.argsort),
+ * nd.py:175 (lateral sort), gpu_t3.py:490-492, gpu_t3.py:546.
+ */
+int64_t mn_sort_workspace_bytes(int64_t P);
+int mn_sort_keys(int64_t P, int key_bits, const uint32_t *key_in,
+                 uint32_t *key_out, uint32_t *perm_out, void *ws,
+                 int64_t ws_bytes, mn_stream_t stream);
+
+/*
+ * Gather per-point arrays into sorted order: out[j] = in[perm[j]] for i1
+ * and fr of each dim, and for an optional complex64 array (extra_in may
+ * be NULL). ref: nd.py:316-318, nd.py:339-340, gpu_t3.py:496-501.
+ */
+int mn_gather_points(int dim, int64_t P, const uint32_t *perm,
+                     const int32_t *const i1_in[3], const float *const fr_in[3],
+                     int32_t *const i1_out[3], float *const fr_out[3],
+                     const void *extra_in, void *extra_out, mn_stream_t stream);
+
+/*
+ * Subproblem table from the sorted bin keys: every non-empty bin is split
+ * into chunks of at most msub points; sub_info receives 3 int32 per
+ * subproblem (bin key, first sorted index, count), ordered by bin. The
+ * table needs room for max_sub = nbins + P/msub + 1 rows. *nsub_out is
+ * written on the host after the stream is synchronised (this call blocks).
+ * ws must hold mn_subproblem_workspace_bytes(g) bytes.
+ * ref: nd.py:347-372 (_od_finish), nd.py:341 (the reference's P-length
+ * host sync, replaced here by one 8-byte read-back).
+ */
+int64_t mn_subproblem_workspace_bytes(const mn_bins *g);
+int mn_build_subproblems(const mn_bins *g, int64_t P, const uint32_t *sorted_key,
+                         int32_t msub, int32_t *sub_info, int64_t max_sub,
+                         int64_t *nsub_out, void *ws, int64_t ws_bytes,
+                         mn_stream_t stream);
+
+/*
+ * Spread (type-1 core): grid[cell] = sum_j c_j * prod_d psi(cell_d - x_j,d)
+ * over the periodic fine grid, psi(d) = exp(beta*(sqrt(1-(2d/w)^2)-1)).
+ * Points are read in sorted order (i1s/frs) and their strengths gathered
+ * as c[perm[j]] (c in caller order); if pre != NULL the strength is
+ * multiplied by pre[j] (sorted order; the type-3 prephase). One workgroup
+ * per subproblem accumulates its padded tile in LDS and flushes it with
+ * fp32 global atomics. grid (prod n complex64) is overwritten.
+ * ref: nd.py:492-579 + nd.py:590-601 (OD spread), nd.py:437-490 (GM
+ * spread), gpu_t3.py:565-591 + gpu_t3.py:1302-1311 (type-3 spread).
+ */
+int mn_spread(const mn_bins *g, float beta, int64_t P, int64_t nsub,
+              const int32_t *sub_info, const uint32_t *perm,
+              const int32_t *const i1s[3], const float *const frs[3],
+              const void *c, const void *pre, void *grid, mn_stream_t stream);
+
+/*
+ * Batched spread: B strength vectors cs (B x P, caller order, row-major)
+ * over the same points into B grids (B x prod n, overwritten); the ES
+ * weights are computed once per point and applied to every vector.
+ * ref: nd.py:683-742 (_get_batch_spread), nd.py:744-794 (execute_batch).
+ */
+int mn_spread_batch(const mn_bins *g, float beta, int64_t P, int64_t nsub,
+                    const int32_t *sub_info, const uint32_t *perm,
+                    const int32_t *const i1s[3], const float *const frs[3],
+                    int64_t B, const void *cs, void *grids, mn_stream_t stream);
+
+/*
+ * Interpolation (type-2 core): out[perm[j]] = post[j] * sum over the w^dim
+ * taps of grid[cell] * prod_d psi(cell_d - x_j,d); post may be NULL (= 1).
+ * One workgroup per subproblem loads its padded tile into LDS once.
+ * ref: nd.py:974-1073 + nd.py:1093-1102 (OD gather), nd.py:908-972 (GM
+ * gather), gpu_t3.py:653-693 + gpu_t3.py:1337-1343 (type-3 gather x post).
+ */
+int mn_interp(const mn_bins *g, float beta, int64_t P, int64_t nsub,
+              const int32_t *sub_info, const uint32_t *perm,
+              const int32_t *const i1s[3], const float *const frs[3],
+              const void *grid, const void *post, void *out, mn_stream_t stream);
+
+/*
+ * Mode shuffle + deconvolution, type 1: for a batch of grids (n_up) and
+ * mode boxes (N, modeord=0, k_d in [-(N_d/2), N_d - N_d/2)):
+ * fk[b][m] = grid[b][(m - N/2) mod n_up] * prod_d dec_d[m_d].
+ * ref: nd.py:416-435 (t1crop), nd.py:615-621.
+ */
+int mn_crop_deconv(int dim, const int64_t n_up[3], const int64_t N[3],
+                   int64_t batch, const void *grid, const float *const dec[3],
+                   void *fk, mn_stream_t stream);
+
+/*
+ * Inverse of the above (type 2, and the type-3 inner pad with N = nf):
+ * grid[b][r] = fk[b][m] * prod_d dec_d[m_d] where r = (m - N/2) mod n_up,
+ * and 0 at every off-band cell. grid is fully overwritten.
+ * ref: nd.py:878-906 (t2pad), nd.py:1084-1089, gpu_t3.py:630-651 (t3pad).
+ */
+int mn_pad_deconv(int dim, const int64_t n_up[3], const int64_t N[3],
+                  int64_t batch, const void *fk, const float *const dec[3],
+                  void *grid, mn_stream_t stream);
+
+/*
+ * Type-3 source setup on the nf grid g (dim 3): per dim
+ * xi = ((x - C)/gam)/hd + nf/2 (fp64, numpy operation order), i1, fr,
+ * bin key, and the prephase pre[j] = exp(i*isign*(D0 x0 + D1 x1 + D2 x2))
+ * (caller order, complex64). prec_flags: bit 0 = coordinate rescale in fp64
+ * (else fp32), bit 1 = phase angles in fp64 (else fp32); "crit64" = 3.
+ * ref: gpu_t3.py:474-488 (host), gpu_t3.py:237-276 + 508-555 (df64 GPU),
+ * gpu_t3.py:345-346 (precision modes).
+ */
+int mn_t3_setpts_src(const mn_bins *g, int64_t P, const double *const x[3],
+                     const double C[3], const double gam[3], const double hd[3],
+                     const double D[3], int isign, int prec_flags,
+                     int32_t *const i1[3], float *const fr[3], uint32_t *key,
+                     void *pre, mn_stream_t stream);
+
+/*
+ * Type-3 target setup on the n_up grid g (dim 3, kernel width g->w = w2):
+ * theta = (s - D)*hg, lam = theta/h2 + n_up/2, i1, fr, bin key, and
+ * post[k] = exp(i*isign*sum_d C_d (s_d - D_d)) / prod_d phihat(theta_d),
+ * phihat(xi) = 2 sum_q fq[q] cos(xi dq[q]) with quad = [dq(nquad), fq(nquad)]
+ * (device fp64; fq = GL weight * psi(dq) of the outer kernel). prec_flags
+ * as for mn_t3_setpts_src.
+ * ref: gpu_t3.py:357-377, sizing.py:74-85 (kernel_ft).
+ */
+int mn_t3_setpts_trg(const mn_bins *g, int64_t M, const double *const s[3],
+                     const double D[3], const double hg[3], const double h2[3],
+                     const double C[3], int isign, int prec_flags,
+                     const double *quad, int nquad, int32_t *const i1[3],
+                     float *const fr[3], uint32_t *key, void *post,
+                     mn_stream_t stream);
+
+/*
+ * e^{i*isign*phi}, phi = sum of ncomp (1..8) fp64 component arrays of n
+ * elements (comps is a host array of device pointers), summed and reduced
+ * in native fp64 on the GPU; out is complex64.
+ * ref: dfmath.py:29-54 (expi_df64 kernel), dfmath.py:57-134 (expi).
+ */
+int mn_expi(int ncomp, const double *const *comps, int64_t n, int isign,
+            void *out, mn_stream_t stream);
+
+/*
+ * In-place complex64 FFT of `batch` contiguous C-ordered grids of shape
+ * n[0..dim-1]; isign > 0 runs the unnormalised backward transform
+ * (e^{+i}), isign < 0 the forward one (e^{-i}). rocFFT plans (and their
+ * work buffers) are cached per (device, dim, n, batch, direction).
+ * ref: gpu_t3.py:94-148 (fft_axis), nd.py:374-383 (_fft_grid),
+ * vkfft_bridge/vkfft_bridge.cpp:25-71 (plan cache + in-place execute).
+ */
+int mn_fft_exec(int dim, const int64_t n[3], int64_t batch, int isign,
+                void *data, mn_stream_t stream);
+/* Destroy all cached FFT plans (call with no transform in flight). */
+int mn_fft_cache_clear(void);
+
+/* Zero `bytes` bytes of device memory with a fill kernel (no memset node). */
+int mn_fill_zero(void *ptr, int64_t bytes, mn_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLX_NUFFT_AMD_H */

@@ -1,0 +1,197 @@
+"""Thin wrappers over the C-ABI used by the plan classes: point setup, the
+stable bin sort, subproblem tables, spread/interp, deconvolution, FFT and
+expi. Every function takes and returns torch device tensors and runs on the
+current stream; shapes are validated by the C side as well.
+
+Bin geometry (the tile a workgroup owns) is chosen here, per dim and kernel
+width, from the LDS budget of one CDNA4 workgroup.
+"""
+
+import contextlib
+import ctypes
+import os
+
+import numpy as np
+import torch
+
+from . import _lib as L
+
+MSUB = 1024                 # max points per spread/interp subproblem
+TILE_BUDGET = 80 * 1024     # LDS bytes for one padded tile (2 workgroups/CU)
+
+
+def bin_sizes(dim, w, n_up):
+    """Bin size m per dim: the padded tile (m + w - 1 cells per dim,
+    complex64) must fit TILE_BUDGET bytes of LDS. Overridable with the
+    environment variable MN_BIN_M="m0,m1,m2" (tuning)."""
+    env = os.environ.get("MN_BIN_M")
+    if env:
+        m = [int(v) for v in env.split(",")]
+        m = (m + [m[-1]] * 3)[:dim]
+    elif dim == 1:
+        m = [1024]
+    elif dim == 2:
+        m = [32, 32]
+    else:
+        side = int(round((TILE_BUDGET / 8) ** (1.0 / 3.0) - 1e-9))
+        while 8 * side ** 3 > TILE_BUDGET:
+            side -= 1
+        m = [max(1, side - w + 1)] * 3
+    m = [max(1, min(int(mi), int(n))) for mi, n in zip(m, n_up)]
+    while 8 * int(np.prod([mi + w - 1 for mi in m])) > TILE_BUDGET and max(m) > 1:
+        k = int(np.argmax(m))
+        m[k] -= 1
+    return m
+
+
+def make_bins(dim, w, n_up, m=None):
+    return L.Bins.make(dim, w, list(n_up), m if m is not None else bin_sizes(dim, w, n_up))
+
+
+def key_bits(bins):
+    return max(1, int(bins.nbins - 1).bit_length())
+
+
+def _rows(t, dim):
+    return [t[d] for d in range(dim)]
+
+
+def setpts_t12(bins, xs, prec64):
+    """Cells, fractions and bin keys of type-1/2 points (caller order)."""
+    dim, P = bins.dim, xs[0].numel()
+    dev = xs[0].device
+    i1 = torch.empty((dim, P), dtype=torch.int32, device=dev)
+    fr = torch.empty((dim, P), dtype=torch.float32, device=dev)
+    key = torch.empty(P, dtype=torch.int32, device=dev)
+    L.check(L.lib().mn_setpts_t12(ctypes.byref(bins), P, L.ptr3(xs), int(bool(prec64)),
+                                  L.ptr3(_rows(i1, dim)), L.ptr3(_rows(fr, dim)), L.ptr(key),
+                                  L.stream()), "setpts")
+    return i1, fr, key
+
+
+def sort_keys(key, nbits):
+    """Stable argsort of uint32 keys (stored in int32 tensors): (sorted, perm)."""
+    P = key.numel()
+    lib = L.lib()
+    ws = torch.empty(int(lib.mn_sort_workspace_bytes(P)), dtype=torch.uint8, device=key.device)
+    skey = torch.empty_like(key)
+    perm = torch.empty_like(key)
+    L.check(lib.mn_sort_keys(P, int(nbits), L.ptr(key), L.ptr(skey), L.ptr(perm), L.ptr(ws),
+                             ws.numel(), L.stream()), "sort")
+    return skey, perm
+
+
+def gather_points(perm, i1, fr, extra=None):
+    dim, P = i1.shape
+    i1s = torch.empty_like(i1)
+    frs = torch.empty_like(fr)
+    ext = torch.empty_like(extra) if extra is not None else None
+    L.check(L.lib().mn_gather_points(dim, P, L.ptr(perm), L.ptr3(_rows(i1, dim)),
+                                     L.ptr3(_rows(fr, dim)), L.ptr3(_rows(i1s, dim)),
+                                     L.ptr3(_rows(frs, dim)), L.ptr(extra), L.ptr(ext),
+                                     L.stream()), "gather_points")
+    return i1s, frs, ext
+
+
+def build_subproblems(bins, skey, msub=MSUB):
+    """(info[nsub, 3] = (bin, start, count), nsub). Blocks on one 8-byte read."""
+    P = skey.numel()
+    lib = L.lib()
+    max_sub = bins.nbins + P // msub + 1
+    info = torch.empty((max_sub, 3), dtype=torch.int32, device=skey.device)
+    ws = torch.empty(int(lib.mn_subproblem_workspace_bytes(ctypes.byref(bins))),
+                     dtype=torch.uint8, device=skey.device)
+    nsub = ctypes.c_int64(0)
+    L.check(lib.mn_build_subproblems(ctypes.byref(bins), P, L.ptr(skey), int(msub), L.ptr(info),
+                                     max_sub, ctypes.byref(nsub), L.ptr(ws), ws.numel(),
+                                     L.stream()), "subproblems")
+    return info, int(nsub.value)
+
+
+class SortedPoints:
+    """Bin-sorted point state of one point set on one fine grid."""
+
+    def __init__(self, bins, i1, fr, key, extra=None, msub=MSUB):
+        self.bins = bins
+        self.P = i1.shape[1]
+        skey, self.perm = sort_keys(key, key_bits(bins))
+        self.i1s, self.frs, self.extra = gather_points(self.perm, i1, fr, extra)
+        self.info, self.nsub = build_subproblems(bins, skey, msub)
+        self.skey = skey
+
+    def i1_rows(self):
+        return _rows(self.i1s, self.bins.dim)
+
+    def fr_rows(self):
+        return _rows(self.frs, self.bins.dim)
+
+
+def spread(pts, beta, c, grid, pre=None):
+    L.check(L.lib().mn_spread(ctypes.byref(pts.bins), float(beta), pts.P, pts.nsub,
+                              L.ptr(pts.info), L.ptr(pts.perm), L.ptr3(pts.i1_rows()),
+                              L.ptr3(pts.fr_rows()), L.ptr(c), L.ptr(pre), L.ptr(grid),
+                              L.stream()), "spread")
+
+
+def spread_batch(pts, beta, cs, grids):
+    L.check(L.lib().mn_spread_batch(ctypes.byref(pts.bins), float(beta), pts.P, pts.nsub,
+                                    L.ptr(pts.info), L.ptr(pts.perm), L.ptr3(pts.i1_rows()),
+                                    L.ptr3(pts.fr_rows()), int(cs.shape[0]), L.ptr(cs),
+                                    L.ptr(grids), L.stream()), "spread_batch")
+
+
+def interp(pts, beta, grid, out, post=None):
+    L.check(L.lib().mn_interp(ctypes.byref(pts.bins), float(beta), pts.P, pts.nsub,
+                              L.ptr(pts.info), L.ptr(pts.perm), L.ptr3(pts.i1_rows()),
+                              L.ptr3(pts.fr_rows()), L.ptr(grid), L.ptr(post), L.ptr(out),
+                              L.stream()), "interp")
+
+
+def crop_deconv(n_up, N, grid, decs, fk, batch=1):
+    dim = len(N)
+    L.check(L.lib().mn_crop_deconv(dim, L.i64x3(n_up), L.i64x3(N), int(batch), L.ptr(grid),
+                                   L.ptr3(decs), L.ptr(fk), L.stream()), "crop_deconv")
+
+
+def pad_deconv(n_up, N, fk, decs, grid, batch=1):
+    dim = len(N)
+    L.check(L.lib().mn_pad_deconv(dim, L.i64x3(n_up), L.i64x3(N), int(batch), L.ptr(fk),
+                                  L.ptr3(decs), L.ptr(grid), L.stream()), "pad_deconv")
+
+
+def fft(grid, n_up, isign, batch=1):
+    L.check(L.lib().mn_fft_exec(len(n_up), L.i64x3(n_up), int(batch), int(isign), L.ptr(grid),
+                                L.stream()), "fft")
+
+
+def expi(comps, isign, out):
+    arr = (ctypes.c_void_p * len(comps))(*[c.data_ptr() for c in comps])
+    L.check(L.lib().mn_expi(len(comps), arr, comps[0].numel(), int(isign), L.ptr(out),
+                            L.stream()), "expi")
+
+
+class StageTimer:
+    """Optional per-stage HIP-event timing on the current stream."""
+
+    def __init__(self, enabled):
+        self.enabled = enabled
+        self.events = []
+
+    @contextlib.contextmanager
+    def __call__(self, name):
+        if not self.enabled:
+            yield
+            return
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        yield
+        b.record()
+        self.events.append((name, a, b))
+
+    def times_ms(self):
+        torch.cuda.synchronize()
+        out = {}
+        for name, a, b in self.events:
+            out[name] = out.get(name, 0.0) + a.elapsed_time(b)
+        return out

@@ -1,0 +1,168 @@
+// Shared helpers of the HIP sources: error state, argument checks, the ES
+// kernel, periodic wrap, and the XCD-aware workgroup remap.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/mlx_nufft_amd.h"
+
+namespace mn {
+
+// ---- error state (one message per host thread) ---------------------------
+void set_error(const std::string &msg);
+void clear_error();
+
+#define MN_REQUIRE(cond, msg)                 \
+    do {                                      \
+        if (!(cond)) {                        \
+            ::mn::set_error(msg);             \
+            return MN_EINVAL;                 \
+        }                                     \
+    } while (0)
+
+#define MN_HIP_CHECK(expr)                                                    \
+    do {                                                                      \
+        hipError_t _e = (expr);                                               \
+        if (_e != hipSuccess) {                                               \
+            ::mn::set_error(std::string(#expr) + ": " + hipGetErrorString(_e)); \
+            return MN_ERUNTIME;                                               \
+        }                                                                     \
+    } while (0)
+
+// Check a kernel launch (launch-configuration errors surface here).
+#define MN_LAUNCH_CHECK(what)                                                   \
+    do {                                                                        \
+        hipError_t _e = hipGetLastError();                                      \
+        if (_e != hipSuccess) {                                                 \
+            ::mn::set_error(std::string(what) + " launch: " + hipGetErrorString(_e)); \
+            return MN_ERUNTIME;                                                 \
+        }                                                                       \
+    } while (0)
+
+inline hipStream_t as_stream(mn_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Validate a bin geometry; returns MN_OK or sets the error and MN_EINVAL.
+int check_bins(const mn_bins *g);
+
+inline int64_t nbins_total(const mn_bins *g) {
+    int64_t t = 1;
+    for (int d = 0; d < g->dim; ++d) t *= g->nb[d];
+    return t;
+}
+
+inline int64_t tile_cells(const mn_bins *g) {
+    int64_t t = 1;
+    for (int d = 0; d < g->dim; ++d) t *= (int64_t)g->m[d] + g->w - 1;
+    return t;
+}
+
+// LDS bytes available to one workgroup on the current device.
+int max_lds_per_block();
+
+// Zero device memory with a fill kernel (usable under graph capture).
+int fill_zero(void *ptr, int64_t bytes, hipStream_t s);
+
+// Exclusive prefix sum of n uint32 values in place; `partials` must hold
+// scan_partials_elems(n) uint32 of scratch. Returns MN_OK or an error.
+int64_t scan_partials_elems(int64_t n);
+int scan_exclusive_u32(uint32_t *data, int64_t n, uint32_t *partials, hipStream_t s);
+
+constexpr int kMaxW = 16;
+constexpr double kTwoPi = 6.283185307179586;  // fl64(2*pi)
+
+// Kernel geometry passed by value to the device.
+struct Geom {
+    int dim;
+    int w;
+    int n[3];   // grid size per dim (1 for unused dims)
+    int m[3];   // bin size
+    int nb[3];  // bins per dim
+    int p[3];   // padded tile size m + w - 1 (1 for unused dims)
+};
+
+inline Geom make_geom(const mn_bins *g) {
+    Geom k;
+    k.dim = g->dim;
+    k.w = g->w;
+    for (int d = 0; d < 3; ++d) {
+        bool used = d < g->dim;
+        k.n[d] = used ? (int)g->n[d] : 1;
+        k.m[d] = used ? g->m[d] : 1;
+        k.nb[d] = used ? g->nb[d] : 1;
+        k.p[d] = used ? g->m[d] + g->w - 1 : 1;
+    }
+    return k;
+}
+
+// ---- device helpers -------------------------------------------------------
+
+// ES kernel psi(d) = exp(beta*(sqrt(1 - (2d/w)^2) - 1)) on |d| <= w/2.
+// Written as 2^(beta*log2(e)*(sqrt(t)-1)) so it maps onto one v_exp_f32;
+// bl2e = beta*log2(e), inv_hw = 2/w. The argument of exp2 is <= 0, so the
+// relative error of the product feeds only the (tiny) tail weights.
+__device__ __forceinline__ float es_weight(float d, float bl2e, float inv_hw) {
+    float z = d * inv_hw;
+    float t = fmaxf(1.0f - z * z, 0.0f);
+    return exp2f(bl2e * (__builtin_sqrtf(t) - 1.0f));
+}
+
+// Map a cell index that is at most one period outside [0, n) back into it.
+__device__ __forceinline__ int wrap1(int i, int n) {
+    i += (i < 0) ? n : 0;
+    i -= (i >= n) ? n : 0;
+    return i;
+}
+
+// True modulo into [0, n) for any int.
+__device__ __forceinline__ int pmod(int i, int n) {
+    int r = i % n;
+    return r < 0 ? r + n : r;
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs (blockIdx % 8).
+// Remap so that XCD k receives one contiguous run of work items, which keeps
+// neighbouring bins (and the grid lines their tiles share) in one L2.
+__device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t nblk) {
+    constexpr int64_t NX = 8;
+    if (nblk < NX) return bid;
+    int64_t q = nblk / NX, r = nblk % NX;
+    int64_t x = bid % NX, slot = bid / NX;
+    return x * q + (x < r ? x : r) + slot;
+}
+
+// Sorted per-point arrays, by value into kernels.
+struct CI3s { const int32_t *p[3]; };
+struct CF3s { const float *p[3]; };
+
+// Validate the point/subproblem arguments shared by spread and interp.
+int check_points(const mn_bins *g, int64_t P, int64_t nsub, const int32_t *info,
+                 const uint32_t *perm, const int32_t *const i1s[3], const float *const frs[3],
+                 CI3s *ci, CF3s *cf);
+
+// Pick the (DIM, W) instantiation of a launcher template at run time.
+template <template <int, int> class L, typename A, int DIM, int W>
+int select_w(int w, const A &a) {
+    if constexpr (W > kMaxW) {
+        set_error("kernel width out of range");
+        return MN_EINVAL;
+    } else {
+        if (w == W) return L<DIM, W>::run(a);
+        return select_w<L, A, DIM, W + 1>(w, a);
+    }
+}
+
+template <template <int, int> class L, typename A>
+int select_dim_w(int dim, int w, const A &a) {
+    switch (dim) {
+        case 1: return select_w<L, A, 1, 2>(w, a);
+        case 2: return select_w<L, A, 2, 2>(w, a);
+        case 3: return select_w<L, A, 3, 2>(w, a);
+    }
+    set_error("dim must be 1, 2 or 3");
+    return MN_EINVAL;
+}
+
+}  // namespace mn

@@ -1,0 +1,207 @@
+// Interpolation (type-2 core, and the type-3 target gather) on LDS tiles.
+//
+// One 256-thread workgroup per subproblem loads the bin's padded tile of the
+// fine grid (m + w - 1 cells per dim, periodic wrap) into LDS once, with
+// rows along the contiguous last dim; then each lane gathers whole points
+// from LDS: w^dim complex taps per point, summed along the last dim first
+// and weighted by the product of the other dims' ES weights. The result is
+// scattered to caller order (out[perm[j]]), optionally times a sorted-order
+// multiplier (the type-3 post factor).
+// ref: nd.py:974-1073 (OD gather), nd.py:908-972 (GM gather),
+// gpu_t3.py:653-693 (type-3 gather x post).
+#include "mn_common.h"
+
+namespace mn {
+namespace {
+
+struct InterpArgs {
+    const mn_bins *g;
+    float beta;
+    int64_t nsub;
+    const int32_t *info;
+    const uint32_t *perm;
+    CI3s i1s;
+    CF3s frs;
+    const float2 *grid;
+    const float2 *post;
+    float2 *out;
+    hipStream_t s;
+};
+
+__device__ __forceinline__ int wrap_tile_i(int v, int n) {
+    v = wrap1(v, n);
+    if (v >= n) v -= n;
+    return v;
+}
+
+template <int DIM, int W>
+__global__ __launch_bounds__(256) void k_interp_tiled(Geom g, float bl2e, float inv_hw,
+                                                      int64_t nsub, const int32_t *__restrict__ info,
+                                                      const uint32_t *__restrict__ perm, CI3s i1s,
+                                                      CF3s frs, const float2 *__restrict__ grid,
+                                                      const float2 *__restrict__ post,
+                                                      float2 *__restrict__ out) {
+    extern __shared__ float2 tile[];
+    const int p1 = g.p[1], p2 = g.p[2];
+    const int T = g.p[0] * p1 * p2;
+    const int64_t sub = xcd_remap(blockIdx.x, nsub);
+    const int bin = info[3 * sub], s0 = info[3 * sub + 1], cnt = info[3 * sub + 2];
+    int b[3] = {0, 0, 0};
+    {
+        int rem = bin;
+#pragma unroll
+        for (int d = DIM - 1; d >= 0; --d) {
+            b[d] = rem % g.nb[d];
+            rem /= g.nb[d];
+        }
+    }
+    const int o0 = b[0] * g.m[0] - W / 2;
+    const int o1 = DIM >= 2 ? b[1] * g.m[1] - W / 2 : 0;
+    const int o2 = DIM >= 3 ? b[2] * g.m[2] - W / 2 : 0;
+    for (int q = threadIdx.x; q < T; q += 256) {
+        const int q2 = q % p2, r12 = q / p2;
+        const int q1 = r12 % p1, q0 = r12 / p1;
+        const int g0 = wrap_tile_i(o0 + q0, g.n[0]);
+        const int g1 = DIM >= 2 ? wrap_tile_i(o1 + q1, g.n[1]) : 0;
+        const int g2 = DIM >= 3 ? wrap_tile_i(o2 + q2, g.n[2]) : 0;
+        tile[q] = grid[((int64_t)g0 * g.n[1] + g1) * g.n[2] + g2];
+    }
+    __syncthreads();
+
+    for (int t = threadIdx.x; t < cnt; t += 256) {
+        const int64_t j = (int64_t)s0 + t;
+        float wt[DIM][W];
+        int loc[3] = {0, 0, 0};
+        bool ok = true;
+#pragma unroll
+        for (int d = 0; d < DIM; ++d) {
+            int v = wrap1(i1s.p[d][j] + W / 2, g.n[d]);
+            if ((unsigned)v >= (unsigned)g.n[d]) v = pmod(v, g.n[d]);
+            loc[d] = v - b[d] * g.m[d];
+            ok = ok && (unsigned)loc[d] < (unsigned)g.m[d];
+            const float f = frs.p[d][j];
+#pragma unroll
+            for (int a = 0; a < W; ++a) wt[d][a] = es_weight((float)a - f, bl2e, inv_hw);
+        }
+        float ar = 0.0f, ai = 0.0f;
+        if (ok) {
+            if constexpr (DIM == 1) {
+#pragma unroll
+                for (int a0 = 0; a0 < W; ++a0) {
+                    const float2 v = tile[loc[0] + a0];
+                    ar = fmaf(v.x, wt[0][a0], ar);
+                    ai = fmaf(v.y, wt[0][a0], ai);
+                }
+            } else if constexpr (DIM == 2) {
+#pragma unroll
+                for (int a0 = 0; a0 < W; ++a0) {
+                    const int base = (loc[0] + a0) * p1 + loc[1];
+                    float sr = 0.0f, si = 0.0f;
+#pragma unroll
+                    for (int a1 = 0; a1 < W; ++a1) {
+                        const float2 v = tile[base + a1];
+                        sr = fmaf(v.x, wt[1][a1], sr);
+                        si = fmaf(v.y, wt[1][a1], si);
+                    }
+                    ar = fmaf(sr, wt[0][a0], ar);
+                    ai = fmaf(si, wt[0][a0], ai);
+                }
+            } else {
+#pragma unroll
+                for (int a0 = 0; a0 < W; ++a0) {
+#pragma unroll
+                    for (int a1 = 0; a1 < W; ++a1) {
+                        const int base = ((loc[0] + a0) * p1 + loc[1] + a1) * p2 + loc[2];
+                        float sr = 0.0f, si = 0.0f;
+#pragma unroll
+                        for (int a2 = 0; a2 < W; ++a2) {
+                            const float2 v = tile[base + a2];
+                            sr = fmaf(v.x, wt[2][a2], sr);
+                            si = fmaf(v.y, wt[2][a2], si);
+                        }
+                        const float w01 = wt[0][a0] * wt[1][a1];
+                        ar = fmaf(sr, w01, ar);
+                        ai = fmaf(si, w01, ai);
+                    }
+                }
+            }
+        }
+        float2 r = make_float2(ar, ai);
+        if (post) {
+            const float2 pv = post[j];
+            r = make_float2(ar * pv.x - ai * pv.y, ar * pv.y + ai * pv.x);
+        }
+        out[perm[j]] = r;
+    }
+}
+
+template <int DIM, int W>
+struct InterpLaunch {
+    static int run(const InterpArgs &a) {
+        Geom g = make_geom(a.g);
+        const float bl2e = (float)(a.beta * 1.4426950408889634);
+        const float inv_hw = (float)(2.0 / W);
+        const size_t lds = (size_t)tile_cells(a.g) * sizeof(float2);
+        if (lds > (size_t)max_lds_per_block()) {
+            set_error("interp: tile does not fit in LDS; use smaller bins");
+            return MN_EINVAL;
+        }
+        if (a.nsub == 0) return MN_OK;
+        auto kern = k_interp_tiled<DIM, W>;
+        if (lds > 65536)
+            MN_HIP_CHECK(hipFuncSetAttribute((const void *)kern,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        kern<<<(unsigned)a.nsub, 256, lds, a.s>>>(g, bl2e, inv_hw, a.nsub, a.info, a.perm, a.i1s,
+                                                  a.frs, a.grid, a.post, a.out);
+        MN_LAUNCH_CHECK("interp");
+        return MN_OK;
+    }
+};
+
+}  // namespace
+
+int check_points(const mn_bins *g, int64_t P, int64_t nsub, const int32_t *info,
+                 const uint32_t *perm, const int32_t *const i1s[3], const float *const frs[3],
+                 CI3s *ci, CF3s *cf) {
+    MN_REQUIRE(P >= 1 && P < (int64_t(1) << 31), "P must be in [1, 2^31)");
+    MN_REQUIRE(nsub >= 0 && nsub < (int64_t(1) << 31), "nsub out of range");
+    MN_REQUIRE(nsub == 0 || (info && perm), "NULL subproblem table or permutation");
+    *ci = CI3s{};
+    *cf = CF3s{};
+    for (int d = 0; d < g->dim; ++d) {
+        MN_REQUIRE(i1s[d] && frs[d], "NULL sorted cell/fraction pointer");
+        ci->p[d] = i1s[d];
+        cf->p[d] = frs[d];
+    }
+    return MN_OK;
+}
+
+}  // namespace mn
+
+using namespace mn;
+
+extern "C" {
+
+int mn_interp(const mn_bins *g, float beta, int64_t P, int64_t nsub, const int32_t *sub_info,
+              const uint32_t *perm, const int32_t *const i1s[3], const float *const frs[3],
+              const void *grid, const void *post, void *out, mn_stream_t stream) {
+    clear_error();
+    int rc = check_bins(g);
+    if (rc) return rc;
+    InterpArgs a{};
+    rc = check_points(g, P, nsub, sub_info, perm, i1s, frs, &a.i1s, &a.frs);
+    if (rc) return rc;
+    MN_REQUIRE(grid && out, "interp: NULL grid or output");
+    a.g = g;
+    a.beta = beta;
+    a.nsub = nsub;
+    a.info = sub_info;
+    a.perm = perm;
+    a.grid = static_cast<const float2 *>(grid);
+    a.post = static_cast<const float2 *>(post);
+    a.out = static_cast<float2 *>(out);
+    a.s = as_stream(stream);
+    return select_dim_w<InterpLaunch>(g->dim, g->w, a);
+}
+
+}  // extern "C"

@@ -1,0 +1,360 @@
+// Stable bin sort and subproblem tables.
+//
+// The bin sort is an LSD radix sort over 8-bit digits of the bin key. Each
+// pass is (1) a per-tile digit histogram, (2) an exclusive scan of the
+// digit-major histogram matrix, (3) a stable scatter in which every tile
+// ranks its elements in index order with wave ballots (64-lane match on the
+// 8 digit bits) and LDS counters. LSD radix passes are stable, so the final
+// permutation equals numpy's argsort(key, kind="stable")
+// (ref: nd.py:314, nd.py:175, gpu_t3.py:490-492).
+//
+// The subproblem table replaces the reference's host-side construction
+// (ref: nd.py:347-372) with three device kernels and one 8-byte read-back.
+#include "mn_common.h"
+
+namespace mn {
+namespace {
+
+constexpr int RS_THREADS = 256;
+constexpr int RS_ITEMS = 16;
+constexpr int RS_TILE = RS_THREADS * RS_ITEMS;  // 4096 elements per tile
+constexpr int RS_RADIX = 256;
+
+constexpr int SC_THREADS = 256;
+constexpr int SC_ITEMS = 8;
+constexpr int SC_TILE = SC_THREADS * SC_ITEMS;  // 2048 elements per scan tile
+
+// ---------------------------------------------------------------- scan ----
+
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        uint32_t t = __shfl_up(v, o, 64);
+        if (lane >= o) v += t;
+    }
+    return v;
+}
+
+// Exclusive scan of the thread totals of one 256-thread block; returns the
+// exclusive prefix of this thread and writes the block total to *total.
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t *total) {
+    __shared__ uint32_t wsum[SC_THREADS / 64];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    uint32_t inc = wave_incl_scan(v);
+    if (lane == 63) wsum[wv] = inc;
+    __syncthreads();
+    uint32_t off = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < SC_THREADS / 64; ++w) {
+        uint32_t s = wsum[w];
+        if (w < wv) off += s;
+        tot += s;
+    }
+    __syncthreads();
+    *total = tot;
+    return off + inc - v;
+}
+
+__global__ void k_tile_reduce(const uint32_t *__restrict__ d, int64_t n,
+                              uint32_t *__restrict__ partials) {
+    int64_t base = (int64_t)blockIdx.x * SC_TILE + (int64_t)threadIdx.x * SC_ITEMS;
+    uint32_t s = 0;
+#pragma unroll
+    for (int i = 0; i < SC_ITEMS; ++i)
+        if (base + i < n) s += d[base + i];
+    uint32_t tot;
+    block_excl_scan(s, &tot);
+    if (threadIdx.x == 0) partials[blockIdx.x] = tot;
+}
+
+// Exclusive scan of one tile in place, offset by partials[blockIdx.x] when
+// partials is non-NULL.
+__global__ void k_tile_scan(uint32_t *__restrict__ d, int64_t n,
+                            const uint32_t *__restrict__ partials) {
+    int64_t base = (int64_t)blockIdx.x * SC_TILE + (int64_t)threadIdx.x * SC_ITEMS;
+    uint32_t v[SC_ITEMS];
+    uint32_t s = 0;
+#pragma unroll
+    for (int i = 0; i < SC_ITEMS; ++i) {
+        v[i] = (base + i < n) ? d[base + i] : 0u;
+        s += v[i];
+    }
+    uint32_t tot;
+    uint32_t run = block_excl_scan(s, &tot);
+    if (partials) run += partials[blockIdx.x];
+#pragma unroll
+    for (int i = 0; i < SC_ITEMS; ++i) {
+        if (base + i < n) d[base + i] = run;
+        run += v[i];
+    }
+}
+
+// ---------------------------------------------------------- radix sort ----
+
+__global__ __launch_bounds__(RS_THREADS) void k_radix_hist(const uint32_t *__restrict__ keys,
+                                                           int64_t P, int shift,
+                                                           uint32_t *__restrict__ hist,
+                                                           int64_t nblk) {
+    __shared__ uint32_t h[RS_RADIX];
+    h[threadIdx.x] = 0;
+    __syncthreads();
+    int64_t base = (int64_t)blockIdx.x * RS_TILE;
+#pragma unroll 4
+    for (int i = 0; i < RS_ITEMS; ++i) {
+        int64_t idx = base + (int64_t)i * RS_THREADS + threadIdx.x;
+        if (idx < P) atomicAdd(&h[(keys[idx] >> shift) & (RS_RADIX - 1)], 1u);
+    }
+    __syncthreads();
+    hist[(int64_t)threadIdx.x * nblk + blockIdx.x] = h[threadIdx.x];
+}
+
+// Stable scatter of one tile. Elements are visited in index order: 16 rounds
+// of 256 consecutive elements; inside a round, wave w holds elements
+// [64w, 64w+64) and ranks lanes with equal digits by a ballot match.
+__global__ __launch_bounds__(RS_THREADS) void k_radix_scatter(
+    const uint32_t *__restrict__ kin, const uint32_t *__restrict__ vin, int64_t P, int shift,
+    const uint32_t *__restrict__ offs, int64_t nblk, uint32_t *__restrict__ kout,
+    uint32_t *__restrict__ vout) {
+    __shared__ uint32_t run[RS_RADIX];
+    __shared__ uint32_t base_off[RS_RADIX];
+    __shared__ uint32_t wcnt[RS_THREADS / 64][RS_RADIX];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    run[tid] = 0;
+    base_off[tid] = offs[(int64_t)tid * nblk + blockIdx.x];
+#pragma unroll
+    for (int w = 0; w < RS_THREADS / 64; ++w) wcnt[w][tid] = 0;
+    __syncthreads();
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int64_t base = (int64_t)blockIdx.x * RS_TILE;
+    for (int r = 0; r < RS_ITEMS; ++r) {
+        int64_t idx = base + (int64_t)r * RS_THREADS + tid;
+        bool valid = idx < P;
+        uint32_t k = valid ? kin[idx] : 0u;
+        uint32_t v = valid ? (vin ? vin[idx] : (uint32_t)idx) : 0u;
+        uint32_t dg = (k >> shift) & (RS_RADIX - 1);
+        uint64_t peers = __ballot(valid);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            bool bit = (dg >> b) & 1u;
+            uint64_t bal = __ballot(bit);
+            peers &= bit ? bal : ~bal;
+        }
+        uint32_t rank = (uint32_t)__popcll(peers & lt_mask);
+        if (valid && rank == 0) wcnt[wv][dg] = (uint32_t)__popcll(peers);
+        __syncthreads();
+        if (valid) {
+            uint32_t pre = run[dg];
+            for (int w = 0; w < wv; ++w) pre += wcnt[w][dg];
+            uint32_t pos = base_off[dg] + pre + rank;
+            kout[pos] = k;
+            vout[pos] = v;
+        }
+        __syncthreads();
+        uint32_t add = 0;
+#pragma unroll
+        for (int w = 0; w < RS_THREADS / 64; ++w) {
+            add += wcnt[w][tid];
+            wcnt[w][tid] = 0;
+        }
+        run[tid] += add;
+        __syncthreads();
+    }
+}
+
+// --------------------------------------------------------- subproblems ----
+
+__global__ void k_bin_bounds(const uint32_t *__restrict__ skey, int64_t P, int64_t nbins,
+                             int32_t *__restrict__ bstart, int32_t *__restrict__ bend) {
+    int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= P) return;
+    uint32_t k = skey[j];
+    if ((int64_t)k >= nbins) return;  // keys come from setpts and are < nbins
+    if (j == 0 || skey[j - 1] != k) bstart[k] = (int32_t)j;
+    if (j == P - 1 || skey[j + 1] != k) bend[k] = (int32_t)(j + 1);
+}
+
+__global__ void k_bin_nsub(const int32_t *__restrict__ bstart, const int32_t *__restrict__ bend,
+                           int64_t nbins, int32_t msub, uint32_t *__restrict__ nsub) {
+    int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b > nbins) return;
+    if (b == nbins) {
+        nsub[b] = 0;
+        return;
+    }
+    int32_t c = bend[b] - bstart[b];
+    nsub[b] = (uint32_t)((c + msub - 1) / msub);
+}
+
+__global__ void k_sub_fill(const int32_t *__restrict__ bstart, const int32_t *__restrict__ bend,
+                           const uint32_t *__restrict__ soff, int64_t nbins, int32_t msub,
+                           int32_t *__restrict__ info) {
+    int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nbins) return;
+    int32_t s0 = bstart[b], c = bend[b] - s0;
+    uint32_t row = soff[b];
+    for (int32_t o = 0; o < c; o += msub, ++row) {
+        info[3 * (int64_t)row + 0] = (int32_t)b;
+        info[3 * (int64_t)row + 1] = s0 + o;
+        info[3 * (int64_t)row + 2] = (c - o < msub) ? (c - o) : msub;
+    }
+}
+
+inline unsigned blocks_for(int64_t n, int t) { return (unsigned)((n + t - 1) / t); }
+
+inline int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace
+
+int64_t scan_partials_elems(int64_t n) {
+    int64_t tot = 0;
+    while (n > SC_TILE) {
+        n = (n + SC_TILE - 1) / SC_TILE;
+        tot += n;
+    }
+    return tot + 1;
+}
+
+int scan_exclusive_u32(uint32_t *data, int64_t n, uint32_t *partials, hipStream_t s) {
+    if (n <= 0) return MN_OK;
+    if (n <= SC_TILE) {
+        k_tile_scan<<<1, SC_THREADS, 0, s>>>(data, n, nullptr);
+        MN_LAUNCH_CHECK("scan");
+        return MN_OK;
+    }
+    int64_t nt = (n + SC_TILE - 1) / SC_TILE;
+    k_tile_reduce<<<(unsigned)nt, SC_THREADS, 0, s>>>(data, n, partials);
+    MN_LAUNCH_CHECK("scan reduce");
+    int rc = scan_exclusive_u32(partials, nt, partials + nt, s);
+    if (rc) return rc;
+    k_tile_scan<<<(unsigned)nt, SC_THREADS, 0, s>>>(data, n, partials);
+    MN_LAUNCH_CHECK("scan");
+    return MN_OK;
+}
+
+}  // namespace mn
+
+using namespace mn;
+
+namespace {
+
+struct SortWs {
+    uint32_t *kalt, *valt, *hist, *partials;
+    int64_t bytes;
+};
+
+SortWs sort_layout(int64_t P, char *base) {
+    int64_t nblk = (P + RS_TILE - 1) / RS_TILE;
+    int64_t nh = nblk * RS_RADIX;
+    SortWs w{};
+    int64_t off = 0;
+    w.kalt = reinterpret_cast<uint32_t *>(base + off);
+    off = align_up(off + 4 * P, 256);
+    w.valt = reinterpret_cast<uint32_t *>(base + off);
+    off = align_up(off + 4 * P, 256);
+    w.hist = reinterpret_cast<uint32_t *>(base + off);
+    off = align_up(off + 4 * nh, 256);
+    w.partials = reinterpret_cast<uint32_t *>(base + off);
+    off = align_up(off + 4 * scan_partials_elems(nh), 256);
+    w.bytes = off;
+    return w;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t mn_sort_workspace_bytes(int64_t P) {
+    if (P < 1) P = 1;
+    return sort_layout(P, nullptr).bytes;
+}
+
+int mn_sort_keys(int64_t P, int key_bits, const uint32_t *key_in, uint32_t *key_out,
+                 uint32_t *perm_out, void *ws, int64_t ws_bytes, mn_stream_t stream) {
+    clear_error();
+    MN_REQUIRE(P >= 1 && P < (int64_t(1) << 32), "sort: P must be in [1, 2^32)");
+    MN_REQUIRE(key_bits >= 0 && key_bits <= 32, "sort: key_bits must be in [0, 32]");
+    MN_REQUIRE(key_in && key_out && perm_out && ws, "sort: NULL pointer");
+    MN_REQUIRE(key_in != key_out, "sort: key_in and key_out must differ");
+    SortWs w = sort_layout(P, static_cast<char *>(ws));
+    MN_REQUIRE(ws_bytes >= w.bytes, "sort: workspace too small");
+    hipStream_t s = as_stream(stream);
+    int npass = key_bits <= 0 ? 1 : (key_bits + 7) / 8;
+    int64_t nblk = (P + RS_TILE - 1) / RS_TILE;
+    const uint32_t *ksrc = key_in;
+    const uint32_t *vsrc = nullptr;  // identity values on the first pass
+    for (int p = 0; p < npass; ++p) {
+        bool to_out = ((npass - 1 - p) % 2) == 0;
+        uint32_t *kdst = to_out ? key_out : w.kalt;
+        uint32_t *vdst = to_out ? perm_out : w.valt;
+        int shift = 8 * p;
+        k_radix_hist<<<(unsigned)nblk, RS_THREADS, 0, s>>>(ksrc, P, shift, w.hist, nblk);
+        MN_LAUNCH_CHECK("radix hist");
+        int rc = scan_exclusive_u32(w.hist, nblk * RS_RADIX, w.partials, s);
+        if (rc) return rc;
+        k_radix_scatter<<<(unsigned)nblk, RS_THREADS, 0, s>>>(ksrc, vsrc, P, shift, w.hist, nblk,
+                                                             kdst, vdst);
+        MN_LAUNCH_CHECK("radix scatter");
+        ksrc = kdst;
+        vsrc = vdst;
+    }
+    return MN_OK;
+}
+
+int64_t mn_subproblem_workspace_bytes(const mn_bins *g) {
+    if (check_bins(g)) return -1;
+    int64_t nb = nbins_total(g);
+    int64_t off = 0;
+    off = align_up(off + 4 * nb, 256);        // bin start
+    off = align_up(off + 4 * nb, 256);        // bin end
+    off = align_up(off + 4 * (nb + 1), 256);  // subproblem offsets
+    off = align_up(off + 4 * scan_partials_elems(nb + 1), 256);
+    return off;
+}
+
+int mn_build_subproblems(const mn_bins *g, int64_t P, const uint32_t *sorted_key, int32_t msub,
+                         int32_t *sub_info, int64_t max_sub, int64_t *nsub_out, void *ws,
+                         int64_t ws_bytes, mn_stream_t stream) {
+    clear_error();
+    int rc = check_bins(g);
+    if (rc) return rc;
+    MN_REQUIRE(P >= 1 && P < (int64_t(1) << 31), "subproblems: P must be in [1, 2^31)");
+    MN_REQUIRE(msub >= 1, "subproblems: msub must be >= 1");
+    MN_REQUIRE(sorted_key && sub_info && nsub_out && ws, "subproblems: NULL pointer");
+    int64_t need = mn_subproblem_workspace_bytes(g);
+    MN_REQUIRE(ws_bytes >= need, "subproblems: workspace too small");
+    int64_t nb = nbins_total(g);
+    char *base = static_cast<char *>(ws);
+    int64_t off = 0;
+    int32_t *bstart = reinterpret_cast<int32_t *>(base + off);
+    off = align_up(off + 4 * nb, 256);
+    int32_t *bend = reinterpret_cast<int32_t *>(base + off);
+    off = align_up(off + 4 * nb, 256);
+    uint32_t *soff = reinterpret_cast<uint32_t *>(base + off);
+    off = align_up(off + 4 * (nb + 1), 256);
+    uint32_t *partials = reinterpret_cast<uint32_t *>(base + off);
+    hipStream_t s = as_stream(stream);
+    rc = fill_zero(bstart, 4 * nb, s);
+    if (rc) return rc;
+    rc = fill_zero(bend, 4 * nb, s);
+    if (rc) return rc;
+    k_bin_bounds<<<blocks_for(P, 256), 256, 0, s>>>(sorted_key, P, nb, bstart, bend);
+    MN_LAUNCH_CHECK("bin bounds");
+    k_bin_nsub<<<blocks_for(nb + 1, 256), 256, 0, s>>>(bstart, bend, nb, msub, soff);
+    MN_LAUNCH_CHECK("bin nsub");
+    rc = scan_exclusive_u32(soff, nb + 1, partials, s);
+    if (rc) return rc;
+    uint32_t total = 0;
+    MN_HIP_CHECK(hipMemcpyAsync(&total, soff + nb, 4, hipMemcpyDeviceToHost, s));
+    MN_HIP_CHECK(hipStreamSynchronize(s));
+    if ((int64_t)total > max_sub) {
+        set_error("subproblems: table capacity max_sub too small");
+        return MN_EINVAL;
+    }
+    k_sub_fill<<<blocks_for(nb, 256), 256, 0, s>>>(bstart, bend, soff, nb, msub, sub_info);
+    MN_LAUNCH_CHECK("subproblem fill");
+    *nsub_out = (int64_t)total;
+    return MN_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,259 @@
+// Spreading (type-1 core) on LDS-staged subproblem tiles.
+//
+// One 256-thread workgroup per subproblem (<= msub bin-sorted points of one
+// bin). The padded tile of the bin (m + w - 1 cells per dim) lives in LDS as
+// two fp32 planes (re, im). Each lane takes one point at a time: it gathers
+// the strength c[perm[j]] (caller order; optionally times the type-3
+// prephase), evaluates the w ES weights per dim once, and adds the w^dim
+// taps into LDS with ds_add_f32. After a barrier the tile is flushed to the
+// periodic fine grid with fp32 global atomics (skipping cells that stayed
+// zero). Workgroups are remapped so each XCD walks a contiguous run of bins.
+// ref: nd.py:492-579 (OD spread), nd.py:683-742 (batched), gpu_t3.py:565-591.
+#include "mn_common.h"
+
+namespace mn {
+
+namespace {
+
+struct SpreadArgs {
+    const mn_bins *g;
+    float beta;
+    int64_t P, nsub;
+    const int32_t *info;
+    const uint32_t *perm;
+    CI3s i1s;
+    CF3s frs;
+    const float2 *c;    // strengths (caller order); batched: B x P
+    const float2 *pre;  // optional sorted-order multiplier
+    float2 *grid;
+    int64_t b0;  // first vector of this launch (batched)
+    int bc;      // vectors in this launch
+    hipStream_t s;
+};
+
+__device__ __forceinline__ int wrap_tile(int v, int n) {
+    v = wrap1(v, n);
+    if (v >= n) v -= n;
+    return v;
+}
+
+// Cell coordinate of point j relative to its bin's tile (in [0, m)), or -1.
+__device__ __forceinline__ int local_cell(int i1, int hw, int n, int b, int m) {
+    int v = wrap1(i1 + hw, n);
+    if ((unsigned)v >= (unsigned)n) v = pmod(v, n);
+    int loc = v - b * m;
+    return ((unsigned)loc < (unsigned)m) ? loc : -1;
+}
+
+template <int DIM, int W, bool BATCH>
+__global__ __launch_bounds__(256) void k_spread_tiled(Geom g, float bl2e, float inv_hw,
+                                                      int64_t nsub, const int32_t *__restrict__ info,
+                                                      const uint32_t *__restrict__ perm, CI3s i1s,
+                                                      CF3s frs, const float2 *__restrict__ c,
+                                                      const float2 *__restrict__ pre,
+                                                      float2 *__restrict__ grid, int64_t P,
+                                                      int64_t b0, int bc) {
+    extern __shared__ float lds[];
+    const int p1 = g.p[1], p2 = g.p[2];
+    const int T = g.p[0] * p1 * p2;
+    const int64_t sub = xcd_remap(blockIdx.x, nsub);
+    const int bin = info[3 * sub], s0 = info[3 * sub + 1], cnt = info[3 * sub + 2];
+    int b[3] = {0, 0, 0};
+    {
+        int rem = bin;
+#pragma unroll
+        for (int d = DIM - 1; d >= 0; --d) {
+            b[d] = rem % g.nb[d];
+            rem /= g.nb[d];
+        }
+    }
+    const int nvec = BATCH ? bc : 1;
+    for (int q = threadIdx.x; q < 2 * T * nvec; q += 256) lds[q] = 0.0f;
+    __syncthreads();
+
+    for (int t = threadIdx.x; t < cnt; t += 256) {
+        const int64_t j = (int64_t)s0 + t;
+        const uint32_t src = perm[j];
+        float wt[DIM][W];
+        int loc[3] = {0, 0, 0};
+        bool ok = true;
+#pragma unroll
+        for (int d = 0; d < DIM; ++d) {
+            loc[d] = local_cell(i1s.p[d][j], W / 2, g.n[d], b[d], g.m[d]);
+            ok = ok && loc[d] >= 0;
+            const float f = frs.p[d][j];
+#pragma unroll
+            for (int a = 0; a < W; ++a) wt[d][a] = es_weight((float)a - f, bl2e, inv_hw);
+        }
+        if (!ok) continue;  // cannot happen for keys built by setpts
+        float2 pv = make_float2(1.0f, 0.0f);
+        if (!BATCH && pre) pv = pre[j];
+        for (int v = 0; v < nvec; ++v) {
+            float2 cv = BATCH ? c[(b0 + v) * P + src] : c[src];
+            if (!BATCH && pre)
+                cv = make_float2(cv.x * pv.x - cv.y * pv.y, cv.x * pv.y + cv.y * pv.x);
+            float *tre = lds + (size_t)2 * T * v;
+            float *tim = tre + T;
+            if constexpr (DIM == 1) {
+#pragma unroll
+                for (int a0 = 0; a0 < W; ++a0) {
+                    const int idx = loc[0] + a0;
+                    atomicAdd(&tre[idx], cv.x * wt[0][a0]);
+                    atomicAdd(&tim[idx], cv.y * wt[0][a0]);
+                }
+            } else if constexpr (DIM == 2) {
+#pragma unroll
+                for (int a0 = 0; a0 < W; ++a0) {
+                    const float r = cv.x * wt[0][a0], i = cv.y * wt[0][a0];
+                    const int base = (loc[0] + a0) * p1 + loc[1];
+#pragma unroll
+                    for (int a1 = 0; a1 < W; ++a1) {
+                        atomicAdd(&tre[base + a1], r * wt[1][a1]);
+                        atomicAdd(&tim[base + a1], i * wt[1][a1]);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int a0 = 0; a0 < W; ++a0) {
+#pragma unroll
+                    for (int a1 = 0; a1 < W; ++a1) {
+                        const float w01 = wt[0][a0] * wt[1][a1];
+                        const float r = cv.x * w01, i = cv.y * w01;
+                        const int base = ((loc[0] + a0) * p1 + loc[1] + a1) * p2 + loc[2];
+#pragma unroll
+                        for (int a2 = 0; a2 < W; ++a2) {
+                            atomicAdd(&tre[base + a2], r * wt[2][a2]);
+                            atomicAdd(&tim[base + a2], i * wt[2][a2]);
+                        }
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    const int o0 = b[0] * g.m[0] - W / 2;
+    const int o1 = DIM >= 2 ? b[1] * g.m[1] - W / 2 : 0;
+    const int o2 = DIM >= 3 ? b[2] * g.m[2] - W / 2 : 0;
+    const int64_t gsz = (int64_t)g.n[0] * g.n[1] * g.n[2];
+    for (int q = threadIdx.x; q < T; q += 256) {
+        const int q2 = q % p2, r12 = q / p2;
+        const int q1 = r12 % p1, q0 = r12 / p1;
+        const int g0 = wrap_tile(o0 + q0, g.n[0]);
+        const int g1 = DIM >= 2 ? wrap_tile(o1 + q1, g.n[1]) : 0;
+        const int g2 = DIM >= 3 ? wrap_tile(o2 + q2, g.n[2]) : 0;
+        const int64_t cell = ((int64_t)g0 * g.n[1] + g1) * g.n[2] + g2;
+        for (int v = 0; v < nvec; ++v) {
+            const float *tre = lds + (size_t)2 * T * v;
+            const float re = tre[q], im = tre[T + q];
+            if (re == 0.0f && im == 0.0f) continue;
+            float *dst = reinterpret_cast<float *>(grid + (BATCH ? (b0 + v) * gsz : 0) + cell);
+            unsafeAtomicAdd(dst, re);
+            unsafeAtomicAdd(dst + 1, im);
+        }
+    }
+}
+
+template <int DIM, int W>
+struct SpreadLaunch {
+    static int run(const SpreadArgs &a) {
+        Geom g = make_geom(a.g);
+        const float bl2e = (float)(a.beta * 1.4426950408889634);
+        const float inv_hw = (float)(2.0 / W);
+        const int64_t T = tile_cells(a.g);
+        const bool batch = a.bc > 1 || a.b0 > 0;
+        const size_t lds = (size_t)2 * T * sizeof(float) * (batch ? a.bc : 1);
+        if (lds > (size_t)max_lds_per_block()) {
+            set_error("spread: tile does not fit in LDS; use smaller bins");
+            return MN_EINVAL;
+        }
+        if (a.nsub == 0) return MN_OK;
+        auto kern = batch ? k_spread_tiled<DIM, W, true> : k_spread_tiled<DIM, W, false>;
+        if (lds > 65536)
+            MN_HIP_CHECK(hipFuncSetAttribute((const void *)kern,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        kern<<<(unsigned)a.nsub, 256, lds, a.s>>>(g, bl2e, inv_hw, a.nsub, a.info, a.perm, a.i1s,
+                                                  a.frs, a.c, a.pre, a.grid, a.P, a.b0, a.bc);
+        MN_LAUNCH_CHECK("spread");
+        return MN_OK;
+    }
+};
+
+}  // namespace
+
+}  // namespace mn
+
+using namespace mn;
+
+extern "C" {
+
+int mn_spread(const mn_bins *g, float beta, int64_t P, int64_t nsub, const int32_t *sub_info,
+              const uint32_t *perm, const int32_t *const i1s[3], const float *const frs[3],
+              const void *c, const void *pre, void *grid, mn_stream_t stream) {
+    clear_error();
+    int rc = check_bins(g);
+    if (rc) return rc;
+    SpreadArgs a{};
+    rc = check_points(g, P, nsub, sub_info, perm, i1s, frs, &a.i1s, &a.frs);
+    if (rc) return rc;
+    MN_REQUIRE(c && grid, "spread: NULL strengths or grid");
+    int64_t gsz = 1;
+    for (int d = 0; d < g->dim; ++d) gsz *= g->n[d];
+    a.g = g;
+    a.beta = beta;
+    a.P = P;
+    a.nsub = nsub;
+    a.info = sub_info;
+    a.perm = perm;
+    a.c = static_cast<const float2 *>(c);
+    a.pre = static_cast<const float2 *>(pre);
+    a.grid = static_cast<float2 *>(grid);
+    a.b0 = 0;
+    a.bc = 1;
+    a.s = as_stream(stream);
+    rc = fill_zero(grid, gsz * 8, a.s);
+    if (rc) return rc;
+    return select_dim_w<SpreadLaunch>(g->dim, g->w, a);
+}
+
+int mn_spread_batch(const mn_bins *g, float beta, int64_t P, int64_t nsub,
+                    const int32_t *sub_info, const uint32_t *perm, const int32_t *const i1s[3],
+                    const float *const frs[3], int64_t B, const void *cs, void *grids,
+                    mn_stream_t stream) {
+    clear_error();
+    int rc = check_bins(g);
+    if (rc) return rc;
+    SpreadArgs a{};
+    rc = check_points(g, P, nsub, sub_info, perm, i1s, frs, &a.i1s, &a.frs);
+    if (rc) return rc;
+    MN_REQUIRE(B >= 1, "spread_batch: B must be >= 1");
+    MN_REQUIRE(cs && grids, "spread_batch: NULL strengths or grids");
+    int64_t gsz = 1;
+    for (int d = 0; d < g->dim; ++d) gsz *= g->n[d];
+    a.g = g;
+    a.beta = beta;
+    a.P = P;
+    a.nsub = nsub;
+    a.info = sub_info;
+    a.perm = perm;
+    a.c = static_cast<const float2 *>(cs);
+    a.pre = nullptr;
+    a.grid = static_cast<float2 *>(grids);
+    a.s = as_stream(stream);
+    rc = fill_zero(grids, B * gsz * 8, a.s);
+    if (rc) return rc;
+    // Vectors per launch: as many tiles as fit in 64 KB of LDS (at least 1).
+    const int64_t tile_bytes = 8 * tile_cells(g);
+    int64_t per = 65536 / tile_bytes;
+    if (per < 1) per = 1;
+    if (per > B) per = B;
+    for (int64_t v0 = 0; v0 < B; v0 += per) {
+        a.b0 = v0;
+        a.bc = (int)((B - v0 < per) ? (B - v0) : per);
+        rc = select_dim_w<SpreadLaunch>(g->dim, g->w, a);
+        if (rc) return rc;
+    }
+    return MN_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,262 @@
+"""Type-1/2 NUFFT plans in 1, 2 and 3 dims on the MI355X engine.
+
+    type 1:  f[k] = sum_j c[j] exp(i*isign * k . x_j)
+    type 2:  c[j] = sum_k f[k] exp(i*isign * k . x_j)
+
+with k_d in [-(N_d//2), (N_d-1)//2] (modeord=0, even or odd N_d) and any x
+(folded mod 2pi in fp64). Mirrors the reference's Type1PlanND/Type2PlanND
+(ref: mlx_nufft/nd.py:94-1119): the constructor is setpts, execute runs
+the transform; all device work is HIP kernels behind the C-ABI.
+
+Pipeline (type 1): fp64 setpts (fold, rescale, cell/frac, bin key) ->
+stable radix bin sort -> subproblem table -> LDS-tiled ES spread with halo
+flush -> rocFFT (unnormalised; backward for isign>0) -> fused mode shuffle
++ deconvolution. Type 2 runs the adjoint chain: pad+deconvolve -> FFT ->
+LDS-tiled interpolation written straight to caller order.
+"""
+
+import numpy as np
+import torch
+
+from . import _engine as E
+from . import _lib as L
+from .sizing import kernel_ft, kernel_params, next235even
+
+PI = np.pi
+
+
+def _as_coord_tuple(x):
+    if isinstance(x, (np.ndarray, torch.Tensor)) and x.ndim == 1:
+        x = (x,)
+    return tuple(x)
+
+
+class _PointsND:
+    """Shared point/kernel setup for ND types 1 and 2 (ref: nd.py:94-150)."""
+
+    def __init__(self, x, n_modes, eps, isign, upsampfac, prec, sort_points):
+        if prec not in ("fp32", "crit64"):
+            raise ValueError("prec must be 'fp32' or 'crit64'")
+        x = _as_coord_tuple(x)
+        self.dim = len(x)
+        if self.dim not in (1, 2, 3):
+            raise ValueError("dims 1, 2, 3 supported")
+        if np.isscalar(n_modes):
+            n_modes = (int(n_modes),) * self.dim
+        self.N = tuple(int(n) for n in n_modes)
+        if len(self.N) != self.dim:
+            raise ValueError(f"n_modes length {len(self.N)} must match dim {self.dim}")
+        if any(n < 1 for n in self.N):
+            raise ValueError("mode dims must be >= 1")
+        if upsampfac in (None, 0, 0.0):
+            upsampfac = 2.0
+        if not 1.0 < upsampfac <= 4.0:
+            raise ValueError(f"upsampfac must be in (1, 4], got {upsampfac}")
+        self.prec = prec
+        self.isign = +1 if isign >= 0 else -1
+        self.eps = eps
+        self.sigma = upsampfac
+        self.w, self.beta = kernel_params(eps, upsampfac)
+        self.n_up = [next235even(max(2 * self.w, int(np.ceil(upsampfac * n)))) for n in self.N]
+        self._sort_points = bool(sort_points)
+        self.profile = False
+        self.last_profile = {}
+
+        self.device = L.require_gpu()
+        x64 = self._coords(x)
+        self.P = x64[0].numel()
+        self.bins = E.make_bins(self.dim, self.w, self.n_up)
+        self._set_points(x64)
+
+        # Mode deconvolution 1/phihat(2 pi k / n_up) on the uncentred fine grid
+        # (points folded into [0, 2pi), so no (-1)^k factor). rocFFT's backward
+        # transform is unnormalised, so no prod(n_up) factor is folded in
+        # (ref: nd.py:136-149 folds it because its ifft divides by n).
+        self.decs = []
+        for d in range(self.dim):
+            k = np.arange(-(self.N[d] // 2), self.N[d] - self.N[d] // 2, dtype=np.float64)
+            self.decs.append(1.0 / kernel_ft(2.0 * PI * k / self.n_up[d], self.beta, self.w))
+        self.dev_dec = [torch.from_numpy(v.astype(np.float32)).to(self.device) for v in self.decs]
+        self._grid = None
+
+    # -- point state -------------------------------------------------------
+
+    def _coords(self, x):
+        x64 = [L.to_dev_f64(v, self.device) for v in x]
+        P = x64[0].numel()
+        if P < 1:
+            raise ValueError("at least one nonuniform point is required")
+        if not all(v.numel() == P for v in x64):
+            raise ValueError("coordinate arrays must have equal length")
+        return x64
+
+    def _compute_cells_gpu(self, x64):
+        """Unsorted device (i1 int32, fr fp32) lists per dim for fp64 coords,
+        bit-exact with the reference's host fp64 path (ref: nd.py:152-165)."""
+        if not isinstance(x64[0], torch.Tensor):
+            x64 = [L.to_dev_f64(v, self.device) for v in x64]
+        i1, fr, _ = E.setpts_t12(self.bins, x64, self.prec == "crit64")
+        return [i1[d] for d in range(self.dim)], [fr[d] for d in range(self.dim)]
+
+    def _compute_cells(self, x64):
+        """numpy mirrors self.i1 / self.fr of the cell setup (caller order)."""
+        i1, fr = self._compute_cells_gpu(x64)
+        self.i1 = [v.cpu().numpy() for v in i1]
+        self.fr = [v.cpu().numpy() for v in fr]
+
+    def _set_points(self, x64):
+        i1, fr, key = E.setpts_t12(self.bins, x64, self.prec == "crit64")
+        self.pts = E.SortedPoints(self.bins, i1, fr, key)
+        self.sorted = True
+        self._od = True
+
+    @property
+    def mx_perm(self):
+        """Device permutation (sorted position -> caller index)."""
+        return self.pts.perm
+
+    @property
+    def perm(self):
+        return self.pts.perm.cpu().numpy().astype(np.intp)
+
+    def _fine_grid(self, batch=1):
+        shape = (batch, *self.n_up)
+        if self._grid is None or tuple(self._grid.shape) != shape:
+            self._grid = None
+            self._grid = torch.empty(shape, dtype=torch.complex64, device=self.device)
+        return self._grid
+
+    def _timer(self):
+        return E.StageTimer(self.profile)
+
+    def _finish_profile(self, tm):
+        if self.profile:
+            self.last_profile = tm.times_ms()
+
+
+class Type1PlanND(_PointsND):
+    """f[k] = sum_j c[j] exp(i*isign * k . x_j), modeord=0 box, dims 1-3.
+
+    ref: nd.py:386-855.
+    """
+
+    def __init__(self, x, n_modes, eps=1e-6, isign=+1, upsampfac=2.0, prec="crit64",
+                 sort_points=True, spread_method="auto"):
+        assert spread_method in ("auto", "od", "gm")
+        self.spread_method = spread_method
+        super().__init__(x, n_modes, eps, isign, upsampfac, prec, sort_points)
+
+    def _strengths(self, c):
+        cd = L.to_dev_c64(c, self.device).reshape(-1)
+        if cd.numel() != self.P:
+            raise ValueError(f"c.size ({cd.numel()}) must equal the number of nonuniform "
+                             f"points ({self.P})")
+        return cd
+
+    def execute(self, c, return_np=True):
+        """ref: nd.py:581-625."""
+        cd = self._strengths(c)
+        grid = self._fine_grid(1)
+        fk = torch.empty(self.N, dtype=torch.complex64, device=self.device)
+        tm = self._timer()
+        with tm("spread"):
+            E.spread(self.pts, self.beta, cd, grid)
+        with tm("fft"):
+            E.fft(grid, self.n_up, self.isign)
+        with tm("deconv"):
+            E.crop_deconv(self.n_up, self.N, grid, self.dev_dec, fk)
+        self._finish_profile(tm)
+        return L.to_host(fk) if return_np else fk
+
+    def execute_batch(self, cs, return_np=True):
+        """B strength vectors over the same points: one shared spread (ES
+        weights once per point), one batched FFT, one batched crop.
+        cs: (B, P) -> (B, *N). ref: nd.py:744-794."""
+        if isinstance(cs, torch.Tensor):
+            shape = tuple(cs.shape)
+        else:
+            cs = np.asarray(cs)
+            shape = cs.shape
+        if len(shape) != 2 or shape[1] != self.P:
+            raise ValueError(f"cs must have shape (B, {self.P})")
+        B = int(shape[0])
+        cd = L.to_dev_c64(cs, self.device).reshape(B, self.P)
+        grids = self._fine_grid(B)
+        fk = torch.empty((B, *self.N), dtype=torch.complex64, device=self.device)
+        tm = self._timer()
+        with tm("spread"):
+            E.spread_batch(self.pts, self.beta, cd, grids)
+        with tm("fft"):
+            E.fft(grids, self.n_up, self.isign, batch=B)
+        with tm("deconv"):
+            E.crop_deconv(self.n_up, self.N, grids, self.dev_dec, fk, batch=B)
+        self._finish_profile(tm)
+        return L.to_host(fk) if return_np else fk
+
+    def set_sources(self, x, backend="host"):
+        """Re-point the plan to new coordinates, keeping kernels, deconvolution
+        and FFT plans; P may change. Both backends run the same bit-exact
+        native-fp64 device setup (the reference's "host" is its fp64 numpy
+        path, "gpu" its df64 Metal path). Returns self. ref: nd.py:627-681."""
+        x = _as_coord_tuple(x)
+        if len(x) != self.dim:
+            raise ValueError(f"expected {self.dim} coordinate arrays, got {len(x)}")
+        if backend not in ("host", "gpu"):
+            raise ValueError(f"unknown backend {backend!r}")
+        x64 = [L.to_dev_f64(v, self.device) for v in x]
+        P = x64[0].numel()
+        if P < 1 or not all(v.numel() == P for v in x64):
+            raise ValueError("coordinate arrays must be non-empty, equal length")
+        self.P = P
+        self.pts = None
+        self._set_points(x64)
+        return self
+
+    def execute_disjoint(self, c, groups, return_np=True):
+        """G independent transforms of disjoint point subsets of one plan:
+        out[g] = type-1 of c restricted to {j : groups[j] == g}; (G, *N).
+        ref: nd.py:796-855."""
+        groups = np.asarray(groups.cpu() if isinstance(groups, torch.Tensor) else groups)
+        if groups.shape != (self.P,):
+            raise ValueError(f"groups must have shape ({self.P},)")
+        cd = self._strengths(c)
+        G = int(groups.max()) + 1 if groups.size else 0
+        if G == 0:
+            out = torch.zeros((0, *self.N), dtype=torch.complex64, device=self.device)
+            return L.to_host(out) if return_np else out
+        gd = torch.from_numpy(groups.astype(np.int64)).to(self.device)
+        sel = gd[None, :] == torch.arange(G, device=self.device)[:, None]
+        cs = torch.where(sel, cd[None, :], torch.zeros((), dtype=cd.dtype, device=self.device))
+        return self.execute_batch(cs.contiguous(), return_np=return_np)
+
+
+class Type2PlanND(_PointsND):
+    """c[j] = sum_k f[k] exp(i*isign * k . x_j), modeord=0 box, dims 1-3.
+
+    ref: nd.py:858-1119.
+    """
+
+    def __init__(self, x, n_modes, eps=1e-6, isign=-1, upsampfac=2.0, prec="crit64",
+                 sort_points=False, spread_method="auto"):
+        assert spread_method in ("auto", "od", "gm")
+        self.spread_method = spread_method
+        super().__init__(x, n_modes, eps, isign, upsampfac, prec, sort_points)
+
+    def execute(self, fk, return_np=True):
+        """ref: nd.py:1075-1119."""
+        fd = L.to_dev_c64(fk, self.device).reshape(-1)
+        ntot = int(np.prod(self.N))
+        if fd.numel() != ntot:
+            raise ValueError(f"f.size ({fd.numel()}) must equal the mode-box size "
+                             f"{tuple(self.N)}")
+        grid = self._fine_grid(1)
+        out = torch.empty(self.P, dtype=torch.complex64, device=self.device)
+        tm = self._timer()
+        with tm("deconv"):
+            E.pad_deconv(self.n_up, self.N, fd, self.dev_dec, grid)
+        with tm("fft"):
+            E.fft(grid, self.n_up, self.isign)
+        with tm("interp"):
+            E.interp(self.pts, self.beta, grid, out)
+        self._finish_profile(tm)
+        return L.to_host(out) if return_np else out

@@ -1,0 +1,234 @@
+"""Type-3 3D NUFFT plan (nonuniform -> nonuniform) on the MI355X engine.
+
+    f[k] = sum_j c[j] exp(i*isign * s_k . x_j)
+
+FINUFFT-structured like the reference (ref: mlx_nufft/gpu_t3.py:287-1364):
+sources are rescaled onto an nf^3 grid, pre-phased by exp(i isign D.x) and
+spread; the grid is deconvolved and zero-padded to n_up^3, FFT'd, and
+interpolated at the rescaled targets, then multiplied by the post factor
+exp(i isign C.(s-D)) / prod_d phihat(theta_d). Plan setup (sizing scalars,
+mode deconvolution vectors) is host fp64; per-point setup (source and target
+rescale, phases, phihat at every target) is native fp64 on the GPU. The
+prephase is fused into the spread and the post factor into the gather.
+
+MI355X holds the n_up^3 grid in HBM at every size the reference handles, so
+there is no slab mode: grids past the reference's 3 GB slab threshold run
+the same single-grid pipeline.
+"""
+
+import warnings
+
+import numpy as np
+import torch
+
+from . import _engine as E
+from . import _lib as L
+from .sizing import (inner_kernel_params, kernel_ft, kernel_params, next235even,
+                     quadrature, set_nhg_type3)
+
+PI = np.pi
+_SLAB_THRESHOLD = 3e9   # the reference's slab switch (bytes); informational here
+_PREC_FLAGS = {"fp32": 0, "coords64": 1, "phases64": 2, "crit64": 3}
+
+
+class GpuT3Plan:
+    def __init__(self, x, s, eps=1e-5, isign=+1, upsampfac=1.25, prec="crit64",
+                 sigma_inner=None, sort_points=True, low_mem=None, source_extent=None,
+                 fft_backend="mlx"):
+        """x: 3 source coordinate arrays (P,), s: 3 target arrays (M,).
+
+        source_extent: optional [(lo, hi)] * 3 bounds to size the plan for,
+        so set_sources() accepts later frames inside them.
+        fft_backend: "mlx" (the built-in rocFFT path on this engine) or
+        "vkfft" (not available on this platform: raises RuntimeError).
+        ref: gpu_t3.py:288-441.
+        """
+        assert prec in ("fp32", "coords64", "phases64", "crit64")
+        assert fft_backend in ("mlx", "vkfft")
+        if fft_backend == "vkfft":
+            raise RuntimeError("the VkFFT-Metal FFT backend is not available on this "
+                               "platform; use fft_backend='mlx' (rocFFT)")
+        self.fft_backend = fft_backend
+        self.prec = prec
+        self._flags = _PREC_FLAGS[prec]
+        self.isign = int(np.sign(isign))
+        self.eps = eps
+        self.sigma = upsampfac
+        self.w, self.beta = kernel_params(eps, upsampfac)
+        if sigma_inner is None or sigma_inner == upsampfac:
+            self.sigma_in = upsampfac
+            self.w2, self.beta2 = self.w, self.beta
+        else:
+            self.sigma_in = sigma_inner
+            self.w2, self.beta2 = inner_kernel_params(eps, sigma_inner)
+        self.device = L.require_gpu()
+        self.profile = False
+        self.last_profile = {}
+
+        x = tuple(x)
+        s = tuple(s)
+        if len(x) != 3 or len(s) != 3:
+            raise ValueError("type-3 plans take 3 source and 3 target coordinate arrays")
+        x64 = [L.to_dev_f64(v, self.device) for v in x]
+        s64 = [L.to_dev_f64(v, self.device) for v in s]
+        self.P = x64[0].numel()
+        self.M = s64[0].numel()
+        if self.P < 1 or self.M < 1:
+            raise ValueError("type-3 needs at least one source and one target")
+        if not all(v.numel() == self.P for v in x64) or not all(v.numel() == self.M for v in s64):
+            raise ValueError("coordinate arrays must have equal length")
+
+        # ---- sizing (host fp64 scalars; ref: gpu_t3.py:326-342) -----------
+        smin = [float(v.min()) for v in s64]
+        smax = [float(v.max()) for v in s64]
+        if source_extent is not None:
+            self._xext = [(float(lo), float(hi)) for lo, hi in source_extent]
+        else:
+            self._xext = [(float(v.min()), float(v.max())) for v in x64]
+        self.nf, self.gam, self.C, self.D = [], [], [], []
+        for d in range(3):
+            xlo, xhi = self._xext[d]
+            C = 0.5 * (xlo + xhi)
+            D = 0.5 * (smin[d] + smax[d])
+            X = 0.5 * (xhi - xlo)
+            S = 0.5 * (smax[d] - smin[d])
+            nf, _, gam = set_nhg_type3(S, X, upsampfac, self.w)
+            self.nf.append(nf)
+            self.gam.append(gam)
+            self.C.append(C)
+            self.D.append(D)
+        self.n_up = [next235even(int(np.ceil(self.sigma_in * nf))) for nf in self.nf]
+        self.slab_mode = False
+
+        # ---- targets: rescale, post factor, bin sort (device fp64) ----------
+        self.bins_trg = E.make_bins(3, self.w2, self.n_up)
+        hd = [2.0 * PI / nf for nf in self.nf]
+        hg = [hd[d] * self.gam[d] for d in range(3)]
+        h2 = [2.0 * PI / n for n in self.n_up]
+        dq, fq = quadrature(self.beta, self.w)
+        quad = torch.from_numpy(np.concatenate([dq, fq])).to(self.device)
+        t_i1 = torch.empty((3, self.M), dtype=torch.int32, device=self.device)
+        t_fr = torch.empty((3, self.M), dtype=torch.float32, device=self.device)
+        t_key = torch.empty(self.M, dtype=torch.int32, device=self.device)
+        post = torch.empty(self.M, dtype=torch.complex64, device=self.device)
+        L.check(L.lib().mn_t3_setpts_trg(
+            L.ctypes.byref(self.bins_trg), self.M, L.ptr3(s64), L.d3(self.D), L.d3(hg), L.d3(h2),
+            L.d3(self.C), self.isign, self._flags, L.ptr(quad), len(dq),
+            L.ptr3([t_i1[d] for d in range(3)]), L.ptr3([t_fr[d] for d in range(3)]),
+            L.ptr(t_key), L.ptr(post), L.stream()), "t3 targets")
+        self.trg = E.SortedPoints(self.bins_trg, t_i1, t_fr, t_key, extra=post)
+        del t_i1, t_fr, t_key, post
+
+        # ---- mode deconvolution (-1)^|q| / phihat(2 pi q / n_up), q in
+        # [-nf/2, nf/2); rocFFT's backward transform is unnormalised
+        # (ref: gpu_t3.py:379-392).
+        self.decs = []
+        for d in range(3):
+            q = np.arange(-self.nf[d] // 2, self.nf[d] // 2, dtype=np.float64)
+            ph = kernel_ft(2.0 * PI * q / self.n_up[d], self.beta2, self.w2)
+            self.decs.append(((-1.0) ** np.abs(q)) / ph)
+        self.dev_dec = [torch.from_numpy(v.astype(np.float32)).to(self.device)
+                        for v in self.decs]
+        self.bins_src = E.make_bins(3, self.w, self.nf)
+        self._hd = hd
+        self._bf = None
+        self._H = None
+        self.low_mem = bool(low_mem) if low_mem is not None else False
+        self.set_sources(x64)
+
+    # ------------------------------------------------------------------
+    def set_sources(self, x, backend="host"):
+        """Per-frame source update against the frozen grid/target setup; new
+        sources must lie inside the planned extent plus half the kernel guard
+        band (else ValueError). Both backends run the same native-fp64 device
+        setup. ref: gpu_t3.py:444-506."""
+        if backend not in ("host", "gpu"):
+            raise ValueError(f"unknown backend {backend!r}")
+        x64 = [L.to_dev_f64(v, self.device) for v in x]
+        P = x64[0].numel()
+        if P < 1 or not all(v.numel() == P for v in x64):
+            raise ValueError("source coordinate arrays must be non-empty, equal length")
+        for d in range(3):
+            lo, hi = self._xext[d]
+            guard = 0.45 * (self.w + 1) * self.gam[d] * (2.0 * PI / self.nf[d])
+            if float(x64[d].min()) < lo - guard or float(x64[d].max()) > hi + guard:
+                raise ValueError(
+                    f"set_sources: dim {d} sources exceed the frozen plan extent "
+                    f"[{lo:.4g}, {hi:.4g}] (+guard {guard:.3g}); rebuild the plan for this "
+                    "geometry")
+        self.P = P
+        i1 = torch.empty((3, P), dtype=torch.int32, device=self.device)
+        fr = torch.empty((3, P), dtype=torch.float32, device=self.device)
+        key = torch.empty(P, dtype=torch.int32, device=self.device)
+        pre = torch.empty(P, dtype=torch.complex64, device=self.device)
+        L.check(L.lib().mn_t3_setpts_src(
+            L.ctypes.byref(self.bins_src), P, L.ptr3(x64), L.d3(self.C), L.d3(self.gam),
+            L.d3(self._hd), L.d3(self.D), self.isign, self._flags,
+            L.ptr3([i1[d] for d in range(3)]), L.ptr3([fr[d] for d in range(3)]), L.ptr(key),
+            L.ptr(pre), L.stream()), "t3 sources")
+        self.src = E.SortedPoints(self.bins_src, i1, fr, key, extra=pre)
+
+    @property
+    def mx_perm(self):
+        return self.src.perm
+
+    @property
+    def perm(self):
+        return self.src.perm.cpu().numpy().astype(np.intp)
+
+    def _buffers(self):
+        if self._bf is None:
+            self._bf = torch.empty(self.nf, dtype=torch.complex64, device=self.device)
+            self._H = torch.empty(self.n_up, dtype=torch.complex64, device=self.device)
+        return self._bf, self._H
+
+    def _run(self, cd, tm):
+        bf, H = self._buffers()
+        out = torch.empty(self.M, dtype=torch.complex64, device=self.device)
+        with tm("spread"):
+            E.spread(self.src, self.beta, cd, bf, pre=self.src.extra)
+        with tm("pad+deconv"):
+            E.pad_deconv(self.n_up, self.nf, bf, self.dev_dec, H)
+        with tm("fft"):
+            E.fft(H, self.n_up, self.isign)
+        with tm("gather"):
+            E.interp(self.trg, self.beta2, H, out, post=self.trg.extra)
+        if self.low_mem:
+            self._bf = self._H = None
+        return out
+
+    def _strengths(self, c):
+        cd = L.to_dev_c64(c, self.device).reshape(-1)
+        assert cd.numel() == self.P, \
+            f"c.size ({cd.numel()}) must equal number of sources ({self.P})"
+        return cd
+
+    def execute(self, c, return_np=True):
+        """ref: gpu_t3.py:1287-1349."""
+        tm = E.StageTimer(self.profile)
+        out = self._run(self._strengths(c), tm)
+        if self.profile:
+            self.last_profile = tm.times_ms()
+        return L.to_host(out) if return_np else out
+
+    def execute_batch(self, cs, return_np=True):
+        """nch strength channels through one plan: (nch, P) -> (nch, M).
+        ref: gpu_t3.py:941-1041 (the reference supports it in slab mode only;
+        here every plan supports it)."""
+        cs_t = cs if isinstance(cs, torch.Tensor) else np.asarray(cs)
+        if cs_t.ndim != 2 or cs_t.shape[1] != self.P:
+            raise ValueError(f"cs must have shape (nch, {self.P})")
+        cd = L.to_dev_c64(cs_t, self.device)
+        tm = E.StageTimer(False)
+        res = torch.stack([self._run(cd[ch], tm) for ch in range(cd.shape[0])])
+        return L.to_host(res) if return_np else res
+
+    def execute_profiled(self, c):
+        """(result, {stage: seconds}) with HIP-event stage times; the prephase
+        is fused into the spread (ref: gpu_t3.py:1351-1364)."""
+        tm = E.StageTimer(True)
+        out = self._run(self._strengths(c), tm)
+        ms = tm.times_ms()
+        times = {"prephase": 0.0}
+        times.update({k: v / 1e3 for k, v in ms.items()})
+        return L.to_host(out), times

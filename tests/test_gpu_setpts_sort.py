@@ -1,0 +1,119 @@
+"""GPU parity of plan-time point setup, the bin sort and the subproblem table.
+
+Bar: bit-exact. i1 and fr against the CPU oracle (itself pinned to numpy's
+np.mod/ceil in test_oracle.py), bin keys against the oracle's key function,
+the permutation against numpy's argsort(kind="stable") on the same keys
+(ref: nd.py:314), and the subproblem rows against a numpy restatement of
+the reference's table build (ref: nd.py:347-360).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+TWO_PI = 2.0 * np.pi
+
+
+def _coords(rng, dim, P):
+    """Half in [-pi, pi), half over +-1000*2pi, plus edge values."""
+    edge = np.array([0.0, -0.0, TWO_PI, -TWO_PI, np.pi, -np.pi, 1e-300, -1e-300, -5e-324,
+                     -1e-17, 1e-17, 7e15, -7e15, 3 * TWO_PI, -1000 * TWO_PI, 12345.678,
+                     np.nextafter(TWO_PI, 0), np.nextafter(-np.pi, 0)])
+    out = []
+    for _ in range(dim):
+        a = rng.uniform(-np.pi, np.pi, P // 2)
+        b = rng.uniform(-1000 * TWO_PI, 1000 * TWO_PI, P - P // 2 - edge.size)
+        out.append(np.concatenate([a, b, rng.permutation(edge)]))
+    return out
+
+
+@pytest.mark.parametrize("dim,N", [(1, (4096,)), (2, (2048, 2048)), (3, (256, 256, 128)),
+                                   (3, (21, 18, 14))])
+@pytest.mark.parametrize("prec", ["crit64", "fp32"])
+def test_setpts_bitexact(dim, N, prec, oracle):
+    from mlx_nufft_amd import _engine as E
+
+    print(f"case setpts dim={dim} N={N} prec={prec}", flush=True)
+    rng = np.random.default_rng(11)
+    x = _coords(rng, dim, 60_000)
+    w, beta, n_up = oracle.type12_grid(N, 1e-5)
+    i1o, fro = oracle.setpts_t12(x, n_up, w, prec == "crit64")
+    bins = E.make_bins(dim, w, n_up)
+    xd = [torch.from_numpy(v).cuda() for v in x]
+    i1, fr, key = E.setpts_t12(bins, xd, prec == "crit64")
+    i1, fr, key = i1.cpu().numpy(), fr.cpu().numpy(), key.cpu().numpy().view(np.uint32)
+    assert np.array_equal(i1, i1o), f"i1 mismatches: {np.sum(i1 != i1o)}"
+    assert np.array_equal(fr.view(np.int32), fro.view(np.int32)), \
+        f"fr mismatches: {np.sum(fr != fro)} max {np.max(np.abs(fr - fro))}"
+    ko, _ = oracle.bin_keys(i1o, n_up, [bins.m[d] for d in range(dim)], w)
+    assert np.array_equal(key, ko)
+
+
+def _keys_for(oracle, x, N, eps=1e-5):
+    from mlx_nufft_amd import _engine as E
+
+    dim = len(x)
+    w, beta, n_up = oracle.type12_grid(N, eps)
+    bins = E.make_bins(dim, w, n_up)
+    i1o, _ = oracle.setpts_t12(x, n_up, w)
+    ko, nk = oracle.bin_keys(i1o, n_up, [bins.m[d] for d in range(dim)], w)
+    return bins, ko, nk
+
+
+@pytest.mark.parametrize("case", ["uniform3d_2M", "cluster3d", "uniform2d", "tiny1", "tile_edge",
+                                  "all_equal"])
+def test_sort_matches_numpy_stable(case, oracle):
+    from mlx_nufft_amd import _engine as E
+
+    print(f"case sort {case}", flush=True)
+    rng = np.random.default_rng(5)
+    if case == "uniform3d_2M":
+        x, N = [rng.uniform(-np.pi, np.pi, 2_000_000) for _ in range(3)], (256,) * 3
+    elif case == "cluster3d":
+        h = 2 * np.pi / 512
+        x, N = [-np.pi + rng.uniform(0, 8 * h, 300_000) for _ in range(3)], (256,) * 3
+    elif case == "uniform2d":
+        x, N = [rng.uniform(-np.pi, np.pi, 1_000_003) for _ in range(2)], (1024, 1024)
+    elif case == "tiny1":
+        x, N = [rng.uniform(-np.pi, np.pi, 1)], (64,)
+    elif case == "tile_edge":
+        x, N = [rng.uniform(-np.pi, np.pi, 4097) for _ in range(2)], (96, 80)
+    else:
+        x, N = [np.full(10_000, 0.5) for _ in range(3)], (32, 32, 32)
+    bins, ko, nk = _keys_for(oracle, x, N)
+    ref = np.argsort(ko, kind="stable")
+    kd = torch.from_numpy(ko.view(np.int32)).cuda()
+    skey, perm = E.sort_keys(kd, E.key_bits(bins))
+    perm = perm.cpu().numpy().view(np.uint32)
+    assert np.array_equal(perm, ref.astype(np.uint32))
+    assert np.array_equal(skey.cpu().numpy().view(np.uint32), ko[ref])
+    # the oracle's own counting sort agrees too
+    assert np.array_equal(oracle.stable_sort(ko, nk), ref.astype(np.uint32))
+
+
+@pytest.mark.parametrize("msub", [1024, 7])
+def test_subproblem_table(msub, oracle):
+    from mlx_nufft_amd import _engine as E
+
+    print(f"case subproblems msub={msub}", flush=True)
+    rng = np.random.default_rng(6)
+    h = 2 * np.pi / 128
+    x = [np.concatenate([rng.uniform(-np.pi, np.pi, 50_000), -np.pi + rng.uniform(0, 4 * h, 20_000)])
+         for _ in range(3)]
+    bins, ko, nk = _keys_for(oracle, x, (64, 64, 64))
+    ks = np.sort(ko, kind="stable")
+    info, nsub = E.build_subproblems(bins, torch.from_numpy(ks.view(np.int32)).cuda(), msub)
+    info = info[:nsub].cpu().numpy()
+    # numpy restatement of the reference's table build (nd.py:351-360)
+    starts = np.flatnonzero(np.r_[True, ks[1:] != ks[:-1]])
+    counts = np.diff(np.r_[starts, ks.size])
+    per = (counts + msub - 1) // msub
+    bin_id = np.repeat(np.arange(starts.size), per)
+    seg = np.cumsum(per) - per
+    off = (np.arange(per.sum()) - np.repeat(seg, per)) * msub
+    exp = np.stack([ks[starts][bin_id].astype(np.int64), starts[bin_id] + off,
+                    np.minimum(msub, counts[bin_id] - off)], axis=1)
+    assert nsub == exp.shape[0]
+    assert np.array_equal(info.astype(np.int64), exp)

@@ -1,0 +1,204 @@
+"""GPU parity of the transforms at sizes the CPU oracle finishes in seconds.
+
+Gate: rel_l2(GPU, exact direct sum)
+    <= max(eps, 2 * ref_err),
+with ref_err = rel_l2(CPU fp64 restatement at the same w, beta, n_up, exact
+direct sum) on the same seeded inputs. Kernel-level checks compare the
+spread grid and interpolated values with the oracle's fp64 kernels at a
+1e-5 relative tolerance (fp32 accumulation).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+CASES = [(1, (87,)), (1, (4096,)), (2, (48, 36)), (2, (45, 34)), (3, (24, 20, 16)),
+         (3, (21, 18, 14))]
+
+
+def _pts(rng, dim, M):
+    return [rng.uniform(-np.pi, np.pi, M) for _ in range(dim)]
+
+
+def _cplx(rng, shape):
+    return (rng.standard_normal(shape) + 1j * rng.standard_normal(shape)).astype(np.complex64)
+
+
+def _modes(N):
+    return [np.arange(-(n // 2), n - n // 2) for n in N]
+
+
+@pytest.mark.parametrize("dim,N", CASES)
+@pytest.mark.parametrize("isign", [+1, -1])
+@pytest.mark.parametrize("eps", [1e-3, 1e-5])
+def test_type1_vs_direct(dim, N, isign, eps, oracle, mn):
+    print(f"case t1 dim={dim} N={N} isign={isign} eps={eps}", flush=True)
+    rng = np.random.default_rng(7)
+    M = 40_000
+    x = _pts(rng, dim, M)
+    c = _cplx(rng, M)
+    f = mn.Type1PlanND(tuple(x), N, eps=eps, isign=isign).execute(c)
+    fe = oracle.dft_t1(x, c, _modes(N), isign)
+    ref_err = oracle.rel_l2(oracle.nufft_t1(x, c, N, eps, isign), fe)
+    err = oracle.rel_l2(f, fe)
+    print(f"  err={err:.3e} ref_err={ref_err:.3e}")
+    assert f.shape == N and f.dtype == np.complex64
+    assert err <= max(eps, 2 * ref_err)
+
+
+@pytest.mark.parametrize("dim,N", CASES)
+@pytest.mark.parametrize("isign", [+1, -1])
+@pytest.mark.parametrize("eps", [1e-3, 1e-5])
+def test_type2_vs_direct(dim, N, isign, eps, oracle, mn):
+    print(f"case t2 dim={dim} N={N} isign={isign} eps={eps}", flush=True)
+    rng = np.random.default_rng(8)
+    M = 40_000
+    x = _pts(rng, dim, M)
+    fk = _cplx(rng, N)
+    c = mn.Type2PlanND(tuple(x), N, eps=eps, isign=isign).execute(fk)
+    idx = np.arange(0, M, 37)
+    ce = oracle.dft_t2(x, fk, isign, idx)
+    ref_err = oracle.rel_l2(oracle.nufft_t2(x, fk, eps, isign)[idx], ce)
+    err = oracle.rel_l2(c[idx], ce)
+    print(f"  err={err:.3e} ref_err={ref_err:.3e}")
+    assert c.shape == (M,)
+    assert err <= max(eps, 2 * ref_err)
+
+
+@pytest.mark.parametrize("dim,N", [(1, (300,)), (2, (64, 48)), (3, (32, 24, 20))])
+def test_spread_grid_vs_oracle(dim, N, oracle, mn):
+    """The spread kernel's fine grid against the oracle's fp64 spread on the
+    same (i1, fr) -- a kernel-level check independent of the FFT."""
+    from mlx_nufft_amd import _engine as E
+
+    print(f"case spread-grid dim={dim} N={N}", flush=True)
+    rng = np.random.default_rng(9)
+    M = 30_000
+    x = _pts(rng, dim, M)
+    c = _cplx(rng, M)
+    p = mn.Type1PlanND(tuple(x), N, eps=1e-6)
+    grid = torch.empty(p.n_up, dtype=torch.complex64, device="cuda")
+    E.spread(p.pts, p.beta, torch.from_numpy(c).cuda(), grid)
+    i1o, fro = oracle.setpts_t12(x, p.n_up, p.w)
+    go = oracle.spread(i1o, fro, c, p.n_up, p.w, p.beta)
+    assert oracle.rel_l2(grid.cpu().numpy(), go) < 1e-5
+
+
+@pytest.mark.parametrize("dim,N", [(1, (300,)), (2, (64, 48)), (3, (32, 24, 20))])
+def test_interp_vs_oracle(dim, N, oracle, mn):
+    from mlx_nufft_amd import _engine as E
+
+    print(f"case interp dim={dim} N={N}", flush=True)
+    rng = np.random.default_rng(10)
+    M = 30_000
+    x = _pts(rng, dim, M)
+    p = mn.Type2PlanND(tuple(x), N, eps=1e-6)
+    g = _cplx(rng, tuple(p.n_up))
+    out = torch.empty(M, dtype=torch.complex64, device="cuda")
+    E.interp(p.pts, p.beta, torch.from_numpy(g).cuda(), out)
+    i1o, fro = oracle.setpts_t12(x, p.n_up, p.w)
+    oo = oracle.interp(i1o, fro, g, p.w, p.beta)
+    assert oracle.rel_l2(out.cpu().numpy(), oo) < 1e-5
+
+
+@pytest.mark.parametrize("isign", [+1, -1])
+@pytest.mark.parametrize("eps", [1e-3, 1e-5])
+def test_type3_vs_direct(isign, eps, oracle, mn):
+    print(f"case t3 isign={isign} eps={eps}", flush=True)
+    rng = np.random.default_rng(12)
+    P, M = 20_000, 3_000
+    x = [rng.uniform(-1, 1, P) for _ in range(3)]
+    s = [rng.uniform(-60, 60, M) for _ in range(3)]
+    c = _cplx(rng, P)
+    f = mn.Type3Plan(tuple(x), tuple(s), eps=eps, isign=isign).execute(c)
+    idx = np.arange(0, M, 7)
+    fe = oracle.dft_t3(x, c, s, isign, idx)
+    ref_err = oracle.rel_l2(oracle.nufft_t3(x, c, s, eps, isign)[idx], fe)
+    err = oracle.rel_l2(f[idx], fe)
+    print(f"  err={err:.3e} ref_err={ref_err:.3e}")
+    assert err <= max(eps, 2 * ref_err)
+
+
+def test_expi_accuracy(mn):
+    """ref gates (harness/test_expi.py:26-27): <= 5e-7 for |phi| <= 1e7,
+    <= 3e-6 up to 1e8, against np.exp(1j*isign*phi)."""
+    print("case expi", flush=True)
+    rng = np.random.default_rng(7)
+    for mag, gate in [(1e0, 5e-7), (1e3, 5e-7), (1e7, 5e-7), (1e8, 3e-6), (1e9, 3e-6)]:
+        phi = rng.uniform(-mag, mag, 200_000)
+        for isign in (+1, -1):
+            e = mn.expi(phi, isign=isign, return_np=True)
+            assert np.max(np.abs(e - np.exp(1j * isign * phi))) <= gate, (mag, isign)
+    comps = [rng.uniform(-3.3e7, 3.3e7, 100_000) for _ in range(3)]
+    e = mn.expi(comps, return_np=True)
+    assert np.max(np.abs(e - np.exp(1j * (comps[0] + comps[1] + comps[2])))) <= 3e-6
+    one = rng.uniform(-1e8, 1e8, 5000)
+    assert np.array_equal(mn.expi([one], return_np=True), mn.expi(one, return_np=True))
+    with pytest.raises(ValueError):
+        mn.expi([0.3, 1.7, -2.2])
+    dev = mn.expi(rng.uniform(-1e8, 1e8, (128, 97)))
+    assert isinstance(dev, torch.Tensor) and dev.is_cuda
+    assert dev.dtype == torch.complex64 and tuple(dev.shape) == (128, 97)
+    nan = mn.expi(np.array([np.inf, np.nan, 1.0]), return_np=True)
+    assert np.isnan(nan[0]) and np.isnan(nan[1]) and np.isfinite(nan[2])
+
+
+@pytest.mark.parametrize("dim,N,B", [(1, (4096,), 5), (2, (256, 256), 5), (3, (64, 64, 48), 6)])
+def test_execute_batch_equals_looped(dim, N, B, mn):
+    """ref gate (harness/test_type1_batch.py:65): batched == looped < 1e-5."""
+    print(f"case batch dim={dim} N={N} B={B}", flush=True)
+    rng = np.random.default_rng(11)
+    P = 200_000
+    x = _pts(rng, dim, P)
+    cs = _cplx(rng, (B, P))
+    p = mn.Type1PlanND(tuple(x), N, eps=1e-5, isign=+1)
+    fb = p.execute_batch(cs)
+    for b in range(B):
+        fl = p.execute(cs[b])
+        assert np.linalg.norm(fb[b] - fl) / np.linalg.norm(fl) < 1e-5
+
+
+@pytest.mark.parametrize("dim,N", [(2, (256, 256)), (3, (64, 64, 48))])
+def test_set_sources_equals_fresh(dim, N, mn):
+    """ref gate (harness/test_type1_batch.py:83): re-point == fresh < 1e-5,
+    including a change of P."""
+    print(f"case set_sources dim={dim}", flush=True)
+    rng = np.random.default_rng(13)
+    P = 50_000
+    x1, x2 = _pts(rng, dim, P), _pts(rng, dim, P)
+    c = _cplx(rng, P)
+    p = mn.Type1PlanND(tuple(x1), N, eps=1e-5)
+    for backend in ("host", "gpu"):
+        p.set_sources(x2, backend=backend)
+        f_rp = p.execute(c)
+        f_fr = mn.Type1PlanND(tuple(x2), N, eps=1e-5).execute(c)
+        assert np.linalg.norm(f_rp - f_fr) / np.linalg.norm(f_fr) < 1e-5
+    x3 = _pts(rng, dim, P // 3)
+    c3 = _cplx(rng, P // 3)
+    p.set_sources(x3, backend="gpu")
+    assert p.P == P // 3
+    f3 = p.execute(c3)
+    f3f = mn.Type1PlanND(tuple(x3), N, eps=1e-5).execute(c3)
+    assert np.linalg.norm(f3 - f3f) / np.linalg.norm(f3f) < 1e-5
+    with pytest.raises(ValueError):
+        p.set_sources(x3, backend="cuda")
+
+
+@pytest.mark.parametrize("dim,N", [(1, (90,)), (2, (40, 36)), (3, (24, 20, 16))])
+def test_adjoint_identity(dim, N, mn):
+    """<T1 c, f> == <c, T2 f> with T2 at the negated sign (ref:
+    harness/test_types12.py:40-48); holds to the fp32 floor plus eps."""
+    print(f"case adjoint dim={dim}", flush=True)
+    rng = np.random.default_rng(14)
+    M = 20_000
+    x = _pts(rng, dim, M)
+    c = _cplx(rng, M)
+    f = _cplx(rng, N)
+    t1 = mn.Type1PlanND(tuple(x), N, eps=1e-6, isign=+1).execute(c)
+    t2 = mn.Type2PlanND(tuple(x), N, eps=1e-6, isign=-1).execute(f)
+    lhs = np.vdot(f.astype(np.complex128), t1.astype(np.complex128))
+    rhs = np.vdot(t2.astype(np.complex128), c.astype(np.complex128))
+    scale = np.linalg.norm(t1) * np.linalg.norm(f)
+    assert abs(lhs - rhs) / scale < 1e-5
