@@ -1,0 +1,184 @@
+"""Benchmark of the north-star workload on one MI355X.
+
+Workload (the metric's config): 3D type-1,
+M = 2e7 fp64 coordinates uniform in [-pi, pi)^3, complex64 strengths with
+re/im i.i.d. N(0,1) (numpy default_rng(0)), N = 256^3 modes, eps = 1e-5,
+isign = +1, upsampfac 2 (w = 6, fine grid 512^3).
+
+A step is one end-to-end pass with inputs already resident in HBM:
+set_sources (fp64 fold/rescale, stable bin sort, subproblem table) +
+execute (zero grid, spread, 512^3 FFT, crop/deconvolve). W untimed warmup
+steps, then K steps between torch.cuda.synchronize() calls.
+
+One JSON line is printed:
+  value      = M / (ms_per_step) in NU pts/s (end to end, device-resident)
+  roofline   = the spread kernel (the metric's "spread HBM GB/s"): algorithmic
+               bytes M*(8 + 8*3 + 4) + 8*512^3 per launch over its mean
+               HIP-event duration in the timed steps, against 8 TB/s
+  cpu_baseline = the same type-1 on the host cores (fp32 OpenMP spread +
+               scipy.fft, the oracle's port; finufft is not installed)
+"""
+
+import argparse
+import json
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "NU pts/s end-to-end + spread HBM GB/s, 3D type-1 M=2e7 N=256^3 eps=1e-5"
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--M", type=float, default=2e7)
+    ap.add_argument("--N", type=int, default=256)
+    ap.add_argument("--eps", type=float, default=1e-5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--exec-only", action="store_true",
+                    help="time execute() only (plan built once), for profiling")
+    return ap.parse_args()
+
+
+def cpu_baseline(x, c, N, eps):
+    """The oracle's fp32 OpenMP type-1 port on the full workload, timed once
+    after a small warm-up call (about 3-10 s of host work)."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    small = [v[:200_000] for v in x]
+    O.cpu_type1_f32(small, c[:200_000], (64, 64, 64), eps, workers=threads)
+    t0 = time.perf_counter()
+    _, parts = O.cpu_type1_f32(x, c, N, eps, workers=threads)
+    dt = time.perf_counter() - t0
+    M = x[0].size
+    return {"value": M / dt, "unit": "NU pts/s", "cores": threads, "kind": "port",
+            "sample": (f"full workload once (M={M:.0e}, N={N[0]}^3, eps={eps:g}, fp32 OpenMP "
+                       f"spread + scipy.fft workers={threads}); {dt:.2f} s"),
+            "seconds": {k: round(v, 4) for k, v in parts.items()}}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
+              "multi-GPU sharding is design-only (see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    import mlx_nufft_amd as mn
+    from mlx_nufft_amd import _lib
+
+    _lib.require_gpu()
+    M, N, eps = int(args.M), (args.N,) * 3, args.eps
+    rng = np.random.default_rng(0)
+    x = [rng.uniform(-np.pi, np.pi, M) for _ in range(3)]
+    c = (rng.standard_normal(M) + 1j * rng.standard_normal(M)).astype(np.complex64)
+    dev = torch.device("cuda")
+    xd = [torch.from_numpy(v).to(dev) for v in x]
+    cd = torch.from_numpy(c).to(dev)
+
+    plan = mn.Type1PlanND(tuple(xd), N, eps=eps, isign=+1)
+    n_up = plan.n_up
+    grid_cells = int(np.prod(n_up))
+
+    def step():
+        if not args.exec_only:
+            plan.set_sources(tuple(xd))
+        plan.execute(cd, return_np=False)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    plan.profile = True
+    stage_sum = {}
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+        prof = dict(plan.last_profile)
+        if not args.exec_only:
+            prof.update(plan.last_setpts_profile)
+        for k, v in prof.items():
+            stage_sum[k] = stage_sum.get(k, 0.0) + v
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    plan.profile = False
+    ms = (t1 - t0) * 1e3 / args.steps
+    stages = {k: v / args.steps for k, v in stage_sum.items()}
+
+    spread_ms = stages.get("spread", float("nan"))
+    alg_bytes = M * (8 + 8 * 3 + 4) + 8 * grid_cells
+    achieved = alg_bytes / (spread_ms * 1e-3) / 1e9
+    traffic = None
+    tf = ROOT / "profiles" / "spread_3d_t1_traffic.json"
+    if tf.exists():
+        try:
+            traffic = json.loads(tf.read_text()).get("bytes_per_launch")
+        except (ValueError, OSError):
+            traffic = None
+    exec_ms = sum(stages.get(k, 0.0) for k in ("zero", "spread", "fft", "deconv"))
+
+    # type-2 leg of the round trip: interp back at the
+    # same points from the type-1 output, timed the same way (not in `value`).
+    fk = plan.execute(cd, return_np=False)
+    plan_w, plan_bins = plan.w, [plan.bins.m[d] for d in range(3)]
+    del plan
+    p2 = mn.Type2PlanND(tuple(xd), N, eps=eps, isign=-1)
+    for _ in range(max(1, args.warmup)):
+        p2.execute(fk, return_np=False)
+    p2.profile = True
+    t2_stages = {}
+    reps = max(3, args.steps // 4)
+    for _ in range(reps):
+        p2.execute(fk, return_np=False)
+        for k, v in p2.last_profile.items():
+            t2_stages[k] = t2_stages.get(k, 0.0) + v / reps
+    interp_ms = t2_stages.get("interp", float("nan"))
+    interp_gbs = alg_bytes / (interp_ms * 1e-3) / 1e9
+    del p2
+    out = {
+        "metric": METRIC,
+        "value": M / (ms * 1e-3),
+        "unit": "NU pts/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: numpy default_rng(0) uniform coords, N(0,1) complex64 strengths",
+        "config": {"workload": "3D type-1 M=2e7 N=256^3 eps=1e-5 (BASELINE.json configs[3])",
+                   "M": M, "N": list(N), "eps": eps, "isign": 1, "w": plan_w,
+                   "n_up": list(n_up), "bins": plan_bins,
+                   "step": ("execute only" if args.exec_only else
+                            "set_sources + execute, device-resident")},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                     "kernel": "k_spread_tiled<3,6>", "alg_bytes_per_launch": alg_bytes,
+                     "ms_per_launch": spread_ms},
+        "stages_ms": {k: round(v, 4) for k, v in stages.items()},
+        "exec_ms": exec_ms,
+        "exec_pts_per_s": M / (exec_ms * 1e-3) if exec_ms else None,
+        "type2_roundtrip": {"stages_ms": {k: round(v, 4) for k, v in t2_stages.items()},
+                            "interp_GBs": interp_gbs, "interp_frac": interp_gbs / HBM_PEAK_GBS},
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(x, c, N, eps)
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

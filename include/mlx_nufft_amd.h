@@ -57,6 +57,9 @@ typedef struct mn_bins {
 const char *mn_last_error(void);
 /* ABI version (major*10000 + minor*100 + patch). */
 int mn_version(void);
+/* LDS bytes one workgroup may use on the current device (bounds the bin
+ * tile: 8 * prod_d (m[d] + w - 1) bytes for spread and interp). */
+int mn_device_lds_bytes(void);
 
 /*
  * Type-1/2 point setup ("crit64"): per point and dim, r = x mod 2pi with
@@ -124,6 +127,18 @@ int mn_spread(const mn_bins *g, float beta, int64_t P, int64_t nsub,
               const int32_t *sub_info, const uint32_t *perm,
               const int32_t *const i1s[3], const float *const frs[3],
               const void *c, const void *pre, void *grid, mn_stream_t stream);
+
+/*
+ * As mn_spread, but adds into the existing grid contents (no zero-fill):
+ * lets a caller accumulate several point sets into one grid, or zero the
+ * grid itself (mn_fill_zero) and time the spread kernel on its own.
+ * ref: nd.py:590-601 (spread launch with init_value=0 split in two).
+ */
+int mn_spread_accumulate(const mn_bins *g, float beta, int64_t P, int64_t nsub,
+                         const int32_t *sub_info, const uint32_t *perm,
+                         const int32_t *const i1s[3], const float *const frs[3],
+                         const void *c, const void *pre, void *grid,
+                         mn_stream_t stream);
 
 /*
  * Batched spread: B strength vectors cs (B x P, caller order, row-major)

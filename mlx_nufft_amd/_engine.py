@@ -20,10 +20,30 @@ MSUB = 1024                 # max points per spread/interp subproblem
 TILE_BUDGET = 80 * 1024     # LDS bytes for one padded tile (2 workgroups/CU)
 
 
-def bin_sizes(dim, w, n_up):
+_budget = None
+
+
+def tile_budget():
+    """LDS bytes for one tile: TILE_BUDGET, capped by the device limit."""
+    global _budget
+    if _budget is None:
+        try:
+            dev = int(L.lib().mn_device_lds_bytes())
+        except RuntimeError:
+            dev = TILE_BUDGET
+        _budget = min(TILE_BUDGET, dev if dev > 0 else 65536)
+    return _budget
+
+
+SPREAD_CELL_BYTES = 16   # spread tiles accumulate complex values in fp64
+INTERP_CELL_BYTES = 8    # interp tiles hold complex64 grid values
+
+
+def bin_sizes(dim, w, n_up, cell_bytes=SPREAD_CELL_BYTES):
     """Bin size m per dim: the padded tile (m + w - 1 cells per dim,
-    complex64) must fit TILE_BUDGET bytes of LDS. Overridable with the
-    environment variable MN_BIN_M="m0,m1,m2" (tuning)."""
+    cell_bytes each) must fit tile_budget() bytes of LDS. Overridable with
+    the environment variable MN_BIN_M="m0,m1,m2" (tuning)."""
+    budget = tile_budget()
     env = os.environ.get("MN_BIN_M")
     if env:
         m = [int(v) for v in env.split(",")]
@@ -33,19 +53,21 @@ def bin_sizes(dim, w, n_up):
     elif dim == 2:
         m = [32, 32]
     else:
-        side = int(round((TILE_BUDGET / 8) ** (1.0 / 3.0) - 1e-9))
-        while 8 * side ** 3 > TILE_BUDGET:
+        side = int(round((budget / cell_bytes) ** (1.0 / 3.0) - 1e-9))
+        while cell_bytes * side ** 3 > budget:
             side -= 1
         m = [max(1, side - w + 1)] * 3
     m = [max(1, min(int(mi), int(n))) for mi, n in zip(m, n_up)]
-    while 8 * int(np.prod([mi + w - 1 for mi in m])) > TILE_BUDGET and max(m) > 1:
+    while cell_bytes * int(np.prod([mi + w - 1 for mi in m])) > budget and max(m) > 1:
         k = int(np.argmax(m))
         m[k] -= 1
     return m
 
 
-def make_bins(dim, w, n_up, m=None):
-    return L.Bins.make(dim, w, list(n_up), m if m is not None else bin_sizes(dim, w, n_up))
+def make_bins(dim, w, n_up, m=None, cell_bytes=SPREAD_CELL_BYTES):
+    if m is None:
+        m = bin_sizes(dim, w, n_up, cell_bytes)
+    return L.Bins.make(dim, w, list(n_up), m)
 
 
 def key_bits(bins):
@@ -126,11 +148,17 @@ class SortedPoints:
         return _rows(self.frs, self.bins.dim)
 
 
-def spread(pts, beta, c, grid, pre=None):
-    L.check(L.lib().mn_spread(ctypes.byref(pts.bins), float(beta), pts.P, pts.nsub,
-                              L.ptr(pts.info), L.ptr(pts.perm), L.ptr3(pts.i1_rows()),
-                              L.ptr3(pts.fr_rows()), L.ptr(c), L.ptr(pre), L.ptr(grid),
-                              L.stream()), "spread")
+def fill_zero(t):
+    L.check(L.lib().mn_fill_zero(L.ptr(t), t.numel() * t.element_size(), L.stream()),
+            "fill_zero")
+
+
+def spread(pts, beta, c, grid, pre=None, accumulate=False):
+    """grid = spread(c) (or grid += spread(c) with accumulate=True)."""
+    fn = L.lib().mn_spread_accumulate if accumulate else L.lib().mn_spread
+    L.check(fn(ctypes.byref(pts.bins), float(beta), pts.P, pts.nsub, L.ptr(pts.info),
+               L.ptr(pts.perm), L.ptr3(pts.i1_rows()), L.ptr3(pts.fr_rows()), L.ptr(c),
+               L.ptr(pre), L.ptr(grid), L.stream()), "spread")
 
 
 def spread_batch(pts, beta, cs, grids):

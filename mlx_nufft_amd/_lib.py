@@ -52,6 +52,7 @@ class Bins(ctypes.Structure):
 _SIGS = [
     ("mn_last_error", ctypes.c_char_p, []),
     ("mn_version", c_int, []),
+    ("mn_device_lds_bytes", c_int, []),
     ("mn_setpts_t12", c_int, [ctypes.POINTER(Bins), c_int64, VP3, c_int, VP3, VP3, c_vp, c_vp]),
     ("mn_sort_workspace_bytes", c_int64, [c_int64]),
     ("mn_sort_keys", c_int, [c_int64, c_int, c_vp, c_vp, c_vp, c_vp, c_int64, c_vp]),
@@ -61,6 +62,8 @@ _SIGS = [
                                      c_int64, ctypes.POINTER(c_int64), c_vp, c_int64, c_vp]),
     ("mn_spread", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int64, c_vp, c_vp, VP3, VP3,
                           c_vp, c_vp, c_vp, c_vp]),
+    ("mn_spread_accumulate", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int64, c_vp, c_vp,
+                                     VP3, VP3, c_vp, c_vp, c_vp, c_vp]),
     ("mn_spread_batch", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int64, c_vp, c_vp, VP3,
                                 VP3, c_int64, c_vp, c_vp, c_vp]),
     ("mn_interp", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int64, c_vp, c_vp, VP3, VP3,

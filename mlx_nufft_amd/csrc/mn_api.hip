@@ -18,6 +18,8 @@ int check_bins(const mn_bins *g) {
     int64_t total = 1;
     for (int d = 0; d < g->dim; ++d) {
         MN_REQUIRE(g->n[d] >= 1 && g->n[d] < (int64_t(1) << 30), "grid size out of range");
+        // tile wrap arithmetic covers [-n, 3n), which needs n >= w
+        MN_REQUIRE(g->n[d] >= g->w, "grid size must be >= the kernel width w");
         MN_REQUIRE(g->m[d] >= 1 && g->m[d] <= g->n[d], "bin size must be in [1, n]");
         MN_REQUIRE(g->nb[d] == (g->n[d] + g->m[d] - 1) / g->m[d], "nb must equal ceil(n/m)");
         total *= g->nb[d];
@@ -85,6 +87,11 @@ extern "C" {
 const char *mn_last_error(void) { return mn::g_last_error.c_str(); }
 
 int mn_version(void) { return 100; }
+
+int mn_device_lds_bytes(void) {
+    mn::clear_error();
+    return mn::max_lds_per_block();
+}
 
 int mn_fill_zero(void *ptr, int64_t bytes, mn_stream_t stream) {
     mn::clear_error();

@@ -2,12 +2,15 @@
 //
 // One 256-thread workgroup per subproblem (<= msub bin-sorted points of one
 // bin). The padded tile of the bin (m + w - 1 cells per dim) lives in LDS as
-// two fp32 planes (re, im). Each lane takes one point at a time: it gathers
+// two fp64 planes (re, im). Each lane takes one point at a time: it gathers
 // the strength c[perm[j]] (caller order; optionally times the type-3
 // prephase), evaluates the w ES weights per dim once, and adds the w^dim
-// taps into LDS with ds_add_f32. After a barrier the tile is flushed to the
-// periodic fine grid with fp32 global atomics (skipping cells that stayed
-// zero). Workgroups are remapped so each XCD walks a contiguous run of bins.
+// taps into LDS with ds_add_f64. On CDNA4 fp32 LDS atomics retire about one
+// lane every two clocks per CU, several times slower than fp64 ones, and the
+// fp64 tile also sums more accurately. After a barrier the tile is flushed
+// to the periodic fine grid with fp32 global atomics (skipping cells that
+// stayed zero). Workgroups are remapped so each XCD walks a contiguous run
+// of bins.
 // ref: nd.py:492-579 (OD spread), nd.py:683-742 (batched), gpu_t3.py:565-591.
 #include "mn_common.h"
 
@@ -53,7 +56,7 @@ __global__ __launch_bounds__(256) void k_spread_tiled(Geom g, float bl2e, float 
                                                       const float2 *__restrict__ pre,
                                                       float2 *__restrict__ grid, int64_t P,
                                                       int64_t b0, int bc) {
-    extern __shared__ float lds[];
+    extern __shared__ double lds[];
     const int p1 = g.p[1], p2 = g.p[2];
     const int T = g.p[0] * p1 * p2;
     const int64_t sub = xcd_remap(blockIdx.x, nsub);
@@ -68,7 +71,7 @@ __global__ __launch_bounds__(256) void k_spread_tiled(Geom g, float bl2e, float 
         }
     }
     const int nvec = BATCH ? bc : 1;
-    for (int q = threadIdx.x; q < 2 * T * nvec; q += 256) lds[q] = 0.0f;
+    for (int q = threadIdx.x; q < 2 * T * nvec; q += 256) lds[q] = 0.0;
     __syncthreads();
 
     for (int t = threadIdx.x; t < cnt; t += 256) {
@@ -92,14 +95,14 @@ __global__ __launch_bounds__(256) void k_spread_tiled(Geom g, float bl2e, float 
             float2 cv = BATCH ? c[(b0 + v) * P + src] : c[src];
             if (!BATCH && pre)
                 cv = make_float2(cv.x * pv.x - cv.y * pv.y, cv.x * pv.y + cv.y * pv.x);
-            float *tre = lds + (size_t)2 * T * v;
-            float *tim = tre + T;
+            double *tre = lds + (size_t)2 * T * v;
+            double *tim = tre + T;
             if constexpr (DIM == 1) {
 #pragma unroll
                 for (int a0 = 0; a0 < W; ++a0) {
                     const int idx = loc[0] + a0;
-                    atomicAdd(&tre[idx], cv.x * wt[0][a0]);
-                    atomicAdd(&tim[idx], cv.y * wt[0][a0]);
+                    atomicAdd(&tre[idx], (double)(cv.x * wt[0][a0]));
+                    atomicAdd(&tim[idx], (double)(cv.y * wt[0][a0]));
                 }
             } else if constexpr (DIM == 2) {
 #pragma unroll
@@ -108,8 +111,8 @@ __global__ __launch_bounds__(256) void k_spread_tiled(Geom g, float bl2e, float 
                     const int base = (loc[0] + a0) * p1 + loc[1];
 #pragma unroll
                     for (int a1 = 0; a1 < W; ++a1) {
-                        atomicAdd(&tre[base + a1], r * wt[1][a1]);
-                        atomicAdd(&tim[base + a1], i * wt[1][a1]);
+                        atomicAdd(&tre[base + a1], (double)(r * wt[1][a1]));
+                        atomicAdd(&tim[base + a1], (double)(i * wt[1][a1]));
                     }
                 }
             } else {
@@ -122,8 +125,8 @@ __global__ __launch_bounds__(256) void k_spread_tiled(Geom g, float bl2e, float 
                         const int base = ((loc[0] + a0) * p1 + loc[1] + a1) * p2 + loc[2];
 #pragma unroll
                         for (int a2 = 0; a2 < W; ++a2) {
-                            atomicAdd(&tre[base + a2], r * wt[2][a2]);
-                            atomicAdd(&tim[base + a2], i * wt[2][a2]);
+                            atomicAdd(&tre[base + a2], (double)(r * wt[2][a2]));
+                            atomicAdd(&tim[base + a2], (double)(i * wt[2][a2]));
                         }
                     }
                 }
@@ -144,8 +147,8 @@ __global__ __launch_bounds__(256) void k_spread_tiled(Geom g, float bl2e, float 
         const int g2 = DIM >= 3 ? wrap_tile(o2 + q2, g.n[2]) : 0;
         const int64_t cell = ((int64_t)g0 * g.n[1] + g1) * g.n[2] + g2;
         for (int v = 0; v < nvec; ++v) {
-            const float *tre = lds + (size_t)2 * T * v;
-            const float re = tre[q], im = tre[T + q];
+            const double *tre = lds + (size_t)2 * T * v;
+            const float re = (float)tre[q], im = (float)tre[T + q];
             if (re == 0.0f && im == 0.0f) continue;
             float *dst = reinterpret_cast<float *>(grid + (BATCH ? (b0 + v) * gsz : 0) + cell);
             unsafeAtomicAdd(dst, re);
@@ -162,7 +165,7 @@ struct SpreadLaunch {
         const float inv_hw = (float)(2.0 / W);
         const int64_t T = tile_cells(a.g);
         const bool batch = a.bc > 1 || a.b0 > 0;
-        const size_t lds = (size_t)2 * T * sizeof(float) * (batch ? a.bc : 1);
+        const size_t lds = (size_t)2 * T * sizeof(double) * (batch ? a.bc : 1);
         if (lds > (size_t)max_lds_per_block()) {
             set_error("spread: tile does not fit in LDS; use smaller bins");
             return MN_EINVAL;
@@ -185,11 +188,11 @@ struct SpreadLaunch {
 
 using namespace mn;
 
-extern "C" {
 
-int mn_spread(const mn_bins *g, float beta, int64_t P, int64_t nsub, const int32_t *sub_info,
-              const uint32_t *perm, const int32_t *const i1s[3], const float *const frs[3],
-              const void *c, const void *pre, void *grid, mn_stream_t stream) {
+static int spread_impl(const mn_bins *g, float beta, int64_t P, int64_t nsub,
+                       const int32_t *sub_info, const uint32_t *perm,
+                       const int32_t *const i1s[3], const float *const frs[3], const void *c,
+                       const void *pre, void *grid, bool zero, mn_stream_t stream) {
     clear_error();
     int rc = check_bins(g);
     if (rc) return rc;
@@ -211,9 +214,26 @@ int mn_spread(const mn_bins *g, float beta, int64_t P, int64_t nsub, const int32
     a.b0 = 0;
     a.bc = 1;
     a.s = as_stream(stream);
-    rc = fill_zero(grid, gsz * 8, a.s);
-    if (rc) return rc;
+    if (zero) {
+        rc = fill_zero(grid, gsz * 8, a.s);
+        if (rc) return rc;
+    }
     return select_dim_w<SpreadLaunch>(g->dim, g->w, a);
+}
+
+extern "C" {
+
+int mn_spread(const mn_bins *g, float beta, int64_t P, int64_t nsub, const int32_t *sub_info,
+              const uint32_t *perm, const int32_t *const i1s[3], const float *const frs[3],
+              const void *c, const void *pre, void *grid, mn_stream_t stream) {
+    return spread_impl(g, beta, P, nsub, sub_info, perm, i1s, frs, c, pre, grid, true, stream);
+}
+
+int mn_spread_accumulate(const mn_bins *g, float beta, int64_t P, int64_t nsub,
+                         const int32_t *sub_info, const uint32_t *perm,
+                         const int32_t *const i1s[3], const float *const frs[3], const void *c,
+                         const void *pre, void *grid, mn_stream_t stream) {
+    return spread_impl(g, beta, P, nsub, sub_info, perm, i1s, frs, c, pre, grid, false, stream);
 }
 
 int mn_spread_batch(const mn_bins *g, float beta, int64_t P, int64_t nsub,
@@ -242,9 +262,10 @@ int mn_spread_batch(const mn_bins *g, float beta, int64_t P, int64_t nsub,
     a.s = as_stream(stream);
     rc = fill_zero(grids, B * gsz * 8, a.s);
     if (rc) return rc;
-    // Vectors per launch: as many tiles as fit in 64 KB of LDS (at least 1).
-    const int64_t tile_bytes = 8 * tile_cells(g);
-    int64_t per = 65536 / tile_bytes;
+    // Vectors per launch: as many fp64 tiles as fit in half of the LDS
+    // (two workgroups per CU), at least one.
+    const int64_t tile_bytes = 16 * tile_cells(g);
+    int64_t per = (max_lds_per_block() / 2) / tile_bytes;
     if (per < 1) per = 1;
     if (per > B) per = B;
     for (int64_t v0 = 0; v0 < B; v0 += per) {

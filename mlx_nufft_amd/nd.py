@@ -65,7 +65,7 @@ class _PointsND:
         self.device = L.require_gpu()
         x64 = self._coords(x)
         self.P = x64[0].numel()
-        self.bins = E.make_bins(self.dim, self.w, self.n_up)
+        self.bins = E.make_bins(self.dim, self.w, self.n_up, cell_bytes=self._cell_bytes)
         self._set_points(x64)
 
         # Mode deconvolution 1/phihat(2 pi k / n_up) on the uncentred fine grid
@@ -105,10 +105,15 @@ class _PointsND:
         self.fr = [v.cpu().numpy() for v in fr]
 
     def _set_points(self, x64):
-        i1, fr, key = E.setpts_t12(self.bins, x64, self.prec == "crit64")
-        self.pts = E.SortedPoints(self.bins, i1, fr, key)
+        tm = self._timer()
+        with tm("setpts"):
+            i1, fr, key = E.setpts_t12(self.bins, x64, self.prec == "crit64")
+        with tm("sort+tables"):
+            self.pts = E.SortedPoints(self.bins, i1, fr, key)
         self.sorted = True
         self._od = True
+        self._finish_profile(tm)
+        self.last_setpts_profile = dict(self.last_profile) if self.profile else {}
 
     @property
     def mx_perm(self):
@@ -140,6 +145,8 @@ class Type1PlanND(_PointsND):
     ref: nd.py:386-855.
     """
 
+    _cell_bytes = E.SPREAD_CELL_BYTES
+
     def __init__(self, x, n_modes, eps=1e-6, isign=+1, upsampfac=2.0, prec="crit64",
                  sort_points=True, spread_method="auto"):
         assert spread_method in ("auto", "od", "gm")
@@ -159,8 +166,10 @@ class Type1PlanND(_PointsND):
         grid = self._fine_grid(1)
         fk = torch.empty(self.N, dtype=torch.complex64, device=self.device)
         tm = self._timer()
+        with tm("zero"):
+            E.fill_zero(grid)
         with tm("spread"):
-            E.spread(self.pts, self.beta, cd, grid)
+            E.spread(self.pts, self.beta, cd, grid, accumulate=True)
         with tm("fft"):
             E.fft(grid, self.n_up, self.isign)
         with tm("deconv"):
@@ -235,6 +244,8 @@ class Type2PlanND(_PointsND):
 
     ref: nd.py:858-1119.
     """
+
+    _cell_bytes = E.INTERP_CELL_BYTES
 
     def __init__(self, x, n_modes, eps=1e-6, isign=-1, upsampfac=2.0, prec="crit64",
                  sort_points=False, spread_method="auto"):

@@ -101,7 +101,7 @@ class GpuT3Plan:
         self.slab_mode = False
 
         # ---- targets: rescale, post factor, bin sort (device fp64) ----------
-        self.bins_trg = E.make_bins(3, self.w2, self.n_up)
+        self.bins_trg = E.make_bins(3, self.w2, self.n_up, cell_bytes=E.INTERP_CELL_BYTES)
         hd = [2.0 * PI / nf for nf in self.nf]
         hg = [hd[d] * self.gam[d] for d in range(3)]
         h2 = [2.0 * PI / n for n in self.n_up]
@@ -129,7 +129,7 @@ class GpuT3Plan:
             self.decs.append(((-1.0) ** np.abs(q)) / ph)
         self.dev_dec = [torch.from_numpy(v.astype(np.float32)).to(self.device)
                         for v in self.decs]
-        self.bins_src = E.make_bins(3, self.w, self.nf)
+        self.bins_src = E.make_bins(3, self.w, self.nf, cell_bytes=E.SPREAD_CELL_BYTES)
         self._hd = hd
         self._bf = None
         self._H = None

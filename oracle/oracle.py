@@ -250,8 +250,25 @@ def nufft_t2(x, f, eps, isign=-1, upsampfac=2.0):
     return interp(i1, fr, _fftn(H, isign), w, beta)
 
 
-def nufft_t3(x, c, s, eps=1e-5, isign=+1, upsampfac=1.25):
-    """fp64 CPU type-3 (3D), following ref_t3.py:48-221 with all stages fp64."""
+def spread_f32(i1, fr, c, n, w, beta):
+    """Spread with fp32 kernel evaluation and fp32 accumulation (the
+    reference's spread64=False stage flag, ref_t3.py:168, 300-317)."""
+    dim, P = i1.shape
+    grid = np.empty(tuple(n), np.complex64)
+    c32 = np.ascontiguousarray(np.asarray(c, np.complex64).ravel())
+    nn = np.asarray(list(n) + [1] * (3 - dim), np.int64)
+    i1c = [np.ascontiguousarray(i1[d]) for d in range(dim)]
+    frc = [np.ascontiguousarray(fr[d]) for d in range(dim)]
+    if lib().or_spread_f32(dim, P, _pa(i1c), _pa(frc), _p(c32), _p(nn), int(w), float(beta),
+                           int(w), _p(grid)):
+        raise MemoryError("or_spread_f32 failed")
+    return grid.astype(np.complex128)
+
+
+def nufft_t3(x, c, s, eps=1e-5, isign=+1, upsampfac=1.25, spread64=True):
+    """CPU type-3 (3D), following ref_t3.py:48-221: all stages fp64, or with
+    the spread stage in fp32 (spread64=False, the reference's most
+    precision-sensitive fp32 stage, ref: harness/diagnose_ref.py:21-41)."""
     w, beta = kernel_params(eps, upsampfac)
     x = [np.asarray(v, np.float64).ravel() for v in x]
     s = [np.asarray(v, np.float64).ravel() for v in s]
@@ -272,7 +289,8 @@ def nufft_t3(x, c, s, eps=1e-5, isign=+1, upsampfac=1.25):
         i1[d] = np.ceil(xi - w / 2.0).astype(np.int32)
         fr[d] = (xi - i1[d]).astype(np.float32)
     pre = np.exp(1j * isign * (D[0] * x[0] + D[1] * x[1] + D[2] * x[2]))
-    b = spread(i1, fr, np.asarray(c, np.complex128) * pre, nf, w, beta)
+    b = (spread if spread64 else spread_f32)(i1, fr, np.asarray(c, np.complex128) * pre, nf, w,
+                                             beta)
     decs = []
     for d in range(3):
         q = np.arange(-nf[d] // 2, nf[d] // 2, dtype=np.float64)
