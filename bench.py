@@ -133,6 +133,8 @@ def main():
     # same points from the type-1 output, timed the same way (not in `value`).
     fk = plan.execute(cd, return_np=False)
     plan_w, plan_bins = plan.w, [plan.bins.m[d] for d in range(3)]
+    zsweep = plan.pts.kind == "zsweep"
+    spread_kernel = f"k_spread_zsweep<{plan_w}>" if zsweep else f"k_spread_tiled<3,{plan_w},false>"
     del plan
     p2 = mn.Type2PlanND(tuple(xd), N, eps=eps, isign=-1)
     for _ in range(max(1, args.warmup)):
@@ -162,12 +164,13 @@ def main():
         "data": "synthetic: numpy default_rng(0) uniform coords, N(0,1) complex64 strengths",
         "config": {"workload": "3D type-1 M=2e7 N=256^3 eps=1e-5 (BASELINE.json configs[3])",
                    "M": M, "N": list(N), "eps": eps, "isign": 1, "w": plan_w,
-                   "n_up": list(n_up), "bins": plan_bins,
+                   "n_up": list(n_up),
+                   "spread": ("z-sweep, 8x8 column blocks" if zsweep else f"LDS tiles {plan_bins}"),
                    "step": ("execute only" if args.exec_only else
                             "set_sources + execute, device-resident")},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "kernel": "k_spread_tiled<3,6>", "alg_bytes_per_launch": alg_bytes,
+                     "kernel": spread_kernel, "alg_bytes_per_launch": alg_bytes,
                      "ms_per_launch": spread_ms},
         "stages_ms": {k: round(v, 4) for k, v in stages.items()},
         "exec_ms": exec_ms,

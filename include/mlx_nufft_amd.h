@@ -141,6 +141,31 @@ int mn_spread_accumulate(const mn_bins *g, float beta, int64_t P, int64_t nsub,
                          mn_stream_t stream);
 
 /*
+ * Owner-computes 3D spread ("z-sweep"), the fast path for 3D type-1 grids
+ * with n0, n1 multiples of 8 (>= 16) and w <= 8. Each wavefront owns an
+ * 8x8 (x, y) column block over a z-segment of zseg cells, sweeps z with a
+ * w-cell window per column in registers and stores every grid cell exactly
+ * once (no atomics; grid is fully overwritten). Points must be sorted by the
+ * z-sweep key (mn_zsweep_keys) and located through zstart
+ * (mn_zsweep_starts, mn_zsweep_nkeys() + 1 int32). g: dim 3, w, n (m and
+ * nb are not used). pre: optional sorted-order strength multiplier.
+ * key = ((bx*(n1/8) + by)*n2 + z)*4 + classpos with (bx, by, z) the block
+ * and z of the first tap and classpos in [00, 01, 11, 10] order of whether
+ * the footprint reaches the next block in x and in y.
+ * ref: nd.py:492-579 (output-driven spread), nd.py:298-372 (bin sort).
+ */
+int mn_zsweep_keys(const mn_bins *g, int64_t P, const int32_t *const i1[3], uint32_t *key,
+                   mn_stream_t stream);
+int64_t mn_zsweep_nkeys(const mn_bins *g);
+int64_t mn_zsweep_starts_workspace_bytes(const mn_bins *g);
+int mn_zsweep_starts(const mn_bins *g, int64_t P, const uint32_t *sorted_key, int32_t *zstart,
+                     void *ws, int64_t ws_bytes, mn_stream_t stream);
+int mn_spread_zsweep(const mn_bins *g, float beta, int64_t P, int zseg, const int32_t *zstart,
+                     const uint32_t *perm, const int32_t *const i1s[3],
+                     const float *const frs[3], const void *c, const void *pre, void *grid,
+                     mn_stream_t stream);
+
+/*
  * Batched spread: B strength vectors cs (B x P, caller order, row-major)
  * over the same points into B grids (B x prod n, overwritten); the ES
  * weights are computed once per point and applied to every vector.

@@ -133,6 +133,8 @@ def build_subproblems(bins, skey, msub=MSUB):
 class SortedPoints:
     """Bin-sorted point state of one point set on one fine grid."""
 
+    kind = "tiles"
+
     def __init__(self, bins, i1, fr, key, extra=None, msub=MSUB):
         self.bins = bins
         self.P = i1.shape[1]
@@ -151,6 +153,57 @@ class SortedPoints:
 def fill_zero(t):
     L.check(L.lib().mn_fill_zero(L.ptr(t), t.numel() * t.element_size(), L.stream()),
             "fill_zero")
+
+
+ZSEG = 128  # z-segment (cells) owned by one z-sweep wavefront
+
+
+def zsweep_eligible(dim, w, n_up):
+    """True when the owner-computes z-sweep spread applies: 3D, w <= 8 and
+    the x and y fine-grid sizes multiples of 8 (>= 16). MN_SPREAD=tiles
+    forces the LDS-tile spread instead."""
+    if os.environ.get("MN_SPREAD", "") == "tiles":
+        return False
+    return (dim == 3 and w <= 8 and all(n % 8 == 0 and n >= 16 for n in n_up[:2]))
+
+
+class ZSweepPoints:
+    """Point state for the z-sweep spread: z-sweep keys, stable sort,
+    sorted cells/fractions and the key start table."""
+
+    kind = "zsweep"
+
+    def __init__(self, bins, i1, fr):
+        lib = L.lib()
+        self.bins = bins
+        self.P = i1.shape[1]
+        key = torch.empty(self.P, dtype=torch.int32, device=i1.device)
+        L.check(lib.mn_zsweep_keys(ctypes.byref(bins), self.P, L.ptr3(_rows(i1, 3)), L.ptr(key),
+                                   L.stream()), "zsweep keys")
+        K = int(lib.mn_zsweep_nkeys(ctypes.byref(bins)))
+        self.skey, self.perm = sort_keys(key, max(1, (K - 1).bit_length()))
+        del key
+        self.i1s, self.frs, self.extra = gather_points(self.perm, i1, fr)
+        self.zstart = torch.empty(K + 1, dtype=torch.int32, device=i1.device)
+        ws = torch.empty(int(lib.mn_zsweep_starts_workspace_bytes(ctypes.byref(bins))),
+                         dtype=torch.uint8, device=i1.device)
+        L.check(lib.mn_zsweep_starts(ctypes.byref(bins), self.P, L.ptr(self.skey),
+                                     L.ptr(self.zstart), L.ptr(ws), ws.numel(), L.stream()),
+                "zsweep starts")
+
+    def i1_rows(self):
+        return _rows(self.i1s, 3)
+
+    def fr_rows(self):
+        return _rows(self.frs, 3)
+
+
+def spread_zsweep(pts, beta, c, grid, pre=None, zseg=ZSEG):
+    """grid = spread(c) with the owner-computes z-sweep (overwrites grid)."""
+    L.check(L.lib().mn_spread_zsweep(ctypes.byref(pts.bins), float(beta), pts.P, int(zseg),
+                                     L.ptr(pts.zstart), L.ptr(pts.perm), L.ptr3(pts.i1_rows()),
+                                     L.ptr3(pts.fr_rows()), L.ptr(c), L.ptr(pre), L.ptr(grid),
+                                     L.stream()), "spread_zsweep")
 
 
 def spread(pts, beta, c, grid, pre=None, accumulate=False):

@@ -64,6 +64,12 @@ _SIGS = [
                           c_vp, c_vp, c_vp, c_vp]),
     ("mn_spread_accumulate", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int64, c_vp, c_vp,
                                      VP3, VP3, c_vp, c_vp, c_vp, c_vp]),
+    ("mn_zsweep_keys", c_int, [ctypes.POINTER(Bins), c_int64, VP3, c_vp, c_vp]),
+    ("mn_zsweep_nkeys", c_int64, [ctypes.POINTER(Bins)]),
+    ("mn_zsweep_starts_workspace_bytes", c_int64, [ctypes.POINTER(Bins)]),
+    ("mn_zsweep_starts", c_int, [ctypes.POINTER(Bins), c_int64, c_vp, c_vp, c_vp, c_int64, c_vp]),
+    ("mn_spread_zsweep", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int, c_vp, c_vp, VP3,
+                                 VP3, c_vp, c_vp, c_vp, c_vp]),
     ("mn_spread_batch", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int64, c_vp, c_vp, VP3,
                                 VP3, c_int64, c_vp, c_vp, c_vp]),
     ("mn_interp", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int64, c_vp, c_vp, VP3, VP3,

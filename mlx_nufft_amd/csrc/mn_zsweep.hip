@@ -1,0 +1,355 @@
+// Owner-computes 3D spread ("z-sweep"): no atomics, every fine-grid cell is
+// written exactly once with a plain store.
+//
+// Layout. The grid is cut into 8x8 (x, y) column blocks. Each wavefront owns
+// one block over a z-segment; lane (lx, ly) owns column (8 bx + lx, 8 by + ly)
+// and keeps a W-cell complex window [z, z + W) of its column in VGPRs. The
+// wave sweeps z upwards: at each z it adds every point whose first tap is at
+// z and whose footprint touches the block, then cell z is complete and is
+// stored (staged in LDS so stores run along z), and the window shifts by one
+// cell -- all register indices are compile-time constants.
+//
+// Point order. Points are sorted by key ((bx*nby + by)*n2 + z)*4 + classpos,
+// where bx, by, z come from the first tap i1 and classpos encodes whether the
+// footprint reaches the next block in x (cx) and in y (cy), ordered
+// [00, 01, 11, 10]. Block b receives points from itself (all classes) and
+// from its -x, -y and -xy neighbours with the reaching classes; with that
+// order each of the four is one contiguous key range per z, located through
+// zstart[key] (exclusive prefix of key counts).
+//
+// Per batch of up to 64 points (two z-steps), a lane-per-point prologue
+// evaluates the ES weights once and writes a table row: the 8 x-weights of
+// the block's columns times the strength (complex), the 8 y-weights and the
+// W z-weights. The sweep then costs each point 2*W FMAs per lane.
+//
+// ref: nd.py:492-579 (the reference's output-driven spread this replaces),
+// nd.py:298-372 (its bin sort and subproblem tables).
+#include "mn_common.h"
+
+namespace mn {
+namespace {
+
+constexpr int ZB = 8;      // block size along x and y (lanes: 8 x 8)
+constexpr int ZST = 4;     // z-slices staged in LDS per store
+constexpr int ZCH = 2;     // z-steps per prologue batch
+constexpr int UNR = 4;     // points per unrolled sweep step
+constexpr int NR = 4;      // key ranges per z: own, -x, -y, -xy
+constexpr int REC = 32;    // floats per table row
+
+__device__ __forceinline__ int rel_offset(int i, int n, int base) {
+    int o = pmod(i, n) - base;
+    if (o > n / 2) o -= n;
+    if (o < -n / 2) o += n;
+    return o;
+}
+
+template <int W>
+__device__ __forceinline__ void store_stage(float2 (*stage)[64], float2 *__restrict__ grid,
+                                            int lane, int s, int zw, int n1, int n2, int bx,
+                                            int by, float wr, float wi, bool last) {
+    stage[s][lane] = make_float2(wr, wi);
+    if (s == ZST - 1 || last) {
+        __syncthreads();
+        const int zb = zw - s, nz = s + 1;
+        for (int colb = 0; colb < 64; colb += 16) {
+            const int col = colb + (lane >> 2), zo = lane & 3;
+            if (zo < nz) {
+                const int gx = ZB * bx + (col >> 3), gy = ZB * by + (col & 7);
+                grid[((int64_t)gx * n1 + gy) * n2 + zb + zo] = stage[zo][col];
+            }
+        }
+        __syncthreads();
+    }
+}
+
+template <int W>
+__global__ __launch_bounds__(64) void k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby,
+                                                      int zseg, int nseg, float bl2e,
+                                                      float inv_hw,
+                                                      const int32_t *__restrict__ zstart,
+                                                      const uint32_t *__restrict__ perm,
+                                                      CI3s i1s, CF3s frs,
+                                                      const float2 *__restrict__ c,
+                                                      const float2 *__restrict__ pre,
+                                                      float2 *__restrict__ grid) {
+    __shared__ float table[64 * REC];
+    __shared__ float2 stage[ZST][64];
+    const int64_t nw = (int64_t)nbx * nby * nseg;
+    int64_t wid = xcd_remap(blockIdx.x, nw);
+    const int seg = (int)(wid % nseg);
+    wid /= nseg;
+    const int by = (int)(wid % nby), bx = (int)(wid / nby);
+    const int z0 = seg * zseg, zend = min(z0 + zseg, n2);
+    const int lane = threadIdx.x, lx = lane >> 3, ly = lane & 7;
+    const int bxm = bx == 0 ? nbx - 1 : bx - 1, bym = by == 0 ? nby - 1 : by - 1;
+    const int blk[NR] = {bx * nby + by, bxm * nby + by, bx * nby + bym, bxm * nby + bym};
+    const int clo[NR] = {0, 2, 1, 2}, chi[NR] = {3, 3, 2, 2};
+    float wre[W], wim[W];
+#pragma unroll
+    for (int a = 0; a < W; ++a) wre[a] = wim[a] = 0.f;
+    int zw = z0 - (W - 1);  // z of window cell 0
+    for (int zc = z0 - (W - 1); zc < zend; zc += ZCH) {
+        int pf[ZCH * NR + 1], rs[ZCH * NR];
+        pf[0] = 0;
+#pragma unroll
+        for (int t = 0; t < ZCH; ++t) {
+            const int z = zc + t;
+            const int zz = z < 0 ? z + n2 : z;
+#pragma unroll
+            for (int r = 0; r < NR; ++r) {
+                const int i = t * NR + r;
+                int st = 0, cnt = 0;
+                if (z < zend) {
+                    const int64_t kb = ((int64_t)blk[r] * n2 + zz) * 4;
+                    st = zstart[kb + clo[r]];
+                    cnt = zstart[kb + chi[r] + 1] - st;
+                }
+                rs[i] = st;
+                pf[i + 1] = pf[i] + cnt;
+            }
+        }
+        const int tot = pf[ZCH * NR];
+        for (int bat = 0; bat < tot; bat += 64) {
+            const int nb = min(64, tot - bat);
+            __syncthreads();
+            if (lane < nb) {
+                const int e = bat + lane;
+                int i = 0;
+#pragma unroll
+                for (int q = 1; q < ZCH * NR; ++q) i += (e >= pf[q]) ? 1 : 0;
+                int st = rs[0], p0 = pf[0];
+#pragma unroll
+                for (int q = 1; q < ZCH * NR; ++q)
+                    if (q == i) {
+                        st = rs[q];
+                        p0 = pf[q];
+                    }
+                const int64_t j = (int64_t)st + (e - p0);
+                const int ox = rel_offset(i1s.p[0][j], n0, ZB * bx);
+                const int oy = rel_offset(i1s.p[1][j], n1, ZB * by);
+                const float fx = frs.p[0][j], fy = frs.p[1][j], fz = frs.p[2][j];
+                float2 cv = c[perm[j]];
+                if (pre) {
+                    const float2 pv = pre[j];
+                    cv = make_float2(cv.x * pv.x - cv.y * pv.y, cv.x * pv.y + cv.y * pv.x);
+                }
+                float *rec = table + lane * REC;
+#pragma unroll
+                for (int q = 0; q < 24; ++q) rec[q] = 0.f;
+#pragma unroll
+                for (int a = 0; a < W; ++a) {
+                    const int qx = ox + a, qy = oy + a;
+                    const float wx = es_weight((float)a - fx, bl2e, inv_hw);
+                    const float wy = es_weight((float)a - fy, bl2e, inv_hw);
+                    if ((unsigned)qx < (unsigned)ZB) {
+                        rec[2 * qx] = cv.x * wx;
+                        rec[2 * qx + 1] = cv.y * wx;
+                    }
+                    if ((unsigned)qy < (unsigned)ZB) rec[16 + qy] = wy;
+                    rec[24 + a] = es_weight((float)a - fz, bl2e, inv_hw);
+                }
+            }
+            __syncthreads();
+            // rows of z-step t occupy [pf[t*NR], pf[(t+1)*NR]) of the chunk
+#pragma unroll
+            for (int t = 0; t < ZCH; ++t) {
+                const int kb = max(pf[t * NR] - bat, 0), ke = min(pf[(t + 1) * NR] - bat, nb);
+                if (kb >= ke) continue;
+                const int ze = zc + t;
+                while (zw < ze) {
+                    if (zw >= z0)
+                        store_stage<W>(stage, grid, lane, (zw - z0) % ZST, zw, n1, n2, bx, by,
+                                       wre[0], wim[0], zw == zend - 1);
+#pragma unroll
+                    for (int a = 0; a < W - 1; ++a) {
+                        wre[a] = wre[a + 1];
+                        wim[a] = wim[a + 1];
+                    }
+                    wre[W - 1] = wim[W - 1] = 0.f;
+                    ++zw;
+                }
+                for (int k = kb; k < ke; k += UNR) {
+                    float vr[UNR], vi[UNR], wz[UNR][W];
+#pragma unroll
+                    for (int u = 0; u < UNR; ++u) {
+                        const int kk = min(k + u, ke - 1);
+                        const float *rec = table + kk * REC;
+                        const float2 wxc = *(const float2 *)(rec + 2 * lx);
+                        const float wy = (k + u < ke) ? rec[16 + ly] : 0.f;
+                        vr[u] = wxc.x * wy;
+                        vi[u] = wxc.y * wy;
+#pragma unroll
+                        for (int a = 0; a < W; ++a) wz[u][a] = rec[24 + a];
+                    }
+#pragma unroll
+                    for (int u = 0; u < UNR; ++u)
+#pragma unroll
+                        for (int a = 0; a < W; ++a) {
+                            wre[a] = fmaf(vr[u], wz[u][a], wre[a]);
+                            wim[a] = fmaf(vi[u], wz[u][a], wim[a]);
+                        }
+                }
+            }
+        }
+    }
+    while (zw < zend) {  // drain the window up to the segment end
+        if (zw >= z0)
+            store_stage<W>(stage, grid, lane, (zw - z0) % ZST, zw, n1, n2, bx, by, wre[0], wim[0],
+                           zw == zend - 1);
+#pragma unroll
+        for (int a = 0; a < W - 1; ++a) {
+            wre[a] = wre[a + 1];
+            wim[a] = wim[a + 1];
+        }
+        wre[W - 1] = wim[W - 1] = 0.f;
+        ++zw;
+    }
+}
+
+// key = ((bx*nby + by)*n2 + z)*4 + classpos (see the file comment).
+__global__ void k_zsweep_keys(int64_t P, int n0, int n1, int n2, int w, const int32_t *__restrict__ i1x,
+                              const int32_t *__restrict__ i1y, const int32_t *__restrict__ i1z,
+                              uint32_t *__restrict__ key) {
+    int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= P) return;
+    const int x = pmod(i1x[j], n0), y = pmod(i1y[j], n1), z = pmod(i1z[j], n2);
+    const int cut = ZB - (w - 1);
+    const int cx = (x % ZB) >= cut, cy = (y % ZB) >= cut;
+    const int cp = cx ? (cy ? 2 : 3) : (cy ? 1 : 0);
+    const uint32_t blkid = (uint32_t)((x / ZB) * (n1 / ZB) + y / ZB);
+    key[j] = (blkid * (uint32_t)n2 + (uint32_t)z) * 4u + (uint32_t)cp;
+}
+
+__global__ void k_key_hist(const uint32_t *__restrict__ skey, int64_t P, int64_t K,
+                           uint32_t *__restrict__ cnt) {
+    int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= P) return;
+    const uint32_t k = skey[j];
+    if ((int64_t)k < K) atomicAdd(&cnt[k], 1u);
+}
+
+inline int zsweep_check(const mn_bins *g) {
+    MN_REQUIRE(g != nullptr && g->dim == 3, "zsweep: 3D geometry required");
+    MN_REQUIRE(g->w >= 2 && g->w <= ZB, "zsweep: kernel width must be in [2, 8]");
+    MN_REQUIRE(g->n[0] % ZB == 0 && g->n[1] % ZB == 0, "zsweep: n0, n1 must be multiples of 8");
+    MN_REQUIRE(g->n[0] >= 2 * ZB && g->n[1] >= 2 * ZB, "zsweep: n0, n1 must be >= 16");
+    MN_REQUIRE(g->n[2] >= g->w && g->n[2] < (int64_t(1) << 24), "zsweep: n2 out of range");
+    const int64_t K = (g->n[0] / ZB) * (g->n[1] / ZB) * g->n[2] * 4;
+    MN_REQUIRE(K < (int64_t(1) << 31), "zsweep: key space too large");
+    return MN_OK;
+}
+
+inline int64_t zsweep_nkeys(const mn_bins *g) {
+    return (g->n[0] / ZB) * (g->n[1] / ZB) * g->n[2] * 4;
+}
+
+struct ZArgs {
+    const mn_bins *g;
+    float beta;
+    int zseg;
+    const int32_t *zstart;
+    const uint32_t *perm;
+    CI3s i1s;
+    CF3s frs;
+    const float2 *c, *pre;
+    float2 *grid;
+    hipStream_t s;
+};
+
+template <int DIM, int W>
+struct ZLaunch {
+    static int run(const ZArgs &a) {
+        if constexpr (DIM != 3 || W > ZB) {
+            set_error("zsweep: unsupported dim/width");
+            return MN_EINVAL;
+        } else {
+            const int n0 = (int)a.g->n[0], n1 = (int)a.g->n[1], n2 = (int)a.g->n[2];
+            const int nbx = n0 / ZB, nby = n1 / ZB, nseg = (n2 + a.zseg - 1) / a.zseg;
+            const int64_t nw = (int64_t)nbx * nby * nseg;
+            const float bl2e = (float)(a.beta * 1.4426950408889634);
+            const float inv_hw = (float)(2.0 / W);
+            k_spread_zsweep<W><<<(unsigned)nw, 64, 0, a.s>>>(n0, n1, n2, nbx, nby, a.zseg, nseg,
+                                                             bl2e, inv_hw, a.zstart, a.perm,
+                                                             a.i1s, a.frs, a.c, a.pre, a.grid);
+            MN_LAUNCH_CHECK("spread_zsweep");
+            return MN_OK;
+        }
+    }
+};
+
+}  // namespace
+}  // namespace mn
+
+using namespace mn;
+
+extern "C" {
+
+int mn_zsweep_keys(const mn_bins *g, int64_t P, const int32_t *const i1[3], uint32_t *key,
+                   mn_stream_t stream) {
+    clear_error();
+    int rc = zsweep_check(g);
+    if (rc) return rc;
+    MN_REQUIRE(P >= 1 && P < (int64_t(1) << 31), "zsweep keys: P must be in [1, 2^31)");
+    MN_REQUIRE(i1[0] && i1[1] && i1[2] && key, "zsweep keys: NULL pointer");
+    k_zsweep_keys<<<(unsigned)((P + 255) / 256), 256, 0, as_stream(stream)>>>(
+        P, (int)g->n[0], (int)g->n[1], (int)g->n[2], g->w, i1[0], i1[1], i1[2], key);
+    MN_LAUNCH_CHECK("zsweep_keys");
+    return MN_OK;
+}
+
+int64_t mn_zsweep_nkeys(const mn_bins *g) {
+    if (zsweep_check(g)) return -1;
+    return zsweep_nkeys(g);
+}
+
+int64_t mn_zsweep_starts_workspace_bytes(const mn_bins *g) {
+    if (zsweep_check(g)) return -1;
+    return 4 * (scan_partials_elems(zsweep_nkeys(g) + 1) + 64);
+}
+
+int mn_zsweep_starts(const mn_bins *g, int64_t P, const uint32_t *sorted_key, int32_t *zstart,
+                     void *ws, int64_t ws_bytes, mn_stream_t stream) {
+    clear_error();
+    int rc = zsweep_check(g);
+    if (rc) return rc;
+    MN_REQUIRE(P >= 1 && P < (int64_t(1) << 31), "zsweep starts: P must be in [1, 2^31)");
+    MN_REQUIRE(sorted_key && zstart && ws, "zsweep starts: NULL pointer");
+    const int64_t K = zsweep_nkeys(g);
+    MN_REQUIRE(ws_bytes >= mn_zsweep_starts_workspace_bytes(g), "zsweep starts: workspace too small");
+    hipStream_t s = as_stream(stream);
+    uint32_t *cnt = reinterpret_cast<uint32_t *>(zstart);
+    rc = fill_zero(cnt, 4 * (K + 1), s);
+    if (rc) return rc;
+    k_key_hist<<<(unsigned)((P + 255) / 256), 256, 0, s>>>(sorted_key, P, K, cnt);
+    MN_LAUNCH_CHECK("zsweep key histogram");
+    return scan_exclusive_u32(cnt, K + 1, static_cast<uint32_t *>(ws), s);
+}
+
+int mn_spread_zsweep(const mn_bins *g, float beta, int64_t P, int zseg, const int32_t *zstart,
+                     const uint32_t *perm, const int32_t *const i1s[3], const float *const frs[3],
+                     const void *c, const void *pre, void *grid, mn_stream_t stream) {
+    clear_error();
+    int rc = zsweep_check(g);
+    if (rc) return rc;
+    MN_REQUIRE(P >= 1 && P < (int64_t(1) << 31), "zsweep spread: P must be in [1, 2^31)");
+    MN_REQUIRE(zseg >= 1, "zsweep spread: zseg must be >= 1");
+    MN_REQUIRE(zstart && perm && c && grid, "zsweep spread: NULL pointer");
+    ZArgs a{};
+    for (int d = 0; d < 3; ++d) {
+        MN_REQUIRE(i1s[d] && frs[d], "zsweep spread: NULL sorted cell/fraction pointer");
+        a.i1s.p[d] = i1s[d];
+        a.frs.p[d] = frs[d];
+    }
+    a.g = g;
+    a.beta = beta;
+    a.zseg = zseg;
+    a.zstart = zstart;
+    a.perm = perm;
+    a.c = static_cast<const float2 *>(c);
+    a.pre = static_cast<const float2 *>(pre);
+    a.grid = static_cast<float2 *>(grid);
+    a.s = as_stream(stream);
+    return select_dim_w<ZLaunch>(3, g->w, a);
+}
+
+}  // extern "C"

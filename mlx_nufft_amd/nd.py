@@ -66,6 +66,9 @@ class _PointsND:
         x64 = self._coords(x)
         self.P = x64[0].numel()
         self.bins = E.make_bins(self.dim, self.w, self.n_up, cell_bytes=self._cell_bytes)
+        self._zsweep = self._use_zsweep and E.zsweep_eligible(self.dim, self.w, self.n_up)
+        if self._zsweep:
+            self._zbins = E.make_bins(3, self.w, self.n_up, m=(8, 8, 1))
         self._set_points(x64)
 
         # Mode deconvolution 1/phihat(2 pi k / n_up) on the uncentred fine grid
@@ -109,7 +112,11 @@ class _PointsND:
         with tm("setpts"):
             i1, fr, key = E.setpts_t12(self.bins, x64, self.prec == "crit64")
         with tm("sort+tables"):
-            self.pts = E.SortedPoints(self.bins, i1, fr, key)
+            if self._zsweep:
+                del key
+                self.pts = E.ZSweepPoints(self._zbins, i1, fr)
+            else:
+                self.pts = E.SortedPoints(self.bins, i1, fr, key)
         self.sorted = True
         self._od = True
         self._finish_profile(tm)
@@ -146,6 +153,7 @@ class Type1PlanND(_PointsND):
     """
 
     _cell_bytes = E.SPREAD_CELL_BYTES
+    _use_zsweep = True
 
     def __init__(self, x, n_modes, eps=1e-6, isign=+1, upsampfac=2.0, prec="crit64",
                  sort_points=True, spread_method="auto"):
@@ -166,10 +174,14 @@ class Type1PlanND(_PointsND):
         grid = self._fine_grid(1)
         fk = torch.empty(self.N, dtype=torch.complex64, device=self.device)
         tm = self._timer()
-        with tm("zero"):
-            E.fill_zero(grid)
-        with tm("spread"):
-            E.spread(self.pts, self.beta, cd, grid, accumulate=True)
+        if self.pts.kind == "zsweep":
+            with tm("spread"):
+                E.spread_zsweep(self.pts, self.beta, cd, grid)
+        else:
+            with tm("zero"):
+                E.fill_zero(grid)
+            with tm("spread"):
+                E.spread(self.pts, self.beta, cd, grid, accumulate=True)
         with tm("fft"):
             E.fft(grid, self.n_up, self.isign)
         with tm("deconv"):
@@ -194,7 +206,11 @@ class Type1PlanND(_PointsND):
         fk = torch.empty((B, *self.N), dtype=torch.complex64, device=self.device)
         tm = self._timer()
         with tm("spread"):
-            E.spread_batch(self.pts, self.beta, cd, grids)
+            if self.pts.kind == "zsweep":
+                for b in range(B):
+                    E.spread_zsweep(self.pts, self.beta, cd[b], grids[b])
+            else:
+                E.spread_batch(self.pts, self.beta, cd, grids)
         with tm("fft"):
             E.fft(grids, self.n_up, self.isign, batch=B)
         with tm("deconv"):
@@ -246,6 +262,7 @@ class Type2PlanND(_PointsND):
     """
 
     _cell_bytes = E.INTERP_CELL_BYTES
+    _use_zsweep = False
 
     def __init__(self, x, n_modes, eps=1e-6, isign=-1, upsampfac=2.0, prec="crit64",
                  sort_points=False, spread_method="auto"):

@@ -67,20 +67,27 @@ def test_type2_vs_direct(dim, N, isign, eps, oracle, mn):
     assert err <= max(eps, 2 * ref_err)
 
 
-@pytest.mark.parametrize("dim,N", [(1, (300,)), (2, (64, 48)), (3, (32, 24, 20))])
-def test_spread_grid_vs_oracle(dim, N, oracle, mn):
+@pytest.mark.parametrize("dim,N,path", [(1, (300,), "tiles"), (2, (64, 48), "tiles"),
+                                        (3, (32, 24, 20), "tiles"), (3, (32, 24, 20), "zsweep")])
+def test_spread_grid_vs_oracle(dim, N, path, oracle, mn, monkeypatch):
     """The spread kernel's fine grid against the oracle's fp64 spread on the
-    same (i1, fr) -- a kernel-level check independent of the FFT."""
+    same (i1, fr) -- a kernel-level check independent of the FFT, for the
+    LDS-tile spread and the owner-computes z-sweep."""
     from mlx_nufft_amd import _engine as E
 
-    print(f"case spread-grid dim={dim} N={N}", flush=True)
+    print(f"case spread-grid dim={dim} N={N} path={path}", flush=True)
+    monkeypatch.setenv("MN_SPREAD", "tiles" if path == "tiles" else "")
     rng = np.random.default_rng(9)
     M = 30_000
     x = _pts(rng, dim, M)
     c = _cplx(rng, M)
     p = mn.Type1PlanND(tuple(x), N, eps=1e-6)
+    assert p.pts.kind == path
     grid = torch.empty(p.n_up, dtype=torch.complex64, device="cuda")
-    E.spread(p.pts, p.beta, torch.from_numpy(c).cuda(), grid)
+    if path == "zsweep":
+        E.spread_zsweep(p.pts, p.beta, torch.from_numpy(c).cuda(), grid)
+    else:
+        E.spread(p.pts, p.beta, torch.from_numpy(c).cuda(), grid)
     i1o, fro = oracle.setpts_t12(x, p.n_up, p.w)
     go = oracle.spread(i1o, fro, c, p.n_up, p.w, p.beta)
     assert oracle.rel_l2(grid.cpu().numpy(), go) < 1e-5

@@ -1,0 +1,112 @@
+"""GPU checks of the owner-computes z-sweep spread.
+
+* keys and the key start table bit-exact against a numpy restatement of the
+  layout (block of the first tap, z, reach class in [00, 01, 11, 10] order);
+* the spread grid against the oracle's fp64 spread on the same (i1, fr) for
+  edge geometries: clustered points (more than 64 points per z-step of one
+  block), 16-wide grids (the -x/-y neighbour block wraps), a z extent that
+  is not a multiple of the segment, and w = 2..8;
+* z-sweep == LDS-tile spread on the same plan inputs.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _keys_numpy(i1, n, w):
+    x, y, z = (i1[d].astype(np.int64) % n[d] for d in range(3))
+    cut = 8 - (w - 1)
+    cx, cy = (x % 8) >= cut, (y % 8) >= cut
+    cp = np.where(cx, np.where(cy, 2, 3), np.where(cy, 1, 0))
+    blk = (x // 8) * (n[1] // 8) + y // 8
+    return ((blk * n[2] + z) * 4 + cp).astype(np.uint32), (n[0] // 8) * (n[1] // 8) * n[2] * 4
+
+
+@pytest.mark.parametrize("N,eps", [((32, 24, 20), 1e-5), ((8, 8, 20), 1e-3), ((64, 64, 64), 1e-6)])
+def test_zsweep_keys_and_starts(N, eps, oracle, mn):
+    print(f"case zsweep keys N={N} eps={eps}", flush=True)
+    rng = np.random.default_rng(21)
+    M = 50_000
+    x = [rng.uniform(-np.pi, np.pi, M) for _ in range(3)]
+    p = mn.Type1PlanND(tuple(x), N, eps=eps)
+    assert p.pts.kind == "zsweep"
+    i1o, _ = oracle.setpts_t12(x, p.n_up, p.w)
+    key, K = _keys_numpy(i1o, p.n_up, p.w)
+    ref = np.argsort(key, kind="stable")
+    assert np.array_equal(p.pts.perm.cpu().numpy().view(np.uint32), ref.astype(np.uint32))
+    zs = p.pts.zstart.cpu().numpy().astype(np.int64)
+    exp = np.zeros(K + 1, np.int64)
+    exp[1:] = np.cumsum(np.bincount(key.astype(np.int64), minlength=K))
+    assert np.array_equal(zs, exp)
+
+
+def _grid_check(oracle, mn, x, c, N, eps, tol=1e-5):
+    from mlx_nufft_amd import _engine as E
+
+    p = mn.Type1PlanND(tuple(x), N, eps=eps)
+    assert p.pts.kind == "zsweep"
+    grid = torch.empty(p.n_up, dtype=torch.complex64, device="cuda")
+    E.spread_zsweep(p.pts, p.beta, torch.from_numpy(c).cuda(), grid)
+    i1o, fro = oracle.setpts_t12(x, p.n_up, p.w)
+    go = oracle.spread(i1o, fro, c, p.n_up, p.w, p.beta)
+    err = oracle.rel_l2(grid.cpu().numpy(), go)
+    assert err < tol, err
+    return p
+
+
+@pytest.mark.parametrize("eps", [1e-1, 1e-2, 1e-3, 1e-4, 1e-5, 1e-6, 1e-7])
+def test_zsweep_widths(eps, oracle, mn):
+    """w = 2 .. 8 through eps (sigma = 2)."""
+    print(f"case zsweep width eps={eps}", flush=True)
+    rng = np.random.default_rng(22)
+    M = 20_000
+    x = [rng.uniform(-np.pi, np.pi, M) for _ in range(3)]
+    c = (rng.standard_normal(M) + 1j * rng.standard_normal(M)).astype(np.complex64)
+    _grid_check(oracle, mn, x, c, (24, 20, 18), eps)
+
+
+def test_zsweep_clustered_and_wrapping(oracle, mn):
+    """Points clustered at the periodic corner (many per block and z, and
+    footprints wrapping in x, y, z) on a 16x16 grid."""
+    print("case zsweep clustered", flush=True)
+    rng = np.random.default_rng(23)
+    M = 40_000
+    h = 2 * np.pi / 16
+    x = [np.concatenate([-np.pi + rng.uniform(0, 3 * h, M // 2),
+                         np.pi - rng.uniform(0, 3 * h, M - M // 2)]) for _ in range(3)]
+    c = (rng.standard_normal(M) + 1j * rng.standard_normal(M)).astype(np.complex64)
+    _grid_check(oracle, mn, x, c, (8, 8, 8), 1e-5)
+
+
+def test_zsweep_partial_segment(oracle, mn):
+    """A z extent (n2 = 300) that is not a multiple of the 128-cell segment."""
+    print("case zsweep partial segment", flush=True)
+    rng = np.random.default_rng(24)
+    M = 60_000
+    x = [rng.uniform(-np.pi, np.pi, M) for _ in range(3)]
+    c = (rng.standard_normal(M) + 1j * rng.standard_normal(M)).astype(np.complex64)
+    p = _grid_check(oracle, mn, x, c, (16, 16, 150), 1e-5)
+    assert p.n_up[2] % 128 != 0
+
+
+def test_zsweep_matches_tiles(mn, monkeypatch):
+    from mlx_nufft_amd import _engine as E
+
+    print("case zsweep vs tiles", flush=True)
+    rng = np.random.default_rng(25)
+    M = 200_000
+    x = [rng.uniform(-np.pi, np.pi, M) for _ in range(3)]
+    c = torch.from_numpy((rng.standard_normal(M) + 1j * rng.standard_normal(M))
+                         .astype(np.complex64)).cuda()
+    pz = mn.Type1PlanND(tuple(x), (64, 64, 48), eps=1e-5)
+    monkeypatch.setenv("MN_SPREAD", "tiles")
+    pt = mn.Type1PlanND(tuple(x), (64, 64, 48), eps=1e-5)
+    assert pz.pts.kind == "zsweep" and pt.pts.kind == "tiles"
+    gz = torch.empty(pz.n_up, dtype=torch.complex64, device="cuda")
+    gt = torch.empty(pt.n_up, dtype=torch.complex64, device="cuda")
+    E.spread_zsweep(pz.pts, pz.beta, c, gz)
+    E.spread(pt.pts, pt.beta, c, gt)
+    assert float((gz - gt).abs().norm() / gt.abs().norm()) < 1e-6
