@@ -1,0 +1,174 @@
+"""Host-side checks that need no GPU.
+
+* the C-ABI library loads and exports every function include/*.h declares,
+  and the ctypes signature table covers exactly that set;
+* the library's pure size queries (no device call);
+* the product's sizing equals the oracle's (which tests/test_oracle.py pins);
+* the engine's bin geometry and key widths;
+* argument validation of the finufft-style surface, which raises before any
+  device work, and the loud failure when no GPU is present (no CPU path).
+"""
+
+import ctypes
+import pathlib
+import re
+
+import numpy as np
+import pytest
+import torch
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+
+
+def _header_functions():
+    names = []
+    for h in sorted((ROOT / "include").glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        text = re.sub(r"//[^\n]*", "", text)
+        names += re.findall(r"\b(mn_[a-z0-9_]+)\s*\(", text)
+    return sorted(set(names))
+
+
+@pytest.fixture(scope="module")
+def clib():
+    from mlx_nufft_amd import _lib
+
+    return _lib.load_library()
+
+
+def test_header_symbols_exported(clib):
+    from mlx_nufft_amd import _lib
+
+    names = _header_functions()
+    assert len(names) >= 25
+    for n in names:
+        assert hasattr(clib, n), f"{n} declared in include/ but not exported"
+    assert sorted(_lib.EXPORTED) == names
+
+
+def test_pure_queries(clib):
+    from mlx_nufft_amd import _lib
+
+    assert clib.mn_version() == 100
+    ws = [clib.mn_sort_workspace_bytes(P) for P in (1, 1000, 1 << 20, 20_000_000)]
+    assert all(b > 0 for b in ws) and ws == sorted(ws)
+    # workspace holds at least the ping-pong key + perm buffers of P entries
+    assert ws[-1] >= 2 * 4 * 20_000_000
+
+    g = _lib.Bins.make(3, 6, [512, 512, 512], [8, 8, 1])
+    assert clib.mn_zsweep_nkeys(ctypes.byref(g)) == 64 * 64 * 512 * 4
+    assert clib.mn_zsweep_starts_workspace_bytes(ctypes.byref(g)) > 4 * 64 * 64 * 512 * 4 // 2048
+    assert clib.mn_subproblem_workspace_bytes(ctypes.byref(_lib.Bins.make(3, 6, [64] * 3,
+                                                                          [11] * 3))) > 0
+    # z-sweep geometry limits: w <= 8, n0 and n1 multiples of 8
+    for bad in (_lib.Bins.make(3, 9, [512] * 3, [8, 8, 1]),
+                _lib.Bins.make(3, 6, [500, 512, 512], [8, 8, 1]),
+                _lib.Bins.make(2, 6, [512, 512], [8, 8])):
+        assert clib.mn_zsweep_nkeys(ctypes.byref(bad)) == -1
+        assert clib.mn_last_error().decode()
+    # a grid smaller than the kernel width is rejected
+    assert clib.mn_subproblem_workspace_bytes(ctypes.byref(_lib.Bins.make(1, 8, [6], [6]))) == -1
+
+
+def test_bins_struct_layout():
+    from mlx_nufft_amd import _lib
+
+    # struct { int32 dim, w; int64 n[3]; int32 m[3], nb[3]; }
+    assert ctypes.sizeof(_lib.Bins) == 8 + 24 + 12 + 12
+    g = _lib.Bins.make(3, 6, [512, 480, 90], [11, 11, 11])
+    assert list(g.nb) == [47, 44, 9] and g.nbins == 47 * 44 * 9
+
+
+# ---------------------------------------------------------------- sizing --
+
+def test_product_sizing_equals_oracle(oracle):
+    from mlx_nufft_amd import sizing as S
+
+    for n in list(range(0, 2000)) + [65537, 99991, 123457]:
+        assert S.next235even(n) == oracle.next235even(n)
+    for eps in (1e-1, 3e-2, 1e-3, 1e-4, 1e-5, 1e-6, 1e-7, 1e-9, 1e-12, 1e-15):
+        for sig in (2.0, 1.25, 1.5):
+            assert S.kernel_params(eps, sig) == oracle.kernel_params(eps, sig)
+    xi = np.linspace(0, np.pi, 33)
+    for w, beta in ((6, 13.8), (9, 16.45566231965758), (2, 4.4)):
+        assert np.allclose(S.kernel_ft(xi, beta, w), oracle.kernel_ft(xi, beta, w),
+                           rtol=1e-13, atol=0)
+    for S_, X_ in ((200.0, 1.0), (0.0, 0.0), (30.0, 0.0), (0.0, 3.0), (1e4, 2.5)):
+        assert S.set_nhg_type3(S_, X_, 1.25, 9) == pytest.approx(
+            oracle.set_nhg_type3(S_, X_, 1.25, 9), rel=1e-15)
+
+
+def test_engine_bin_geometry(monkeypatch):
+    from mlx_nufft_amd import _engine as E
+
+    monkeypatch.setattr(E, "_budget", 80 * 1024)
+    monkeypatch.delenv("MN_BIN_M", raising=False)
+    for w in range(2, 17):
+        m = E.bin_sizes(3, w, [512] * 3)
+        assert E.SPREAD_CELL_BYTES * np.prod([v + w - 1 for v in m]) <= 80 * 1024
+        assert min(m) >= 1
+    assert E.bin_sizes(1, 6, [8192]) == [1024]
+    assert E.bin_sizes(2, 6, [20, 2048]) == [20, 32]
+    assert E.zsweep_eligible(3, 6, [512, 512, 512])
+    assert not E.zsweep_eligible(3, 9, [512, 512, 512])
+    assert not E.zsweep_eligible(3, 6, [514, 512, 512])
+    assert not E.zsweep_eligible(2, 6, [512, 512])
+    g = E.make_bins(3, 6, [512] * 3, m=(8, 8, 1))
+    assert E.key_bits(g) == (64 * 64 * 512 - 1).bit_length()
+
+
+# ------------------------------------------------------------ validation --
+
+def test_api_validation_errors(mn):
+    x = np.zeros(10)
+    with pytest.raises(NotImplementedError):
+        mn.nufft1d1(x, x.astype(complex), 8, modeord=1)
+    with pytest.raises(ValueError):
+        mn.Plan(4, (8, 8))
+    with pytest.raises(ValueError):
+        mn.Plan(1, (8, 8), dtype="float64")
+    with pytest.raises(ValueError):
+        mn.Plan(1, (8, 8, 8, 8))
+    with pytest.raises(ValueError):
+        mn.Type1PlanND((x, x), (8, 8), prec="fp16")
+    with pytest.raises(ValueError):
+        mn.Type1PlanND((x, x), (8, 8, 8))
+    with pytest.raises(ValueError):
+        mn.Type1PlanND((x, x), (8, 0))
+    with pytest.raises(ValueError):
+        mn.Type1PlanND((x, x), (8, 8), upsampfac=5.0)
+    with pytest.raises(ValueError):
+        mn.Type1PlanND((x, x, x, x), 8)
+    with pytest.raises(ValueError):
+        mn.expi([np.zeros(3)] * 9)
+    with pytest.raises(ValueError):
+        mn.expi([np.zeros(3), np.zeros(4)])
+    with pytest.raises(RuntimeError):
+        mn.Type3Plan((x, x, x), (x, x, x), fft_backend="vkfft")
+    assert mn.vkfft_available() is False
+    p = mn.Plan(1, (8, 8))
+    with pytest.raises(RuntimeError):
+        p.execute(np.zeros(10, complex))
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU failure")
+def test_no_gpu_fails_loudly(mn):
+    """Without a ROCm device every compute entry raises; nothing falls back
+    to a CPU implementation."""
+    rng = np.random.default_rng(0)
+    x = [rng.uniform(-np.pi, np.pi, 100) for _ in range(3)]
+    c = np.ones(100, complex)
+    for call in (lambda: mn.nufft3d1(*x, c, (8, 8, 8)),
+                 lambda: mn.nufft2d2(x[0], x[1], np.ones((8, 8), complex)),
+                 lambda: mn.nufft3d3(*x, c, *x),
+                 lambda: mn.Type1PlanND(tuple(x), (8, 8, 8)),
+                 lambda: mn.expi(np.zeros(4))):
+        with pytest.raises(RuntimeError, match="GPU"):
+            call()
+
+
+def test_product_does_not_import_oracle():
+    for f in (ROOT / "mlx_nufft_amd").rglob("*.py"):
+        text = f.read_text()
+        assert not re.search(r"^\s*(from|import)\s+oracle\b", text, re.M), f
+        assert "liboracle" not in text, f
