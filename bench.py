@@ -44,7 +44,24 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--exec-only", action="store_true",
                     help="time execute() only (plan built once), for profiling")
+    ap.add_argument("--copy-calibration", type=float, default=0.0, metavar="GIB",
+                    help="only copy a GIB-sized device buffer 5 times: the plain copy "
+                         "kernel whose FETCH_SIZE / WRITE_SIZE scale the traffic counters")
     return ap.parse_args()
+
+
+def copy_calibration(gib):
+    """5 device-to-device copies of gib GiB (torch's copy kernel): each reads
+    and writes exactly that many bytes of HBM."""
+    import torch
+
+    nbytes = int(gib * (1 << 30))
+    a = torch.ones(nbytes, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_per_launch": nbytes, "launches": 5}))
 
 
 def cpu_baseline(x, c, N, eps):
@@ -73,6 +90,9 @@ def main():
         print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
               "multi-GPU sharding is design-only (see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration > 0:
+        copy_calibration(args.copy_calibration)
+        return
     import numpy as np
     import torch
 

@@ -58,7 +58,8 @@ const char *mn_last_error(void);
 /* ABI version (major*10000 + minor*100 + patch). */
 int mn_version(void);
 /* LDS bytes one workgroup may use on the current device (bounds the bin
- * tile: 8 * prod_d (m[d] + w - 1) bytes for spread and interp). */
+ * tiles: prod_d (m[d] + w - 1) cells of 16 bytes for the tile spread, which
+ * accumulates in fp64, and of 8 bytes for interp). */
 int mn_device_lds_bytes(void);
 
 /*
@@ -85,6 +86,22 @@ int64_t mn_sort_workspace_bytes(int64_t P);
 int mn_sort_keys(int64_t P, int key_bits, const uint32_t *key_in,
                  uint32_t *key_out, uint32_t *perm_out, void *ws,
                  int64_t ws_bytes, mn_stream_t stream);
+
+/*
+ * The same stable sort carrying ncols (<= MN_SORT_MAX_COLS) 32-bit payload
+ * columns: cols_out[c][r] = cols_in[c][perm_out[r]]. Only the low key_bits
+ * bits of a key are sorted on; higher bits travel with the key unchanged.
+ * Moving the per-point data through the radix passes replaces a gather by
+ * perm (one cache line per 4-byte element) with coalesced tile writes.
+ * ws must hold mn_sort_pairs_workspace_bytes(P, ncols) bytes.
+ * ref: nd.py:314-318 (argsort, then take of i1/fr by perm), nd.py:338-340.
+ */
+#define MN_SORT_MAX_COLS 8
+int64_t mn_sort_pairs_workspace_bytes(int64_t P, int ncols);
+int mn_sort_pairs(int64_t P, int key_bits, const uint32_t *key_in, uint32_t *key_out,
+                  uint32_t *perm_out, int ncols, const uint32_t *const *cols_in,
+                  uint32_t *const *cols_out, void *ws, int64_t ws_bytes,
+                  mn_stream_t stream);
 
 /*
  * Gather per-point arrays into sorted order: out[j] = in[perm[j]] for i1
@@ -142,28 +159,44 @@ int mn_spread_accumulate(const mn_bins *g, float beta, int64_t P, int64_t nsub,
 
 /*
  * Owner-computes 3D spread ("z-sweep"), the fast path for 3D type-1 grids
- * with n0, n1 multiples of 8 (>= 16) and w <= 8. Each wavefront owns an
- * 8x8 (x, y) column block over a z-segment of zseg cells, sweeps z with a
- * w-cell window per column in registers and stores every grid cell exactly
- * once (no atomics; grid is fully overwritten). Points must be sorted by the
- * z-sweep key (mn_zsweep_keys) and located through zstart
- * (mn_zsweep_starts, mn_zsweep_nkeys() + 1 int32). g: dim 3, w, n (m and
- * nb are not used). pre: optional sorted-order strength multiplier.
- * key = ((bx*(n1/8) + by)*n2 + z)*4 + classpos with (bx, by, z) the block
- * and z of the first tap and classpos in [00, 01, 11, 10] order of whether
- * the footprint reaches the next block in x and in y.
- * ref: nd.py:492-579 (output-driven spread), nd.py:298-372 (bin sort).
+ * with n0, n1 multiples of 8 (>= 16), w <= 8 and n0*n1*n2/16 <= 2^26 keys.
+ * Each wavefront owns an 8x8 (x, y) column block over a z-segment of zseg
+ * cells, sweeps z with a w-cell window per column in registers and stores
+ * every grid cell exactly once (no atomics; grid is fully overwritten).
+ * g: dim 3, w, n (m and nb are not used).
+ *
+ * Point word (one uint32 per point, from mn_zsweep_setpts):
+ *   bits 0-25  key = ((bx*(n1/8) + by)*n2 + z)*4 + class, where (bx, by)
+ *              is the 8x8 block of the first tap, z its cell, and class in
+ *              [00, 01, 11, 10] order of whether the footprint reaches the
+ *              next block in x and in y;
+ *   bits 26-28 / 29-31  x / y cell of the first tap within its block.
+ * mn_zsweep_setpts computes the words and fr exactly as mn_setpts_t12 does
+ * the cells (crit64, bit for bit); sort them with mn_sort_pairs(key_bits =
+ * bits of mn_zsweep_nkeys() - 1, fr as payload) and build zstart
+ * (mn_zsweep_nkeys() + 1 int32: zstart[k] = first sorted index with key
+ * >= k) with mn_zsweep_starts. The spread reads the sorted words and
+ * fractions; strengths are c[perm[j]] (caller order), or c[j] when perm is
+ * NULL (c already in sorted order); pre: optional sorted-order multiplier.
+ * ref: nd.py:152-165 (cells), nd.py:492-579 (output-driven spread),
+ * nd.py:298-372 (bin sort).
  */
-int mn_zsweep_keys(const mn_bins *g, int64_t P, const int32_t *const i1[3], uint32_t *key,
-                   mn_stream_t stream);
 int64_t mn_zsweep_nkeys(const mn_bins *g);
-int64_t mn_zsweep_starts_workspace_bytes(const mn_bins *g);
-int mn_zsweep_starts(const mn_bins *g, int64_t P, const uint32_t *sorted_key, int32_t *zstart,
-                     void *ws, int64_t ws_bytes, mn_stream_t stream);
+int mn_zsweep_setpts(const mn_bins *g, int64_t P, const double *const x[3], int prec64,
+                     uint32_t *word, float *const fr[3], mn_stream_t stream);
+int mn_zsweep_starts(const mn_bins *g, int64_t P, const uint32_t *sorted_word, int32_t *zstart,
+                     mn_stream_t stream);
 int mn_spread_zsweep(const mn_bins *g, float beta, int64_t P, int zseg, const int32_t *zstart,
-                     const uint32_t *perm, const int32_t *const i1s[3],
+                     const uint32_t *perm, const uint32_t *sorted_word,
                      const float *const frs[3], const void *c, const void *pre, void *grid,
                      mn_stream_t stream);
+
+/*
+ * out[j] = in[perm[j]] for P complex64 values (a strength vector into
+ * sorted order). ref: nd.py:603 (mx.take of c by perm, GM spread).
+ */
+int mn_permute_c64(int64_t P, const uint32_t *perm, const void *in, void *out,
+                   mn_stream_t stream);
 
 /*
  * Batched spread: B strength vectors cs (B x P, caller order, row-major)

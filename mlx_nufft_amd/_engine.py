@@ -93,14 +93,28 @@ def setpts_t12(bins, xs, prec64):
 
 def sort_keys(key, nbits):
     """Stable argsort of uint32 keys (stored in int32 tensors): (sorted, perm)."""
+    skey, perm, _ = sort_pairs(key, nbits, [])
+    return skey, perm
+
+
+def sort_pairs(key, nbits, cols, outs=None):
+    """Stable sort of uint32 keys on their low nbits bits, carrying 32-bit
+    payload columns (int32/float32 tensors of P elements) into outs (new
+    tensors if None): (sorted keys, perm, sorted columns)."""
     P = key.numel()
     lib = L.lib()
-    ws = torch.empty(int(lib.mn_sort_workspace_bytes(P)), dtype=torch.uint8, device=key.device)
+    ncols = len(cols)
+    ws = torch.empty(int(lib.mn_sort_pairs_workspace_bytes(P, ncols)), dtype=torch.uint8,
+                     device=key.device)
     skey = torch.empty_like(key)
     perm = torch.empty_like(key)
-    L.check(lib.mn_sort_keys(P, int(nbits), L.ptr(key), L.ptr(skey), L.ptr(perm), L.ptr(ws),
-                             ws.numel(), L.stream()), "sort")
-    return skey, perm
+    if outs is None:
+        outs = [torch.empty_like(c) for c in cols]
+    cin = (ctypes.c_void_p * max(1, ncols))(*[c.data_ptr() for c in cols])
+    cout = (ctypes.c_void_p * max(1, ncols))(*[c.data_ptr() for c in outs])
+    L.check(lib.mn_sort_pairs(P, int(nbits), L.ptr(key), L.ptr(skey), L.ptr(perm), ncols, cin,
+                              cout, L.ptr(ws), ws.numel(), L.stream()), "sort")
+    return skey, perm, outs
 
 
 def gather_points(perm, i1, fr, extra=None):
@@ -138,8 +152,17 @@ class SortedPoints:
     def __init__(self, bins, i1, fr, key, extra=None, msub=MSUB):
         self.bins = bins
         self.P = i1.shape[1]
-        skey, self.perm = sort_keys(key, key_bits(bins))
-        self.i1s, self.frs, self.extra = gather_points(self.perm, i1, fr, extra)
+        dim = bins.dim
+        self.i1s = torch.empty_like(i1)
+        self.frs = torch.empty_like(fr)
+        cols = _rows(i1, dim) + _rows(fr, dim)
+        outs = _rows(self.i1s, dim) + _rows(self.frs, dim)
+        if extra is not None:
+            cols += [extra.real.contiguous(), extra.imag.contiguous()]
+            outs += [torch.empty_like(cols[-2]), torch.empty_like(cols[-1])]
+        skey, self.perm, out = sort_pairs(key, key_bits(bins), cols, outs)
+        self.extra = torch.complex(out[2 * dim], out[2 * dim + 1]) if extra is not None else None
+        del out, outs, cols
         self.info, self.nsub = build_subproblems(bins, skey, msub)
         self.skey = skey
 
@@ -159,51 +182,59 @@ ZSEG = 128  # z-segment (cells) owned by one z-sweep wavefront
 
 
 def zsweep_eligible(dim, w, n_up):
-    """True when the owner-computes z-sweep spread applies: 3D, w <= 8 and
-    the x and y fine-grid sizes multiples of 8 (>= 16). MN_SPREAD=tiles
-    forces the LDS-tile spread instead."""
+    """True when the owner-computes z-sweep spread applies: 3D, w <= 8, the
+    x and y fine-grid sizes multiples of 8 (>= 16) and at most 2^26 sort keys
+    (n0*n1*n2/16). MN_SPREAD=tiles forces the LDS-tile spread instead."""
     if os.environ.get("MN_SPREAD", "") == "tiles":
         return False
-    return (dim == 3 and w <= 8 and all(n % 8 == 0 and n >= 16 for n in n_up[:2]))
+    return (dim == 3 and w <= 8 and all(n % 8 == 0 and n >= 16 for n in n_up[:2])
+            and n_up[0] * n_up[1] * n_up[2] // 16 <= 1 << 26)
 
 
 class ZSweepPoints:
-    """Point state for the z-sweep spread: z-sweep keys, stable sort,
-    sorted cells/fractions and the key start table."""
+    """Point state for the z-sweep spread: packed point words and fractions
+    (setpts), stably sorted together by the z-sweep key, and the key start
+    table."""
 
     kind = "zsweep"
 
-    def __init__(self, bins, i1, fr):
+    def __init__(self, bins, x64, prec64):
         lib = L.lib()
+        dev = x64[0].device
         self.bins = bins
-        self.P = i1.shape[1]
-        key = torch.empty(self.P, dtype=torch.int32, device=i1.device)
-        L.check(lib.mn_zsweep_keys(ctypes.byref(bins), self.P, L.ptr3(_rows(i1, 3)), L.ptr(key),
-                                   L.stream()), "zsweep keys")
+        self.P = P = x64[0].numel()
+        word = torch.empty(P, dtype=torch.int32, device=dev)
+        fr = torch.empty((3, P), dtype=torch.float32, device=dev)
+        L.check(lib.mn_zsweep_setpts(ctypes.byref(bins), P, L.ptr3(x64), int(bool(prec64)),
+                                     L.ptr(word), L.ptr3(_rows(fr, 3)), L.stream()),
+                "zsweep setpts")
         K = int(lib.mn_zsweep_nkeys(ctypes.byref(bins)))
-        self.skey, self.perm = sort_keys(key, max(1, (K - 1).bit_length()))
-        del key
-        self.i1s, self.frs, self.extra = gather_points(self.perm, i1, fr)
-        self.zstart = torch.empty(K + 1, dtype=torch.int32, device=i1.device)
-        ws = torch.empty(int(lib.mn_zsweep_starts_workspace_bytes(ctypes.byref(bins))),
-                         dtype=torch.uint8, device=i1.device)
-        L.check(lib.mn_zsweep_starts(ctypes.byref(bins), self.P, L.ptr(self.skey),
-                                     L.ptr(self.zstart), L.ptr(ws), ws.numel(), L.stream()),
-                "zsweep starts")
-
-    def i1_rows(self):
-        return _rows(self.i1s, 3)
+        self.K = K
+        self.frs = torch.empty_like(fr)
+        self.word, self.perm, _ = sort_pairs(word, max(1, (K - 1).bit_length()), _rows(fr, 3),
+                                             _rows(self.frs, 3))
+        del word, fr
+        self.zstart = torch.empty(K + 1, dtype=torch.int32, device=dev)
+        L.check(lib.mn_zsweep_starts(ctypes.byref(bins), P, L.ptr(self.word), L.ptr(self.zstart),
+                                     L.stream()), "zsweep starts")
 
     def fr_rows(self):
         return _rows(self.frs, 3)
 
 
-def spread_zsweep(pts, beta, c, grid, pre=None, zseg=ZSEG):
-    """grid = spread(c) with the owner-computes z-sweep (overwrites grid)."""
+def permute_c64(perm, c, out):
+    """out[j] = c[perm[j]] (complex64 strengths into sorted order)."""
+    L.check(L.lib().mn_permute_c64(perm.numel(), L.ptr(perm), L.ptr(c), L.ptr(out), L.stream()),
+            "permute")
+
+
+def spread_zsweep(pts, beta, c, grid, pre=None, zseg=ZSEG, presorted=False):
+    """grid = spread(c) with the owner-computes z-sweep (overwrites grid).
+    c is in caller order, or in sorted order when presorted."""
     L.check(L.lib().mn_spread_zsweep(ctypes.byref(pts.bins), float(beta), pts.P, int(zseg),
-                                     L.ptr(pts.zstart), L.ptr(pts.perm), L.ptr3(pts.i1_rows()),
-                                     L.ptr3(pts.fr_rows()), L.ptr(c), L.ptr(pre), L.ptr(grid),
-                                     L.stream()), "spread_zsweep")
+                                     L.ptr(pts.zstart), None if presorted else L.ptr(pts.perm),
+                                     L.ptr(pts.word), L.ptr3(pts.fr_rows()), L.ptr(c), L.ptr(pre),
+                                     L.ptr(grid), L.stream()), "spread_zsweep")
 
 
 def spread(pts, beta, c, grid, pre=None, accumulate=False):

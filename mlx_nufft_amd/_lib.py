@@ -56,6 +56,9 @@ _SIGS = [
     ("mn_setpts_t12", c_int, [ctypes.POINTER(Bins), c_int64, VP3, c_int, VP3, VP3, c_vp, c_vp]),
     ("mn_sort_workspace_bytes", c_int64, [c_int64]),
     ("mn_sort_keys", c_int, [c_int64, c_int, c_vp, c_vp, c_vp, c_vp, c_int64, c_vp]),
+    ("mn_sort_pairs_workspace_bytes", c_int64, [c_int64, c_int]),
+    ("mn_sort_pairs", c_int, [c_int64, c_int, c_vp, c_vp, c_vp, c_int, ctypes.POINTER(c_vp),
+                              ctypes.POINTER(c_vp), c_vp, c_int64, c_vp]),
     ("mn_gather_points", c_int, [c_int, c_int64, c_vp, VP3, VP3, VP3, VP3, c_vp, c_vp, c_vp]),
     ("mn_subproblem_workspace_bytes", c_int64, [ctypes.POINTER(Bins)]),
     ("mn_build_subproblems", c_int, [ctypes.POINTER(Bins), c_int64, c_vp, c_int32, c_vp,
@@ -64,12 +67,12 @@ _SIGS = [
                           c_vp, c_vp, c_vp, c_vp]),
     ("mn_spread_accumulate", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int64, c_vp, c_vp,
                                      VP3, VP3, c_vp, c_vp, c_vp, c_vp]),
-    ("mn_zsweep_keys", c_int, [ctypes.POINTER(Bins), c_int64, VP3, c_vp, c_vp]),
     ("mn_zsweep_nkeys", c_int64, [ctypes.POINTER(Bins)]),
-    ("mn_zsweep_starts_workspace_bytes", c_int64, [ctypes.POINTER(Bins)]),
-    ("mn_zsweep_starts", c_int, [ctypes.POINTER(Bins), c_int64, c_vp, c_vp, c_vp, c_int64, c_vp]),
-    ("mn_spread_zsweep", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int, c_vp, c_vp, VP3,
+    ("mn_zsweep_setpts", c_int, [ctypes.POINTER(Bins), c_int64, VP3, c_int, c_vp, VP3, c_vp]),
+    ("mn_zsweep_starts", c_int, [ctypes.POINTER(Bins), c_int64, c_vp, c_vp, c_vp]),
+    ("mn_spread_zsweep", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int, c_vp, c_vp, c_vp,
                                  VP3, c_vp, c_vp, c_vp, c_vp]),
+    ("mn_permute_c64", c_int, [c_int64, c_vp, c_vp, c_vp, c_vp]),
     ("mn_spread_batch", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int64, c_vp, c_vp, VP3,
                                 VP3, c_int64, c_vp, c_vp, c_vp]),
     ("mn_interp", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int64, c_vp, c_vp, VP3, VP3,

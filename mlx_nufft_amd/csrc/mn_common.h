@@ -137,6 +137,33 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t nblk) {
 struct CI3s { const int32_t *p[3]; };
 struct CF3s { const float *p[3]; };
 
+// ---- z-sweep point word ----------------------------------------------------
+// The 3D owner-computes spread sorts one 32-bit word per point:
+//   bits  0-25  key = ((bx*nby + by)*n2 + z)*4 + reach class (sorted on)
+//   bits 26-28  x cell of the first tap within its 8-column block
+//   bits 29-31  y cell likewise
+// where (bx, by) is the 8x8 column block of the first tap (x, y), z its cell,
+// and the reach class says whether the footprint crosses into the next
+// block along x and along y, ordered [00, 01, 11, 10].
+constexpr int kZsBlock = 8;
+constexpr int kZsKeyBits = 26;
+constexpr uint32_t kZsKeyMask = (1u << kZsKeyBits) - 1u;
+
+__device__ __forceinline__ uint32_t zs_word(int x, int y, int z, int n1, int n2, int w) {
+    const int cut = kZsBlock - (w - 1);
+    const int lx = x & (kZsBlock - 1), ly = y & (kZsBlock - 1);
+    const int cx = lx >= cut, cy = ly >= cut;
+    const int cp = cx ? (cy ? 2 : 3) : (cy ? 1 : 0);
+    const uint32_t blk = (uint32_t)((x / kZsBlock) * (n1 / kZsBlock) + y / kZsBlock);
+    const uint32_t key = (blk * (uint32_t)n2 + (uint32_t)z) * 4u + (uint32_t)cp;
+    return key | ((uint32_t)lx << kZsKeyBits) | ((uint32_t)ly << (kZsKeyBits + 3));
+}
+
+// Validate a z-sweep geometry (3D, 2 <= w <= 8, n0 and n1 multiples of 8 and
+// >= 16, key space within kZsKeyBits); number of keys K = nbx*nby*n2*4.
+int zsweep_check(const mn_bins *g);
+int64_t zsweep_nkeys(const mn_bins *g);
+
 // Validate the point/subproblem arguments shared by spread and interp.
 int check_points(const mn_bins *g, int64_t P, int64_t nsub, const int32_t *info,
                  const uint32_t *perm, const int32_t *const i1s[3], const float *const frs[3],

@@ -40,6 +40,22 @@ __device__ __forceinline__ int bin_of(int i1, int hw, int n, int m) {
     return v / m;
 }
 
+// Cell index and fraction of one coordinate along one dim (crit64 when
+// prec64, else the fp32 path); see mn_setpts_t12.
+__device__ __forceinline__ void cell_t12(double x, double h, double halfw, int prec64, int &ii,
+                                         float &f) {
+    double r = np_mod_2pi(x);
+    if (prec64) {
+        double xi = r / h;
+        ii = (int)ceil(xi - halfw);
+        f = (float)(xi - (double)ii);
+    } else {
+        float xi = (float)r / (float)h;
+        ii = (int)ceilf(xi - (float)halfw);
+        f = xi - (float)ii;
+    }
+}
+
 template <int DIM>
 __global__ void k_setpts_t12(int64_t P, D3 x, Geom g, double h0, double h1, double h2,
                              int prec64, I3 i1o, F3 fro, uint32_t *__restrict__ key) {
@@ -50,23 +66,32 @@ __global__ void k_setpts_t12(int64_t P, D3 x, Geom g, double h0, double h1, doub
     uint32_t k = 0;
 #pragma unroll
     for (int d = 0; d < DIM; ++d) {
-        double r = np_mod_2pi(x.p[d][j]);
         int ii;
         float f;
-        if (prec64) {
-            double xi = r / hh[d];
-            ii = (int)ceil(xi - halfw);
-            f = (float)(xi - (double)ii);
-        } else {
-            float xi = (float)r / (float)hh[d];
-            ii = (int)ceilf(xi - (float)halfw);
-            f = xi - (float)ii;
-        }
+        cell_t12(x.p[d][j], hh[d], halfw, prec64, ii, f);
         i1o.p[d][j] = ii;
         fro.p[d][j] = f;
         k = k * (uint32_t)g.nb[d] + (uint32_t)bin_of(ii, g.w / 2, g.n[d], g.m[d]);
     }
     key[j] = k;
+}
+
+// 3D type-1 setup for the z-sweep spread: the same cells and fractions, and
+// the packed point word (zs_word) instead of a bin key.
+__global__ void k_zs_setpts(int64_t P, D3 x, int n0, int n1, int n2, int w, double h0, double h1,
+                            double h2, int prec64, uint32_t *__restrict__ word, F3 fro) {
+    int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= P) return;
+    const double halfw = 0.5 * (double)w;
+    int ix, iy, iz;
+    float fx, fy, fz;
+    cell_t12(x.p[0][j], h0, halfw, prec64, ix, fx);
+    cell_t12(x.p[1][j], h1, halfw, prec64, iy, fy);
+    cell_t12(x.p[2][j], h2, halfw, prec64, iz, fz);
+    word[j] = zs_word(pmod(ix, n0), pmod(iy, n1), pmod(iz, n2), n1, n2, w);
+    fro.p[0][j] = fx;
+    fro.p[1][j] = fy;
+    fro.p[2][j] = fz;
 }
 
 struct T3Src {
@@ -187,6 +212,12 @@ __global__ void k_gather_points(int64_t P, const uint32_t *__restrict__ perm, CI
     if (xin) xout[j] = xin[src];
 }
 
+__global__ void k_permute_c64(int64_t P, const uint32_t *__restrict__ perm,
+                              const float2 *__restrict__ in, float2 *__restrict__ out) {
+    int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j < P) out[j] = in[perm[j]];
+}
+
 inline unsigned blocks_for(int64_t n, int t) { return (unsigned)((n + t - 1) / t); }
 
 }  // namespace
@@ -224,6 +255,39 @@ int mn_setpts_t12(const mn_bins *g, int64_t P, const double *const x[3], int pre
         default: k_setpts_t12<3><<<nb, 256, 0, s>>>(P, xs, k, h[0], h[1], h[2], prec64, io, fo, key); break;
     }
     MN_LAUNCH_CHECK("setpts_t12");
+    return MN_OK;
+}
+
+int mn_zsweep_setpts(const mn_bins *g, int64_t P, const double *const x[3], int prec64,
+                     uint32_t *word, float *const fr[3], mn_stream_t stream) {
+    clear_error();
+    int rc = zsweep_check(g);
+    if (rc) return rc;
+    MN_REQUIRE(P >= 1 && P < (int64_t(1) << 31), "zsweep setpts: P must be in [1, 2^31)");
+    MN_REQUIRE(x && fr && word, "zsweep setpts: NULL pointer");
+    D3 xs{};
+    F3 fo{};
+    double h[3];
+    for (int d = 0; d < 3; ++d) {
+        MN_REQUIRE(x[d] && fr[d], "zsweep setpts: NULL coordinate/output pointer");
+        xs.p[d] = x[d];
+        fo.p[d] = fr[d];
+        h[d] = kTwoPi / (double)g->n[d];
+    }
+    k_zs_setpts<<<blocks_for(P, 256), 256, 0, as_stream(stream)>>>(
+        P, xs, (int)g->n[0], (int)g->n[1], (int)g->n[2], g->w, h[0], h[1], h[2], prec64, word, fo);
+    MN_LAUNCH_CHECK("zsweep_setpts");
+    return MN_OK;
+}
+
+int mn_permute_c64(int64_t P, const uint32_t *perm, const void *in, void *out,
+                   mn_stream_t stream) {
+    clear_error();
+    MN_REQUIRE(P >= 1 && P < (int64_t(1) << 32), "permute: P must be in [1, 2^32)");
+    MN_REQUIRE(perm && in && out && in != out, "permute: NULL or aliased pointer");
+    k_permute_c64<<<blocks_for(P, 256), 256, 0, as_stream(stream)>>>(
+        P, perm, static_cast<const float2 *>(in), static_cast<float2 *>(out));
+    MN_LAUNCH_CHECK("permute_c64");
     return MN_OK;
 }
 

@@ -92,8 +92,12 @@ __global__ void k_tile_scan(uint32_t *__restrict__ d, int64_t n,
 
 // ---------------------------------------------------------- radix sort ----
 
+__device__ __forceinline__ uint32_t digit_of(uint32_t k, uint32_t kmask, int shift) {
+    return ((k & kmask) >> shift) & (RS_RADIX - 1);
+}
+
 __global__ __launch_bounds__(RS_THREADS) void k_radix_hist(const uint32_t *__restrict__ keys,
-                                                           int64_t P, int shift,
+                                                           int64_t P, int shift, uint32_t kmask,
                                                            uint32_t *__restrict__ hist,
                                                            int64_t nblk) {
     __shared__ uint32_t h[RS_RADIX];
@@ -103,53 +107,70 @@ __global__ __launch_bounds__(RS_THREADS) void k_radix_hist(const uint32_t *__res
 #pragma unroll 4
     for (int i = 0; i < RS_ITEMS; ++i) {
         int64_t idx = base + (int64_t)i * RS_THREADS + threadIdx.x;
-        if (idx < P) atomicAdd(&h[(keys[idx] >> shift) & (RS_RADIX - 1)], 1u);
+        if (idx < P) atomicAdd(&h[digit_of(keys[idx], kmask, shift)], 1u);
     }
     __syncthreads();
     hist[(int64_t)threadIdx.x * nblk + blockIdx.x] = h[threadIdx.x];
 }
 
-// Stable scatter of one tile. Elements are visited in index order: 16 rounds
-// of 256 consecutive elements; inside a round, wave w holds elements
-// [64w, 64w+64) and ranks lanes with equal digits by a ballot match.
+struct SortCols {
+    const uint32_t *in[MN_SORT_MAX_COLS];
+    uint32_t *out[MN_SORT_MAX_COLS];
+};
+
+// Stable scatter of one 4096-element tile: the key, its value (the caller
+// index; implicit on the first pass) and up to MN_SORT_MAX_COLS payload
+// columns.
+//  1. Rank: 16 rounds of 256 consecutive elements; in a round wave w holds
+//     [64w, 64w+64) and ranks lanes with equal digits by a ballot match;
+//     run[d] counts the tile's earlier elements of digit d. Index order is
+//     kept, so the pass is stable.
+//  2. The tile's digit counts are scanned into lstart; an element's slot in
+//     the tile-local sorted order is lstart[d] + its rank.
+//  3. Every column goes through LDS: written at the slots, read back in slot
+//     order and stored at gbase[d] + slot - lstart[d], so consecutive lanes
+//     store consecutive addresses inside each digit run.
+// Tiles are mapped XCD-contiguously, so the runs that adjacent tiles write
+// for one digit meet in the same L2 and leave as whole lines.
 __global__ __launch_bounds__(RS_THREADS) void k_radix_scatter(
     const uint32_t *__restrict__ kin, const uint32_t *__restrict__ vin, int64_t P, int shift,
-    const uint32_t *__restrict__ offs, int64_t nblk, uint32_t *__restrict__ kout,
-    uint32_t *__restrict__ vout) {
+    uint32_t kmask, const uint32_t *__restrict__ offs, int64_t nblk,
+    uint32_t *__restrict__ kout, uint32_t *__restrict__ vout, int ncols, SortCols cols) {
     __shared__ uint32_t run[RS_RADIX];
-    __shared__ uint32_t base_off[RS_RADIX];
+    __shared__ uint32_t gbase[RS_RADIX];
     __shared__ uint32_t wcnt[RS_THREADS / 64][RS_RADIX];
+    __shared__ uint32_t stage[RS_TILE];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int64_t tile = xcd_remap(blockIdx.x, nblk);
+    const int64_t base = tile * RS_TILE;
+    const int nvalid = (int)((P - base) < RS_TILE ? (P - base) : RS_TILE);
     run[tid] = 0;
-    base_off[tid] = offs[(int64_t)tid * nblk + blockIdx.x];
+    gbase[tid] = offs[(int64_t)tid * nblk + tile];
 #pragma unroll
     for (int w = 0; w < RS_THREADS / 64; ++w) wcnt[w][tid] = 0;
     __syncthreads();
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    int64_t base = (int64_t)blockIdx.x * RS_TILE;
+    uint32_t kv[RS_ITEMS], rk[RS_ITEMS];
+#pragma unroll
     for (int r = 0; r < RS_ITEMS; ++r) {
-        int64_t idx = base + (int64_t)r * RS_THREADS + tid;
-        bool valid = idx < P;
-        uint32_t k = valid ? kin[idx] : 0u;
-        uint32_t v = valid ? (vin ? vin[idx] : (uint32_t)idx) : 0u;
-        uint32_t dg = (k >> shift) & (RS_RADIX - 1);
+        const int q = r * RS_THREADS + tid;
+        const bool valid = q < nvalid;
+        const uint32_t k = valid ? kin[base + q] : 0u;
+        const uint32_t dg = digit_of(k, kmask, shift);
         uint64_t peers = __ballot(valid);
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
-            bool bit = (dg >> b) & 1u;
-            uint64_t bal = __ballot(bit);
+            const bool bit = (dg >> b) & 1u;
+            const uint64_t bal = __ballot(bit);
             peers &= bit ? bal : ~bal;
         }
-        uint32_t rank = (uint32_t)__popcll(peers & lt_mask);
+        const uint32_t rank = (uint32_t)__popcll(peers & lt_mask);
         if (valid && rank == 0) wcnt[wv][dg] = (uint32_t)__popcll(peers);
         __syncthreads();
-        if (valid) {
-            uint32_t pre = run[dg];
-            for (int w = 0; w < wv; ++w) pre += wcnt[w][dg];
-            uint32_t pos = base_off[dg] + pre + rank;
-            kout[pos] = k;
-            vout[pos] = v;
-        }
+        uint32_t pre = run[dg];
+        for (int w = 0; w < wv; ++w) pre += wcnt[w][dg];
+        kv[r] = k;
+        rk[r] = valid ? ((dg << 16) | (pre + rank)) : 0xFFFFFFFFu;
         __syncthreads();
         uint32_t add = 0;
 #pragma unroll
@@ -158,6 +179,53 @@ __global__ __launch_bounds__(RS_THREADS) void k_radix_scatter(
             wcnt[w][tid] = 0;
         }
         run[tid] += add;
+        __syncthreads();
+    }
+    // Tile-local digit starts (wcnt[0] is free again).
+    uint32_t *lstart = wcnt[0];
+    uint32_t tot;
+    const uint32_t ex = block_excl_scan(run[tid], &tot);
+    lstart[tid] = ex;
+    __syncthreads();
+    int slot[RS_ITEMS];
+#pragma unroll
+    for (int r = 0; r < RS_ITEMS; ++r)
+        slot[r] = rk[r] == 0xFFFFFFFFu ? -1 : (int)(lstart[rk[r] >> 16] + (rk[r] & 0xFFFFu));
+    // Keys: stage, then derive each slot's destination from its digit.
+#pragma unroll
+    for (int r = 0; r < RS_ITEMS; ++r)
+        if (slot[r] >= 0) stage[slot[r]] = kv[r];
+    __syncthreads();
+    uint32_t dst[RS_ITEMS];
+#pragma unroll
+    for (int r = 0; r < RS_ITEMS; ++r) {
+        const int q = r * RS_THREADS + tid;
+        dst[r] = 0;
+        if (q < nvalid) {
+            const uint32_t k = stage[q];
+            const uint32_t d = digit_of(k, kmask, shift);
+            dst[r] = gbase[d] + (uint32_t)q - lstart[d];
+            kout[dst[r]] = k;
+        }
+    }
+    __syncthreads();
+    // Values and payload columns, one LDS round trip each.
+    for (int c = -1; c < ncols; ++c) {
+        const uint32_t *src = c < 0 ? vin : cols.in[c];
+        uint32_t *out = c < 0 ? vout : cols.out[c];
+#pragma unroll
+        for (int r = 0; r < RS_ITEMS; ++r) {
+            if (slot[r] >= 0) {
+                const int64_t idx = base + r * RS_THREADS + tid;
+                stage[slot[r]] = src ? src[idx] : (uint32_t)idx;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < RS_ITEMS; ++r) {
+            const int q = r * RS_THREADS + tid;
+            if (q < nvalid) out[dst[r]] = stage[q];
+        }
         __syncthreads();
     }
 }
@@ -240,10 +308,11 @@ namespace {
 
 struct SortWs {
     uint32_t *kalt, *valt, *hist, *partials;
+    uint32_t *calt[MN_SORT_MAX_COLS];
     int64_t bytes;
 };
 
-SortWs sort_layout(int64_t P, char *base) {
+SortWs sort_layout(int64_t P, int ncols, char *base) {
     int64_t nblk = (P + RS_TILE - 1) / RS_TILE;
     int64_t nh = nblk * RS_RADIX;
     SortWs w{};
@@ -252,6 +321,10 @@ SortWs sort_layout(int64_t P, char *base) {
     off = align_up(off + 4 * P, 256);
     w.valt = reinterpret_cast<uint32_t *>(base + off);
     off = align_up(off + 4 * P, 256);
+    for (int c = 0; c < ncols; ++c) {
+        w.calt[c] = reinterpret_cast<uint32_t *>(base + off);
+        off = align_up(off + 4 * P, 256);
+    }
     w.hist = reinterpret_cast<uint32_t *>(base + off);
     off = align_up(off + 4 * nh, 256);
     w.partials = reinterpret_cast<uint32_t *>(base + off);
@@ -264,41 +337,64 @@ SortWs sort_layout(int64_t P, char *base) {
 
 extern "C" {
 
-int64_t mn_sort_workspace_bytes(int64_t P) {
+int64_t mn_sort_workspace_bytes(int64_t P) { return mn_sort_pairs_workspace_bytes(P, 0); }
+
+int64_t mn_sort_pairs_workspace_bytes(int64_t P, int ncols) {
     if (P < 1) P = 1;
-    return sort_layout(P, nullptr).bytes;
+    if (ncols < 0 || ncols > MN_SORT_MAX_COLS) return -1;
+    return sort_layout(P, ncols, nullptr).bytes;
+}
+
+int mn_sort_pairs(int64_t P, int key_bits, const uint32_t *key_in, uint32_t *key_out,
+                  uint32_t *perm_out, int ncols, const uint32_t *const *cols_in,
+                  uint32_t *const *cols_out, void *ws, int64_t ws_bytes, mn_stream_t stream) {
+    clear_error();
+    MN_REQUIRE(P >= 1 && P < (int64_t(1) << 32), "sort: P must be in [1, 2^32)");
+    MN_REQUIRE(key_bits >= 0 && key_bits <= 32, "sort: key_bits must be in [0, 32]");
+    MN_REQUIRE(ncols >= 0 && ncols <= MN_SORT_MAX_COLS, "sort: ncols out of range");
+    MN_REQUIRE(key_in && key_out && perm_out && ws, "sort: NULL pointer");
+    MN_REQUIRE(key_in != key_out, "sort: key_in and key_out must differ");
+    SortCols user{};
+    for (int c = 0; c < ncols; ++c) {
+        MN_REQUIRE(cols_in && cols_out && cols_in[c] && cols_out[c], "sort: NULL column");
+        MN_REQUIRE(cols_in[c] != cols_out[c], "sort: column in and out must differ");
+        user.in[c] = cols_in[c];
+        user.out[c] = cols_out[c];
+    }
+    SortWs w = sort_layout(P, ncols, static_cast<char *>(ws));
+    MN_REQUIRE(ws_bytes >= w.bytes, "sort: workspace too small");
+    hipStream_t s = as_stream(stream);
+    const int npass = key_bits <= 0 ? 1 : (key_bits + 7) / 8;
+    const uint32_t kmask = key_bits >= 32 ? 0xFFFFFFFFu : ((1u << key_bits) - 1u);
+    const int64_t nblk = (P + RS_TILE - 1) / RS_TILE;
+    const uint32_t *ksrc = key_in;
+    const uint32_t *vsrc = nullptr;  // identity values on the first pass
+    SortCols cur{};
+    for (int c = 0; c < ncols; ++c) cur.in[c] = user.in[c];
+    for (int p = 0; p < npass; ++p) {
+        const bool to_out = ((npass - 1 - p) % 2) == 0;
+        uint32_t *kdst = to_out ? key_out : w.kalt;
+        uint32_t *vdst = to_out ? perm_out : w.valt;
+        for (int c = 0; c < ncols; ++c) cur.out[c] = to_out ? user.out[c] : w.calt[c];
+        const int shift = 8 * p;
+        k_radix_hist<<<(unsigned)nblk, RS_THREADS, 0, s>>>(ksrc, P, shift, kmask, w.hist, nblk);
+        MN_LAUNCH_CHECK("radix hist");
+        int rc = scan_exclusive_u32(w.hist, nblk * RS_RADIX, w.partials, s);
+        if (rc) return rc;
+        k_radix_scatter<<<(unsigned)nblk, RS_THREADS, 0, s>>>(ksrc, vsrc, P, shift, kmask, w.hist,
+                                                             nblk, kdst, vdst, ncols, cur);
+        MN_LAUNCH_CHECK("radix scatter");
+        ksrc = kdst;
+        vsrc = vdst;
+        for (int c = 0; c < ncols; ++c) cur.in[c] = cur.out[c];
+    }
+    return MN_OK;
 }
 
 int mn_sort_keys(int64_t P, int key_bits, const uint32_t *key_in, uint32_t *key_out,
                  uint32_t *perm_out, void *ws, int64_t ws_bytes, mn_stream_t stream) {
-    clear_error();
-    MN_REQUIRE(P >= 1 && P < (int64_t(1) << 32), "sort: P must be in [1, 2^32)");
-    MN_REQUIRE(key_bits >= 0 && key_bits <= 32, "sort: key_bits must be in [0, 32]");
-    MN_REQUIRE(key_in && key_out && perm_out && ws, "sort: NULL pointer");
-    MN_REQUIRE(key_in != key_out, "sort: key_in and key_out must differ");
-    SortWs w = sort_layout(P, static_cast<char *>(ws));
-    MN_REQUIRE(ws_bytes >= w.bytes, "sort: workspace too small");
-    hipStream_t s = as_stream(stream);
-    int npass = key_bits <= 0 ? 1 : (key_bits + 7) / 8;
-    int64_t nblk = (P + RS_TILE - 1) / RS_TILE;
-    const uint32_t *ksrc = key_in;
-    const uint32_t *vsrc = nullptr;  // identity values on the first pass
-    for (int p = 0; p < npass; ++p) {
-        bool to_out = ((npass - 1 - p) % 2) == 0;
-        uint32_t *kdst = to_out ? key_out : w.kalt;
-        uint32_t *vdst = to_out ? perm_out : w.valt;
-        int shift = 8 * p;
-        k_radix_hist<<<(unsigned)nblk, RS_THREADS, 0, s>>>(ksrc, P, shift, w.hist, nblk);
-        MN_LAUNCH_CHECK("radix hist");
-        int rc = scan_exclusive_u32(w.hist, nblk * RS_RADIX, w.partials, s);
-        if (rc) return rc;
-        k_radix_scatter<<<(unsigned)nblk, RS_THREADS, 0, s>>>(ksrc, vsrc, P, shift, w.hist, nblk,
-                                                             kdst, vdst);
-        MN_LAUNCH_CHECK("radix scatter");
-        ksrc = kdst;
-        vsrc = vdst;
-    }
-    return MN_OK;
+    return mn_sort_pairs(P, key_bits, key_in, key_out, perm_out, 0, nullptr, nullptr, ws,
+                         ws_bytes, stream);
 }
 
 int64_t mn_subproblem_workspace_bytes(const mn_bins *g) {

@@ -15,7 +15,9 @@
 // [00, 01, 11, 10]. Block b receives points from itself (all classes) and
 // from its -x, -y and -xy neighbours with the reaching classes; with that
 // order each of the four is one contiguous key range per z, located through
-// zstart[key] (exclusive prefix of key counts).
+// zstart[key] (first sorted index with that key or above). The sorted word
+// (zs_word) carries the first tap's cell inside its block above the key, so
+// the sweep needs no cell indices.
 //
 // Per batch of up to 64 points (two z-steps), a lane-per-point prologue
 // evaluates the ES weights once and writes a table row: the 8 x-weights of
@@ -29,19 +31,12 @@
 namespace mn {
 namespace {
 
-constexpr int ZB = 8;      // block size along x and y (lanes: 8 x 8)
+constexpr int ZB = kZsBlock;  // block size along x and y (lanes: 8 x 8)
 constexpr int ZST = 4;     // z-slices staged in LDS per store
 constexpr int ZCH = 2;     // z-steps per prologue batch
 constexpr int UNR = 4;     // points per unrolled sweep step
 constexpr int NR = 4;      // key ranges per z: own, -x, -y, -xy
 constexpr int REC = 32;    // floats per table row
-
-__device__ __forceinline__ int rel_offset(int i, int n, int base) {
-    int o = pmod(i, n) - base;
-    if (o > n / 2) o -= n;
-    if (o < -n / 2) o += n;
-    return o;
-}
 
 template <int W>
 __device__ __forceinline__ void store_stage(float2 (*stage)[64], float2 *__restrict__ grid,
@@ -68,7 +63,8 @@ __global__ __launch_bounds__(64) void k_spread_zsweep(int n0, int n1, int n2, in
                                                       float inv_hw,
                                                       const int32_t *__restrict__ zstart,
                                                       const uint32_t *__restrict__ perm,
-                                                      CI3s i1s, CF3s frs,
+                                                      const uint32_t *__restrict__ word,
+                                                      CF3s frs,
                                                       const float2 *__restrict__ c,
                                                       const float2 *__restrict__ pre,
                                                       float2 *__restrict__ grid) {
@@ -125,10 +121,14 @@ __global__ __launch_bounds__(64) void k_spread_zsweep(int n0, int n1, int n2, in
                         p0 = pf[q];
                     }
                 const int64_t j = (int64_t)st + (e - p0);
-                const int ox = rel_offset(i1s.p[0][j], n0, ZB * bx);
-                const int oy = rel_offset(i1s.p[1][j], n1, ZB * by);
+                // first tap relative to this block: the word's in-block cell,
+                // minus 8 for points of the -x / -y neighbour blocks
+                const uint32_t wd = word[j];
+                const int r = i % NR;
+                const int ox = (int)((wd >> kZsKeyBits) & 7u) - ((r & 1) ? ZB : 0);
+                const int oy = (int)((wd >> (kZsKeyBits + 3)) & 7u) - ((r & 2) ? ZB : 0);
                 const float fx = frs.p[0][j], fy = frs.p[1][j], fz = frs.p[2][j];
-                float2 cv = c[perm[j]];
+                float2 cv = perm ? c[perm[j]] : c[j];
                 if (pre) {
                     const float2 pv = pre[j];
                     cv = make_float2(cv.x * pv.x - cv.y * pv.y, cv.x * pv.y + cv.y * pv.x);
@@ -206,42 +206,51 @@ __global__ __launch_bounds__(64) void k_spread_zsweep(int n0, int n1, int n2, in
     }
 }
 
-// key = ((bx*nby + by)*n2 + z)*4 + classpos (see the file comment).
-__global__ void k_zsweep_keys(int64_t P, int n0, int n1, int n2, int w, const int32_t *__restrict__ i1x,
-                              const int32_t *__restrict__ i1y, const int32_t *__restrict__ i1z,
-                              uint32_t *__restrict__ key) {
-    int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= P) return;
-    const int x = pmod(i1x[j], n0), y = pmod(i1y[j], n1), z = pmod(i1z[j], n2);
-    const int cut = ZB - (w - 1);
-    const int cx = (x % ZB) >= cut, cy = (y % ZB) >= cut;
-    const int cp = cx ? (cy ? 2 : 3) : (cy ? 1 : 0);
-    const uint32_t blkid = (uint32_t)((x / ZB) * (n1 / ZB) + y / ZB);
-    key[j] = (blkid * (uint32_t)n2 + (uint32_t)z) * 4u + (uint32_t)cp;
+// zstart[k] = first sorted index whose key is >= k, for k in [0, K]: the
+// thread of sorted position j (j in [0, P]) writes j for every key in
+// (key[j-1], key[j]] (from 0 for j = 0, up to K for j = P). Short ranges are
+// written by their lane; long ones (sparse or clustered points) by the whole
+// wave, 64 consecutive entries per store.
+__global__ __launch_bounds__(256) void k_zs_starts(const uint32_t *__restrict__ word, int64_t P,
+                                                   int64_t K, int32_t *__restrict__ zstart) {
+    const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    int64_t lo = 0, hi = -1;  // inclusive key range to fill with j
+    if (j <= P) {
+        lo = (j == 0) ? 0 : (int64_t)(word[j - 1] & kZsKeyMask) + 1;
+        hi = (j == P) ? K : (int64_t)(word[j] & kZsKeyMask);
+    }
+    const bool big = hi - lo >= 16;
+    if (!big)
+        for (int64_t k = lo; k <= hi; ++k) zstart[k] = (int32_t)j;
+    uint64_t todo = __ballot(big);
+    while (todo) {
+        const int src = __ffsll((unsigned long long)todo) - 1;
+        todo &= todo - 1;
+        const int64_t blo = __shfl(lo, src, 64), bhi = __shfl(hi, src, 64);
+        const int32_t v = (int32_t)__shfl(j, src, 64);
+        for (int64_t k = blo + lane; k <= bhi; k += 64) zstart[k] = v;
+    }
 }
 
-__global__ void k_key_hist(const uint32_t *__restrict__ skey, int64_t P, int64_t K,
-                           uint32_t *__restrict__ cnt) {
-    int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= P) return;
-    const uint32_t k = skey[j];
-    if ((int64_t)k < K) atomicAdd(&cnt[k], 1u);
-}
+}  // namespace
 
-inline int zsweep_check(const mn_bins *g) {
+int zsweep_check(const mn_bins *g) {
     MN_REQUIRE(g != nullptr && g->dim == 3, "zsweep: 3D geometry required");
     MN_REQUIRE(g->w >= 2 && g->w <= ZB, "zsweep: kernel width must be in [2, 8]");
     MN_REQUIRE(g->n[0] % ZB == 0 && g->n[1] % ZB == 0, "zsweep: n0, n1 must be multiples of 8");
     MN_REQUIRE(g->n[0] >= 2 * ZB && g->n[1] >= 2 * ZB, "zsweep: n0, n1 must be >= 16");
     MN_REQUIRE(g->n[2] >= g->w && g->n[2] < (int64_t(1) << 24), "zsweep: n2 out of range");
-    const int64_t K = (g->n[0] / ZB) * (g->n[1] / ZB) * g->n[2] * 4;
-    MN_REQUIRE(K < (int64_t(1) << 31), "zsweep: key space too large");
+    MN_REQUIRE(zsweep_nkeys(g) <= (int64_t(1) << kZsKeyBits),
+               "zsweep: key space above 2^26 (n0*n1*n2/16)");
     return MN_OK;
 }
 
-inline int64_t zsweep_nkeys(const mn_bins *g) {
+int64_t zsweep_nkeys(const mn_bins *g) {
     return (g->n[0] / ZB) * (g->n[1] / ZB) * g->n[2] * 4;
 }
+
+namespace {
 
 struct ZArgs {
     const mn_bins *g;
@@ -249,7 +258,7 @@ struct ZArgs {
     int zseg;
     const int32_t *zstart;
     const uint32_t *perm;
-    CI3s i1s;
+    const uint32_t *word;
     CF3s frs;
     const float2 *c, *pre;
     float2 *grid;
@@ -270,7 +279,7 @@ struct ZLaunch {
             const float inv_hw = (float)(2.0 / W);
             k_spread_zsweep<W><<<(unsigned)nw, 64, 0, a.s>>>(n0, n1, n2, nbx, nby, a.zseg, nseg,
                                                              bl2e, inv_hw, a.zstart, a.perm,
-                                                             a.i1s, a.frs, a.c, a.pre, a.grid);
+                                                             a.word, a.frs, a.c, a.pre, a.grid);
             MN_LAUNCH_CHECK("spread_zsweep");
             return MN_OK;
         }
@@ -284,60 +293,38 @@ using namespace mn;
 
 extern "C" {
 
-int mn_zsweep_keys(const mn_bins *g, int64_t P, const int32_t *const i1[3], uint32_t *key,
-                   mn_stream_t stream) {
-    clear_error();
-    int rc = zsweep_check(g);
-    if (rc) return rc;
-    MN_REQUIRE(P >= 1 && P < (int64_t(1) << 31), "zsweep keys: P must be in [1, 2^31)");
-    MN_REQUIRE(i1[0] && i1[1] && i1[2] && key, "zsweep keys: NULL pointer");
-    k_zsweep_keys<<<(unsigned)((P + 255) / 256), 256, 0, as_stream(stream)>>>(
-        P, (int)g->n[0], (int)g->n[1], (int)g->n[2], g->w, i1[0], i1[1], i1[2], key);
-    MN_LAUNCH_CHECK("zsweep_keys");
-    return MN_OK;
-}
-
 int64_t mn_zsweep_nkeys(const mn_bins *g) {
     if (zsweep_check(g)) return -1;
     return zsweep_nkeys(g);
 }
 
-int64_t mn_zsweep_starts_workspace_bytes(const mn_bins *g) {
-    if (zsweep_check(g)) return -1;
-    return 4 * (scan_partials_elems(zsweep_nkeys(g) + 1) + 64);
-}
-
-int mn_zsweep_starts(const mn_bins *g, int64_t P, const uint32_t *sorted_key, int32_t *zstart,
-                     void *ws, int64_t ws_bytes, mn_stream_t stream) {
+int mn_zsweep_starts(const mn_bins *g, int64_t P, const uint32_t *sorted_word, int32_t *zstart,
+                     mn_stream_t stream) {
     clear_error();
     int rc = zsweep_check(g);
     if (rc) return rc;
     MN_REQUIRE(P >= 1 && P < (int64_t(1) << 31), "zsweep starts: P must be in [1, 2^31)");
-    MN_REQUIRE(sorted_key && zstart && ws, "zsweep starts: NULL pointer");
+    MN_REQUIRE(sorted_word && zstart, "zsweep starts: NULL pointer");
     const int64_t K = zsweep_nkeys(g);
-    MN_REQUIRE(ws_bytes >= mn_zsweep_starts_workspace_bytes(g), "zsweep starts: workspace too small");
-    hipStream_t s = as_stream(stream);
-    uint32_t *cnt = reinterpret_cast<uint32_t *>(zstart);
-    rc = fill_zero(cnt, 4 * (K + 1), s);
-    if (rc) return rc;
-    k_key_hist<<<(unsigned)((P + 255) / 256), 256, 0, s>>>(sorted_key, P, K, cnt);
-    MN_LAUNCH_CHECK("zsweep key histogram");
-    return scan_exclusive_u32(cnt, K + 1, static_cast<uint32_t *>(ws), s);
+    k_zs_starts<<<(unsigned)((P + 1 + 255) / 256), 256, 0, as_stream(stream)>>>(sorted_word, P, K,
+                                                                               zstart);
+    MN_LAUNCH_CHECK("zsweep starts");
+    return MN_OK;
 }
 
 int mn_spread_zsweep(const mn_bins *g, float beta, int64_t P, int zseg, const int32_t *zstart,
-                     const uint32_t *perm, const int32_t *const i1s[3], const float *const frs[3],
-                     const void *c, const void *pre, void *grid, mn_stream_t stream) {
+                     const uint32_t *perm, const uint32_t *sorted_word,
+                     const float *const frs[3], const void *c, const void *pre, void *grid,
+                     mn_stream_t stream) {
     clear_error();
     int rc = zsweep_check(g);
     if (rc) return rc;
     MN_REQUIRE(P >= 1 && P < (int64_t(1) << 31), "zsweep spread: P must be in [1, 2^31)");
     MN_REQUIRE(zseg >= 1, "zsweep spread: zseg must be >= 1");
-    MN_REQUIRE(zstart && perm && c && grid, "zsweep spread: NULL pointer");
+    MN_REQUIRE(zstart && sorted_word && c && grid, "zsweep spread: NULL pointer");
     ZArgs a{};
     for (int d = 0; d < 3; ++d) {
-        MN_REQUIRE(i1s[d] && frs[d], "zsweep spread: NULL sorted cell/fraction pointer");
-        a.i1s.p[d] = i1s[d];
+        MN_REQUIRE(frs[d], "zsweep spread: NULL sorted fraction pointer");
         a.frs.p[d] = frs[d];
     }
     a.g = g;
@@ -345,6 +332,7 @@ int mn_spread_zsweep(const mn_bins *g, float beta, int64_t P, int zseg, const in
     a.zseg = zseg;
     a.zstart = zstart;
     a.perm = perm;
+    a.word = sorted_word;
     a.c = static_cast<const float2 *>(c);
     a.pre = static_cast<const float2 *>(pre);
     a.grid = static_cast<float2 *>(grid);

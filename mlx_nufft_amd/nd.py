@@ -109,14 +109,15 @@ class _PointsND:
 
     def _set_points(self, x64):
         tm = self._timer()
-        with tm("setpts"):
-            i1, fr, key = E.setpts_t12(self.bins, x64, self.prec == "crit64")
-        with tm("sort+tables"):
-            if self._zsweep:
-                del key
-                self.pts = E.ZSweepPoints(self._zbins, i1, fr)
-            else:
+        if self._zsweep:
+            with tm("setpts+sort+tables"):
+                self.pts = E.ZSweepPoints(self._zbins, x64, self.prec == "crit64")
+        else:
+            with tm("setpts"):
+                i1, fr, key = E.setpts_t12(self.bins, x64, self.prec == "crit64")
+            with tm("sort+tables"):
                 self.pts = E.SortedPoints(self.bins, i1, fr, key)
+                del i1, fr, key
         self.sorted = True
         self._od = True
         self._finish_profile(tm)

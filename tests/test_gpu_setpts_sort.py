@@ -93,6 +93,33 @@ def test_sort_matches_numpy_stable(case, oracle):
     assert np.array_equal(oracle.stable_sort(ko, nk), ref.astype(np.uint32))
 
 
+@pytest.mark.parametrize("P,nbits,ncols", [(1, 5, 3), (4095, 7, 0), (4097, 12, 1),
+                                             (300_001, 23, 3), (1_000_000, 32, 8),
+                                             (65_536, 16, 6)])
+def test_sort_pairs_payload(P, nbits, ncols):
+    """Stable sort on the low nbits of each key, bits above nbits travelling
+    with the key, and payload columns following their keys: against numpy's
+    stable argsort."""
+    from mlx_nufft_amd import _engine as E
+
+    print(f"case sort_pairs P={P} nbits={nbits} ncols={ncols}", flush=True)
+    rng = np.random.default_rng(P + nbits)
+    key = rng.integers(0, 1 << 32, P, dtype=np.uint64).astype(np.uint32)
+    low = key & np.uint32(0xFFFFFFFF if nbits == 32 else (1 << nbits) - 1)
+    if nbits >= 12:   # many ties
+        low[rng.integers(0, P, P // 3)] = low[0]
+        key = (key & ~np.uint32((1 << nbits) - 1 if nbits < 32 else 0xFFFFFFFF)) | low
+    cols = [rng.integers(-2**31, 2**31, P, dtype=np.int64).astype(np.int32) for _ in range(ncols)]
+    ref = np.argsort(low, kind="stable")
+    kd = torch.from_numpy(key.view(np.int32)).cuda()
+    cd = [torch.from_numpy(c).cuda() for c in cols]
+    skey, perm, outs = E.sort_pairs(kd, nbits, cd)
+    assert np.array_equal(perm.cpu().numpy().view(np.uint32), ref.astype(np.uint32))
+    assert np.array_equal(skey.cpu().numpy().view(np.uint32), key[ref])
+    for c, o in zip(cols, outs):
+        assert np.array_equal(o.cpu().numpy(), c[ref])
+
+
 @pytest.mark.parametrize("msub", [1024, 7])
 def test_subproblem_table(msub, oracle):
     from mlx_nufft_amd import _engine as E

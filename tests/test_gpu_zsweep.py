@@ -1,12 +1,14 @@
 """GPU checks of the owner-computes z-sweep spread.
 
-* keys and the key start table bit-exact against a numpy restatement of the
-  layout (block of the first tap, z, reach class in [00, 01, 11, 10] order);
+* point words (key: block of the first tap, z, reach class in [00, 01, 11,
+  10] order; in-block x/y cell above it), sorted fractions, perm and the key
+  start table bit-exact against a numpy restatement;
 * the spread grid against the oracle's fp64 spread on the same (i1, fr) for
   edge geometries: clustered points (more than 64 points per z-step of one
   block), 16-wide grids (the -x/-y neighbour block wraps), a z extent that
   is not a multiple of the segment, and w = 2..8;
-* z-sweep == LDS-tile spread on the same plan inputs.
+* z-sweep == LDS-tile spread on the same plan inputs, with strengths read
+  through perm or pre-permuted into sorted order.
 """
 
 import numpy as np
@@ -16,31 +18,51 @@ import torch
 pytestmark = pytest.mark.gpu
 
 
-def _keys_numpy(i1, n, w):
+def _words_numpy(i1, n, w):
+    """The z-sweep point word: key ((bx*nby + by)*n2 + z)*4 + class in bits
+    0-25, the in-block x / y cell of the first tap in bits 26-28 / 29-31."""
     x, y, z = (i1[d].astype(np.int64) % n[d] for d in range(3))
     cut = 8 - (w - 1)
     cx, cy = (x % 8) >= cut, (y % 8) >= cut
     cp = np.where(cx, np.where(cy, 2, 3), np.where(cy, 1, 0))
     blk = (x // 8) * (n[1] // 8) + y // 8
-    return ((blk * n[2] + z) * 4 + cp).astype(np.uint32), (n[0] // 8) * (n[1] // 8) * n[2] * 4
+    key = (blk * n[2] + z) * 4 + cp
+    word = key | ((x % 8) << 26) | ((y % 8) << 29)
+    return key.astype(np.uint32), word.astype(np.uint32), (n[0] // 8) * (n[1] // 8) * n[2] * 4
 
 
 @pytest.mark.parametrize("N,eps", [((32, 24, 20), 1e-5), ((8, 8, 20), 1e-3), ((64, 64, 64), 1e-6)])
-def test_zsweep_keys_and_starts(N, eps, oracle, mn):
-    print(f"case zsweep keys N={N} eps={eps}", flush=True)
+def test_zsweep_words_sort_and_starts(N, eps, oracle, mn):
+    """Words, sorted fractions and perm bit-exact; zstart[k] = first sorted
+    index with key >= k."""
+    print(f"case zsweep words N={N} eps={eps}", flush=True)
     rng = np.random.default_rng(21)
     M = 50_000
     x = [rng.uniform(-np.pi, np.pi, M) for _ in range(3)]
+    x[0][:4] = [-np.pi, np.pi, 0.0, -1e-300]   # fold edges
     p = mn.Type1PlanND(tuple(x), N, eps=eps)
     assert p.pts.kind == "zsweep"
-    i1o, _ = oracle.setpts_t12(x, p.n_up, p.w)
-    key, K = _keys_numpy(i1o, p.n_up, p.w)
+    i1o, fro = oracle.setpts_t12(x, p.n_up, p.w)
+    key, word, K = _words_numpy(i1o, p.n_up, p.w)
     ref = np.argsort(key, kind="stable")
-    assert np.array_equal(p.pts.perm.cpu().numpy().view(np.uint32), ref.astype(np.uint32))
+    perm = p.pts.perm.cpu().numpy().view(np.uint32)
+    assert np.array_equal(perm, ref.astype(np.uint32))
+    assert np.array_equal(p.pts.word.cpu().numpy().view(np.uint32), word[ref])
+    assert np.array_equal(p.pts.frs.cpu().numpy().view(np.int32), fro[:, ref].view(np.int32))
     zs = p.pts.zstart.cpu().numpy().astype(np.int64)
-    exp = np.zeros(K + 1, np.int64)
-    exp[1:] = np.cumsum(np.bincount(key.astype(np.int64), minlength=K))
+    exp = np.searchsorted(key[ref], np.arange(K + 1), side="left")
     assert np.array_equal(zs, exp)
+
+
+def test_zsweep_starts_sparse(mn):
+    """Few points far apart: long key gaps, filled by whole waves."""
+    print("case zsweep sparse starts", flush=True)
+    rng = np.random.default_rng(26)
+    x = [rng.uniform(-np.pi, np.pi, 7) for _ in range(3)]
+    p = mn.Type1PlanND(tuple(x), (64, 64, 64), eps=1e-5)
+    key = p.pts.word.cpu().numpy().view(np.uint32) & ((1 << 26) - 1)
+    zs = p.pts.zstart.cpu().numpy().astype(np.int64)
+    assert np.array_equal(zs, np.searchsorted(key, np.arange(p.pts.K + 1), side="left"))
 
 
 def _grid_check(oracle, mn, x, c, N, eps, tol=1e-5):
@@ -110,3 +132,9 @@ def test_zsweep_matches_tiles(mn, monkeypatch):
     E.spread_zsweep(pz.pts, pz.beta, c, gz)
     E.spread(pt.pts, pt.beta, c, gt)
     assert float((gz - gt).abs().norm() / gt.abs().norm()) < 1e-6
+    cs = torch.empty_like(c)
+    E.permute_c64(pz.pts.perm, c, cs)
+    assert torch.equal(cs, c[pz.pts.perm.long()])
+    gp = torch.empty_like(gz)
+    E.spread_zsweep(pz.pts, pz.beta, cs, gp, presorted=True)
+    assert torch.equal(gp, gz)

@@ -57,7 +57,14 @@ def test_pure_queries(clib):
 
     g = _lib.Bins.make(3, 6, [512, 512, 512], [8, 8, 1])
     assert clib.mn_zsweep_nkeys(ctypes.byref(g)) == 64 * 64 * 512 * 4
-    assert clib.mn_zsweep_starts_workspace_bytes(ctypes.byref(g)) > 4 * 64 * 64 * 512 * 4 // 2048
+    # payload columns add one P-length alternate buffer each
+    assert (clib.mn_sort_pairs_workspace_bytes(1 << 20, 3)
+            >= clib.mn_sort_pairs_workspace_bytes(1 << 20, 0) + 3 * 4 * (1 << 20))
+    assert clib.mn_sort_pairs_workspace_bytes(1000, 9) == -1
+    # the z-sweep key space is capped at 2^26 keys
+    assert clib.mn_zsweep_nkeys(ctypes.byref(_lib.Bins.make(3, 6, [1024] * 3, [8, 8, 1]))) == 1 << 26
+    assert clib.mn_zsweep_nkeys(ctypes.byref(_lib.Bins.make(3, 6, [1024, 1024, 1040],
+                                                            [8, 8, 1]))) == -1
     assert clib.mn_subproblem_workspace_bytes(ctypes.byref(_lib.Bins.make(3, 6, [64] * 3,
                                                                           [11] * 3))) > 0
     # z-sweep geometry limits: w <= 8, n0 and n1 multiples of 8
@@ -113,6 +120,8 @@ def test_engine_bin_geometry(monkeypatch):
     assert not E.zsweep_eligible(3, 9, [512, 512, 512])
     assert not E.zsweep_eligible(3, 6, [514, 512, 512])
     assert not E.zsweep_eligible(2, 6, [512, 512])
+    assert E.zsweep_eligible(3, 6, [1024] * 3)
+    assert not E.zsweep_eligible(3, 6, [1024, 1024, 1040])
     g = E.make_bins(3, 6, [512] * 3, m=(8, 8, 1))
     assert E.key_bits(g) == (64 * 64 * 512 - 1).bit_length()
 
