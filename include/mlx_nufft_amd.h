@@ -291,6 +291,30 @@ int mn_expi(int ncomp, const double *const *comps, int64_t n, int isign,
  */
 int mn_fft_exec(int dim, const int64_t n[3], int64_t batch, int isign,
                 void *data, mn_stream_t stream);
+
+/*
+ * Pruned, deconvolving FFTs for power-of-two fine grids (16 <= n[d] <= 4096;
+ * mn_fftp_supported). One pass per axis transforms that axis's lines and
+ * keeps (type 1) or fills (type 2) only the N[d] modes of modeord 0
+ * (k = i - N[d]/2 at FFT index k mod n[d]), multiplied by dec[d][i]:
+ *   mn_fft_crop_deconv: fk = crop(FFT(grid)) * dec0 x dec1 x dec2; grid is
+ *     read only (batch grids of prod n -> batch mode boxes of prod N);
+ *   mn_pad_deconv_fft:  grid = FFT(pad(fk * dec0 x dec1 x dec2)).
+ * isign > 0 is the unnormalised e^{+i} transform, isign < 0 e^{-i}. work
+ * (device) holds the intermediate arrays: mn_fftp_work_bytes(...) bytes,
+ * 8*batch*(n0*n1*N2 + n0*N1*N2) in 3D. Replaces FFT + crop (or pad + FFT):
+ * at n = 2N a 3D type-1 pass set moves 2.8 GB instead of 8.9 GB.
+ * ref: nd.py:374-383 (_fft_grid), nd.py:416-435 (crop/deconv kernel),
+ * nd.py:878-906 (pad/deconv), gpu_t3.py:94-148 (fft_axis).
+ */
+int mn_fftp_supported(int dim, const int64_t n[3]);
+int64_t mn_fftp_work_bytes(int dim, const int64_t n[3], const int64_t N[3], int64_t batch);
+int mn_fft_crop_deconv(int dim, const int64_t n_up[3], const int64_t N[3], int64_t batch,
+                       int isign, const void *grid, const float *const dec[3], void *work,
+                       int64_t work_bytes, void *fk, mn_stream_t stream);
+int mn_pad_deconv_fft(int dim, const int64_t n_up[3], const int64_t N[3], int64_t batch,
+                      int isign, const void *fk, const float *const dec[3], void *work,
+                      int64_t work_bytes, void *grid, mn_stream_t stream);
 /* Destroy all cached FFT plans (call with no transform in flight). */
 int mn_fft_cache_clear(void);
 

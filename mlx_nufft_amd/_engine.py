@@ -271,6 +271,34 @@ def pad_deconv(n_up, N, fk, decs, grid, batch=1):
                                   L.ptr3(decs), L.ptr(grid), L.stream()), "pad_deconv")
 
 
+def fftp_supported(n_up):
+    """True when the pruned per-axis FFT applies (power-of-two fine grid
+    sizes in [16, 4096]); MN_FFT=rocfft forces full rocFFT + crop/pad."""
+    if os.environ.get("MN_FFT", "") == "rocfft":
+        return False
+    return bool(L.lib().mn_fftp_supported(len(n_up), L.i64x3(n_up)))
+
+
+def fftp_work_bytes(n_up, N, batch=1):
+    return int(L.lib().mn_fftp_work_bytes(len(N), L.i64x3(n_up), L.i64x3(N), int(batch)))
+
+
+def fft_crop_deconv(n_up, N, grid, decs, fk, isign, work, batch=1):
+    """fk = crop(FFT(grid)) * prod_d dec_d with the pruned per-axis FFT."""
+    L.check(L.lib().mn_fft_crop_deconv(len(N), L.i64x3(n_up), L.i64x3(N), int(batch), int(isign),
+                                       L.ptr(grid), L.ptr3(decs), L.ptr(work),
+                                       0 if work is None else work.numel(), L.ptr(fk),
+                                       L.stream()), "fft_crop_deconv")
+
+
+def pad_deconv_fft(n_up, N, fk, decs, grid, isign, work, batch=1):
+    """grid = FFT(pad(fk * prod_d dec_d)) with the pruned per-axis FFT."""
+    L.check(L.lib().mn_pad_deconv_fft(len(N), L.i64x3(n_up), L.i64x3(N), int(batch), int(isign),
+                                      L.ptr(fk), L.ptr3(decs), L.ptr(work),
+                                      0 if work is None else work.numel(), L.ptr(grid),
+                                      L.stream()), "pad_deconv_fft")
+
+
 def fft(grid, n_up, isign, batch=1):
     L.check(L.lib().mn_fft_exec(len(n_up), L.i64x3(n_up), int(batch), int(isign), L.ptr(grid),
                                 L.stream()), "fft")

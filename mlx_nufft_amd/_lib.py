@@ -86,6 +86,12 @@ _SIGS = [
     ("mn_expi", c_int, [c_int, ctypes.POINTER(c_vp), c_int64, c_int, c_vp, c_vp]),
     ("mn_fft_exec", c_int, [c_int, I64x3, c_int64, c_int, c_vp, c_vp]),
     ("mn_fft_cache_clear", c_int, []),
+    ("mn_fftp_supported", c_int, [c_int, I64x3]),
+    ("mn_fftp_work_bytes", c_int64, [c_int, I64x3, I64x3, c_int64]),
+    ("mn_fft_crop_deconv", c_int, [c_int, I64x3, I64x3, c_int64, c_int, c_vp, VP3, c_vp, c_int64,
+                                   c_vp, c_vp]),
+    ("mn_pad_deconv_fft", c_int, [c_int, I64x3, I64x3, c_int64, c_int, c_vp, VP3, c_vp, c_int64,
+                                  c_vp, c_vp]),
     ("mn_fill_zero", c_int, [c_vp, c_int64, c_vp]),
 ]
 

@@ -8,11 +8,12 @@ with k_d in [-(N_d//2), (N_d-1)//2] (modeord=0, even or odd N_d) and any x
 (ref: mlx_nufft/nd.py:94-1119): the constructor is setpts, execute runs
 the transform; all device work is HIP kernels behind the C-ABI.
 
-Pipeline (type 1): fp64 setpts (fold, rescale, cell/frac, bin key) ->
-stable radix bin sort -> subproblem table -> LDS-tiled ES spread with halo
-flush -> rocFFT (unnormalised; backward for isign>0) -> fused mode shuffle
-+ deconvolution. Type 2 runs the adjoint chain: pad+deconvolve -> FFT ->
-LDS-tiled interpolation written straight to caller order.
+Pipeline (type 1): fp64 setpts (fold, rescale, cell/frac, sort key) ->
+stable radix sort carrying the point data -> ES spread (3D: owner-computes
+z-sweep, no atomics; otherwise LDS tiles flushed with atomics) -> FFT with
+the mode crop and deconvolution fused (pruned per-axis FFT on power-of-two
+grids, else rocFFT + crop). Type 2 runs the adjoint chain: deconvolve +
+zero-pad + FFT -> LDS-tiled interpolation written straight to caller order.
 """
 
 import numpy as np
@@ -81,6 +82,8 @@ class _PointsND:
             self.decs.append(1.0 / kernel_ft(2.0 * PI * k / self.n_up[d], self.beta, self.w))
         self.dev_dec = [torch.from_numpy(v.astype(np.float32)).to(self.device) for v in self.decs]
         self._grid = None
+        self._pruned = E.fftp_supported(self.n_up)
+        self._work = None
 
     # -- point state -------------------------------------------------------
 
@@ -139,6 +142,16 @@ class _PointsND:
             self._grid = torch.empty(shape, dtype=torch.complex64, device=self.device)
         return self._grid
 
+    def _fft_work(self, batch=1):
+        """Work buffer of the pruned FFT (intermediate per-axis arrays)."""
+        nbytes = E.fftp_work_bytes(self.n_up, self.N, batch)
+        if nbytes <= 0:
+            return None
+        if self._work is None or self._work.numel() < nbytes:
+            self._work = None
+            self._work = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        return self._work
+
     def _timer(self):
         return E.StageTimer(self.profile)
 
@@ -183,12 +196,20 @@ class Type1PlanND(_PointsND):
                 E.fill_zero(grid)
             with tm("spread"):
                 E.spread(self.pts, self.beta, cd, grid, accumulate=True)
-        with tm("fft"):
-            E.fft(grid, self.n_up, self.isign)
-        with tm("deconv"):
-            E.crop_deconv(self.n_up, self.N, grid, self.dev_dec, fk)
+        self._fft_crop(grid, fk, tm, 1)
         self._finish_profile(tm)
         return L.to_host(fk) if return_np else fk
+
+    def _fft_crop(self, grid, fk, tm, batch):
+        if self._pruned:
+            with tm("fft"):
+                E.fft_crop_deconv(self.n_up, self.N, grid, self.dev_dec, fk, self.isign,
+                                  self._fft_work(batch), batch=batch)
+            return
+        with tm("fft"):
+            E.fft(grid, self.n_up, self.isign, batch=batch)
+        with tm("deconv"):
+            E.crop_deconv(self.n_up, self.N, grid, self.dev_dec, fk, batch=batch)
 
     def execute_batch(self, cs, return_np=True):
         """B strength vectors over the same points: one shared spread (ES
@@ -212,10 +233,7 @@ class Type1PlanND(_PointsND):
                     E.spread_zsweep(self.pts, self.beta, cd[b], grids[b])
             else:
                 E.spread_batch(self.pts, self.beta, cd, grids)
-        with tm("fft"):
-            E.fft(grids, self.n_up, self.isign, batch=B)
-        with tm("deconv"):
-            E.crop_deconv(self.n_up, self.N, grids, self.dev_dec, fk, batch=B)
+        self._fft_crop(grids, fk, tm, B)
         self._finish_profile(tm)
         return L.to_host(fk) if return_np else fk
 
@@ -281,10 +299,15 @@ class Type2PlanND(_PointsND):
         grid = self._fine_grid(1)
         out = torch.empty(self.P, dtype=torch.complex64, device=self.device)
         tm = self._timer()
-        with tm("deconv"):
-            E.pad_deconv(self.n_up, self.N, fd, self.dev_dec, grid)
-        with tm("fft"):
-            E.fft(grid, self.n_up, self.isign)
+        if self._pruned:
+            with tm("fft"):
+                E.pad_deconv_fft(self.n_up, self.N, fd, self.dev_dec, grid, self.isign,
+                                 self._fft_work(1))
+        else:
+            with tm("deconv"):
+                E.pad_deconv(self.n_up, self.N, fd, self.dev_dec, grid)
+            with tm("fft"):
+                E.fft(grid, self.n_up, self.isign)
         with tm("interp"):
             E.interp(self.pts, self.beta, grid, out)
         self._finish_profile(tm)

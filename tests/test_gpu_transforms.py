@@ -14,8 +14,10 @@ import torch
 
 pytestmark = pytest.mark.gpu
 
+# fine grids: 180, 8192, 96x72, 90x68, 48x40x32, 42x36x28 (rocFFT + crop/pad) and
+# 128, 128x64, 64x32x128 (pruned per-axis FFT, even and odd mode counts)
 CASES = [(1, (87,)), (1, (4096,)), (2, (48, 36)), (2, (45, 34)), (3, (24, 20, 16)),
-         (3, (21, 18, 14))]
+         (3, (21, 18, 14)), (1, (63,)), (2, (64, 31)), (3, (31, 16, 63))]
 
 
 def _pts(rng, dim, M):
@@ -215,3 +217,65 @@ def test_adjoint_identity(dim, N, mn):
     rhs = np.vdot(t2.astype(np.complex128), c.astype(np.complex128))
     scale = np.linalg.norm(t1) * np.linalg.norm(f)
     assert abs(lhs - rhs) / scale < 1e-5
+
+
+@pytest.mark.parametrize("dim,N,B", [(1, (63,), 1), (1, (2048,), 2), (2, (64, 31), 3),
+                                     (2, (1024, 512), 1), (3, (31, 16, 63), 2),
+                                     (3, (128, 128, 128), 1), (3, (8, 8, 8), 1)])
+@pytest.mark.parametrize("isign", [+1, -1])
+def test_pruned_fft_vs_numpy(dim, N, B, isign, mn):
+    """The pruned per-axis FFT against numpy: crop(FFT(grid)) * dec and
+    FFT(pad(fk * dec)), batched, even and odd mode counts."""
+    from mlx_nufft_amd import _engine as E
+
+    print(f"case pruned fft dim={dim} N={N} B={B} isign={isign}", flush=True)
+    rng = np.random.default_rng(15)
+    n_up = [next_pow2 for next_pow2 in (1 << int(np.ceil(np.log2(max(16, 2 * n)))) for n in N)]
+    assert E.fftp_supported(n_up)
+    decs = [rng.uniform(0.5, 2.0, n).astype(np.float32) for n in N]
+    dd = [torch.from_numpy(d).cuda() for d in decs]
+    work = torch.empty(max(1, E.fftp_work_bytes(n_up, N, B)), dtype=torch.uint8, device="cuda")
+    grid = _cplx(rng, (B, *n_up))
+    fk = torch.empty((B, *N), dtype=torch.complex64, device="cuda")
+    E.fft_crop_deconv(n_up, N, torch.from_numpy(grid).cuda(), dd, fk, isign, work, batch=B)
+    axes = tuple(range(1, dim + 1))
+    G = grid.astype(np.complex128)
+    F = np.fft.ifftn(G, axes=axes) * np.prod(n_up) if isign > 0 else np.fft.fftn(G, axes=axes)
+    idx = np.ix_(range(B), *[np.arange(-(n // 2), n - n // 2) % m for n, m in zip(N, n_up)])
+    dec = decs[0].astype(np.float64)
+    for d in decs[1:]:
+        dec = np.multiply.outer(dec, d.astype(np.float64))
+    ref = F[idx] * dec
+    got = fk.cpu().numpy()
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 3e-6
+    # type-2 direction
+    f2 = _cplx(rng, (B, *N))
+    g2 = torch.empty((B, *n_up), dtype=torch.complex64, device="cuda")
+    E.pad_deconv_fft(n_up, N, torch.from_numpy(f2).cuda(), dd, g2, isign, work, batch=B)
+    H = np.zeros((B, *n_up), np.complex128)
+    H[idx] = f2 * dec
+    R = np.fft.ifftn(H, axes=axes) * np.prod(n_up) if isign > 0 else np.fft.fftn(H, axes=axes)
+    got2 = g2.cpu().numpy()
+    assert np.linalg.norm(got2 - R) / np.linalg.norm(R) < 3e-6
+
+
+def test_pruned_equals_rocfft_path(mn, monkeypatch):
+    """Type-1 and type-2 plans give the same result through the pruned FFT
+    and through rocFFT + crop/pad."""
+    print("case pruned vs rocfft plans", flush=True)
+    rng = np.random.default_rng(16)
+    M, N = 100_000, (32, 64, 16)
+    x = _pts(rng, 3, M)
+    c = _cplx(rng, M)
+    fk = _cplx(rng, N)
+    p1 = mn.Type1PlanND(tuple(x), N, eps=1e-5)
+    p2 = mn.Type2PlanND(tuple(x), N, eps=1e-5)
+    assert p1._pruned and p2._pruned
+    a1, a2 = p1.execute(c), p2.execute(fk)
+    monkeypatch.setenv("MN_FFT", "rocfft")
+    q1 = mn.Type1PlanND(tuple(x), N, eps=1e-5)
+    q2 = mn.Type2PlanND(tuple(x), N, eps=1e-5)
+    assert not q1._pruned and not q2._pruned
+    b1, b2 = q1.execute(c), q2.execute(fk)
+    assert np.linalg.norm(a1 - b1) / np.linalg.norm(b1) < 2e-6
+    assert np.linalg.norm(a2 - b2) / np.linalg.norm(b2) < 2e-6
