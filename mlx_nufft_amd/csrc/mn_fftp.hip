@@ -26,6 +26,8 @@
 // deconvolution), gpu_t3.py:94-148 (fft_axis).
 #include "mn_common.h"
 
+#include <stdlib.h>
+
 namespace mn {
 namespace {
 
@@ -92,55 +94,28 @@ __device__ __forceinline__ void dft(float2 *v) {
     else dft2<S>(v);
 }
 
-// One Stockham stage of radix R over TI lines of length N in buf
-// (element l of line t at buf[l*TI + t]); Ns = product of the radices of
-// the earlier stages. tw[m] = exp(S 2 pi i m / N).
-template <int N, int TI, int R, int S>
-__device__ __forceinline__ void stage(float2 *buf, const float2 *tw, int Ns) {
-    constexpr int NB = (N / R) * TI;  // butterflies in the tile
-    constexpr int MB = (NB + FP_THREADS - 1) / FP_THREADS;
-    float2 v[MB][R];
-#pragma unroll
-    for (int m = 0; m < MB; ++m) {
-        const int b = threadIdx.x + m * FP_THREADS;
-        if (b < NB) {
-            const int t = b % TI, j = b / TI, k = j & (Ns - 1);
-            const int tstep = N / (Ns * R);
-#pragma unroll
-            for (int r = 0; r < R; ++r) v[m][r] = buf[(j + r * (N / R)) * TI + t];
-            if (Ns > 1) {
-#pragma unroll
-                for (int r = 1; r < R; ++r) v[m][r] = cmul(v[m][r], tw[k * r * tstep]);
-            }
-            dft<R, S>(v[m]);
-        }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int m = 0; m < MB; ++m) {
-        const int b = threadIdx.x + m * FP_THREADS;
-        if (b < NB) {
-            const int t = b % TI, j = b / TI, k = j & (Ns - 1);
-            const int base = (j - k) * R + k;
-#pragma unroll
-            for (int r = 0; r < R; ++r) buf[(base + r * Ns) * TI + t] = v[m][r];
-        }
-    }
-    __syncthreads();
+// LDS slot of element l of line t in a tile of TI lines: rows of TI values,
+// the column XOR-swizzled by the row so that both access patterns -- TI
+// lines side by side (t fastest) and one line walked along l (l fastest) --
+// spread over the LDS banks.
+template <int TI>
+__device__ __forceinline__ int lds_at(int l, int t) {
+    constexpr int SH = TI >= 16 ? 0 : (TI >= 8 ? 1 : (TI >= 4 ? 2 : (TI >= 2 ? 3 : 4)));
+    return l * TI + (t ^ ((l >> SH) & (TI - 1)));
 }
 
-template <int LOGN, int TI, int S>
-__device__ __forceinline__ void fft_lines(float2 *buf, const float2 *tw) {
-    constexpr int N = 1 << LOGN;
-    constexpr int N8 = LOGN / 3, REM = LOGN % 3;
-    int Ns = 1;
-#pragma unroll
-    for (int s = 0; s < N8; ++s) {
-        stage<N, TI, 8, S>(buf, tw, Ns);
-        Ns *= 8;
+// Butterfly b of a stage with NJ butterflies per line: (line t, index j).
+// Contiguous lines put j fastest across lanes, strided ones t fastest, so
+// that the global accesses of the first and last stages coalesce.
+template <int TI, int NJ>
+__device__ __forceinline__ void bfly_of(int b, bool contig, int &t, int &j) {
+    if (contig) {
+        t = b / NJ;
+        j = b % NJ;
+    } else {
+        t = b % TI;
+        j = b / TI;
     }
-    if constexpr (REM == 2) stage<N, TI, 4, S>(buf, tw, Ns);
-    if constexpr (REM == 1) stage<N, TI, 2, S>(buf, tw, Ns);
 }
 
 struct AxisArgs {
@@ -155,18 +130,67 @@ __device__ __forceinline__ int64_t line_base(int64_t line, int64_t inner, int L)
     return (line / inner) * (int64_t)L * inner + line % inner;
 }
 
+// Mode index i in [0, M) of FFT position p, or -1 if p is not kept.
+template <int N>
+__device__ __forceinline__ int mode_of(int p, int M, int hM) {
+    if (p < M - hM) return p + hM;
+    if (p >= N - hM) return p - (N - hM);
+    return -1;
+}
+
+// Middle Stockham stage of radix R (LDS to LDS); Ns = product of the radices
+// of the earlier stages; tw[m] = exp(S 2 pi i m / N).
+template <int N, int TI, int R, int S>
+__device__ __forceinline__ void stage(float2 *buf, const float2 *tw, int Ns) {
+    constexpr int NJ = N / R, NB = NJ * TI;
+    constexpr int MB = (NB + FP_THREADS - 1) / FP_THREADS;
+    float2 v[MB][R];
+    const int tstep = N / (Ns * R);
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+        const int b = threadIdx.x + m * FP_THREADS;
+        if (b < NB) {
+            const int t = b % TI, j = b / TI, k = j & (Ns - 1);
+#pragma unroll
+            for (int r = 0; r < R; ++r) v[m][r] = buf[lds_at<TI>(j + r * NJ, t)];
+#pragma unroll
+            for (int r = 1; r < R; ++r) v[m][r] = cmul(v[m][r], tw[k * r * tstep]);
+            dft<R, S>(v[m]);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+        const int b = threadIdx.x + m * FP_THREADS;
+        if (b < NB) {
+            const int t = b % TI, j = b / TI, k = j & (Ns - 1);
+            const int base = (j - k) * R + k;
+#pragma unroll
+            for (int r = 0; r < R; ++r) buf[lds_at<TI>(base + r * Ns, t)] = v[m][r];
+        }
+    }
+    __syncthreads();
+}
+
 // PRUNE_OUT: full n-point lines in, M modes out (type 1).
 // otherwise: M modes in (zero elsewhere), full n-point lines out (type 2).
+// The first radix-8 stage reads its inputs straight from global memory and
+// the last stage writes its outputs straight back; LDS carries the stages
+// in between.
 template <int LOGN, int TI, int S, bool PRUNE_OUT>
 __global__ __launch_bounds__(FP_THREADS) void k_fft_axis(const float2 *__restrict__ in,
                                                          float2 *__restrict__ out, AxisArgs a) {
     constexpr int N = 1 << LOGN;
+    constexpr int N8 = LOGN / 3, REM = LOGN % 3;
+    constexpr int RL = REM == 0 ? 8 : (REM == 1 ? 2 : 4);  // radix of the last stage
+    static_assert(LOGN >= 4, "n >= 16");
     __shared__ float2 buf[N * TI];
     __shared__ float2 tw[N];
     __shared__ int64_t lbi[TI], lbo[TI];  // line bases in and out (-1: past the end)
     const int tid = threadIdx.x;
     const int64_t ntile = (a.nlines + TI - 1) / TI;
     const int64_t line0 = xcd_remap(blockIdx.x, ntile) * TI;
+    const bool contig = a.inner == 1;  // the lines are contiguous rows
     for (int m = tid; m < N; m += FP_THREADS) {
         double sn, cs;
         sincospi(2.0 * (double)m / (double)N, &sn, &cs);
@@ -178,52 +202,91 @@ __global__ __launch_bounds__(FP_THREADS) void k_fft_axis(const float2 *__restric
         lbi[tid] = ok ? line_base(line, a.inner, a.Lin) : -1;
         lbo[tid] = ok ? line_base(line, a.inner, a.Lout) : -1;
     }
-    const bool contig = a.inner == 1;  // the lines are contiguous rows
-    if constexpr (!PRUNE_OUT)
-        for (int idx = tid; idx < N * TI; idx += FP_THREADS) buf[idx] = make_float2(0.f, 0.f);
     __syncthreads();
-    if constexpr (PRUNE_OUT) {
-#pragma unroll 8
-        for (int idx = tid; idx < N * TI; idx += FP_THREADS) {
-            const int t = contig ? idx / N : idx % TI, l = contig ? idx % N : idx / TI;
-            const int64_t b = lbi[t];
-            buf[l * TI + t] = b >= 0 ? in[b + (int64_t)l * a.inner] : make_float2(0.f, 0.f);
-        }
-    } else {
-        const int nin = a.M * TI;
-#pragma unroll 4
-        for (int idx = tid; idx < nin; idx += FP_THREADS) {
-            const int t = contig ? idx / a.M : idx % TI, i = contig ? idx % a.M : idx / TI;
-            const int64_t b = lbi[t];
-            if (b >= 0) {
-                const float2 v = in[b + (int64_t)i * a.inner];
-                const float d = a.dec[i];
-                const int p = (i - a.hM + N) & (N - 1);
-                buf[p * TI + t] = make_float2(v.x * d, v.y * d);
+
+    // ---- first stage: radix 8, Ns = 1, inputs from global memory ----
+    {
+        constexpr int NJ = N / 8, NB = NJ * TI, MB = (NB + FP_THREADS - 1) / FP_THREADS;
+        float2 v[MB][8];
+#pragma unroll
+        for (int m = 0; m < MB; ++m) {
+            const int b = tid + m * FP_THREADS;
+            int t = 0, j = 0;
+            bfly_of<TI, NJ>(b, contig, t, j);
+            const int64_t lb = b < NB ? lbi[t] : -1;
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                const int p = j + r * NJ;
+                float2 x = make_float2(0.f, 0.f);
+                if (lb >= 0) {
+                    if constexpr (PRUNE_OUT) {
+                        x = in[lb + (int64_t)p * a.inner];
+                    } else {
+                        const int i = mode_of<N>(p, a.M, a.hM);
+                        if (i >= 0) {
+                            const float2 y = in[lb + (int64_t)i * a.inner];
+                            const float d = a.dec[i];
+                            x = make_float2(y.x * d, y.y * d);
+                        }
+                    }
+                }
+                v[m][r] = x;
             }
         }
+#pragma unroll
+        for (int m = 0; m < MB; ++m) {
+            const int b = tid + m * FP_THREADS;
+            if (b < NB) {
+                int t, j;
+                bfly_of<TI, NJ>(b, contig, t, j);
+                dft8<S>(v[m]);
+#pragma unroll
+                for (int r = 0; r < 8; ++r) buf[lds_at<TI>(j * 8 + r, t)] = v[m][r];
+            }
+        }
+        __syncthreads();
     }
-    __syncthreads();
-    fft_lines<LOGN, TI, S>(buf, tw);
-    if constexpr (PRUNE_OUT) {
-        const int nout = a.M * TI;
-#pragma unroll 4
-        for (int idx = tid; idx < nout; idx += FP_THREADS) {
-            const int t = contig ? idx / a.M : idx % TI, i = contig ? idx % a.M : idx / TI;
-            const int64_t b = lbo[t];
-            if (b >= 0) {
-                const int p = (i - a.hM + N) & (N - 1);
-                const float2 v = buf[p * TI + t];
-                const float d = a.dec[i];
-                out[b + (int64_t)i * a.inner] = make_float2(v.x * d, v.y * d);
+
+    // ---- middle stages ----
+    int Ns = 8;
+#pragma unroll
+    for (int s = 1; s < (REM == 0 ? N8 - 1 : N8); ++s) {
+        stage<N, TI, 8, S>(buf, tw, Ns);
+        Ns *= 8;
+    }
+
+    // ---- last stage: radix RL, Ns = N / RL, outputs to global memory ----
+    {
+        constexpr int NJ = N / RL, NB = NJ * TI, MB = (NB + FP_THREADS - 1) / FP_THREADS;
+#pragma unroll
+        for (int m = 0; m < MB; ++m) {
+            const int b = tid + m * FP_THREADS;
+            if (b < NB) {
+                int t, j;
+                bfly_of<TI, NJ>(b, contig, t, j);
+                float2 v[RL];
+#pragma unroll
+                for (int r = 0; r < RL; ++r) v[r] = buf[lds_at<TI>(j + r * NJ, t)];
+#pragma unroll
+                for (int r = 1; r < RL; ++r) v[r] = cmul(v[r], tw[j * r]);
+                dft<RL, S>(v);
+                const int64_t lb = lbo[t];
+                if (lb >= 0) {
+#pragma unroll
+                    for (int r = 0; r < RL; ++r) {
+                        const int p = j + r * NJ;  // natural-order output position
+                        if constexpr (PRUNE_OUT) {
+                            const int i = mode_of<N>(p, a.M, a.hM);
+                            if (i >= 0) {
+                                const float d = a.dec[i];
+                                out[lb + (int64_t)i * a.inner] = make_float2(v[r].x * d, v[r].y * d);
+                            }
+                        } else {
+                            out[lb + (int64_t)p * a.inner] = v[r];
+                        }
+                    }
+                }
             }
-        }
-    } else {
-#pragma unroll 8
-        for (int idx = tid; idx < N * TI; idx += FP_THREADS) {
-            const int t = contig ? idx / N : idx % TI, l = contig ? idx % N : idx / TI;
-            const int64_t b = lbo[t];
-            if (b >= 0) out[b + (int64_t)l * a.inner] = buf[l * TI + t];
         }
     }
 }
@@ -232,10 +295,9 @@ constexpr int fp_ti(int logn) {
     return (FP_ELEMS >> logn) < 16 ? (FP_ELEMS >> logn) : 16;
 }
 
-template <int LOGN>
-int launch_axis(bool prune_out, int isign, const float2 *in, float2 *out, const AxisArgs &a,
-                hipStream_t s) {
-    constexpr int TI = fp_ti(LOGN);
+template <int LOGN, int TI>
+int launch_axis_ti(bool prune_out, int isign, const float2 *in, float2 *out, const AxisArgs &a,
+                   hipStream_t s) {
     const int64_t ntile = (a.nlines + TI - 1) / TI;
     if (ntile > 0x7fffffff) {
         set_error("fft: too many lines");
@@ -251,6 +313,40 @@ int launch_axis(bool prune_out, int isign, const float2 *in, float2 *out, const 
     }
     MN_LAUNCH_CHECK("fft axis");
     return MN_OK;
+}
+
+// Lines per workgroup: fp_ti(LOGN) fills 64 KB of LDS. Measured on MI355X
+// at 512^3, a quarter of that for contiguous lines (the last axis) and half
+// for strided ones run fastest: more resident workgroups per CU keep more
+// loads in flight. MN_FFT_TI_SHIFT / MN_FFT_TI_SHIFT_STRIDED override the
+// shifts (tuning).
+int fp_ti_shift(bool contig) {
+    static const int vc = [] {
+        const char *e = getenv("MN_FFT_TI_SHIFT");
+        return e ? atoi(e) : 2;
+    }();
+    static const int vs = [] {
+        const char *e = getenv("MN_FFT_TI_SHIFT_STRIDED");
+        return e ? atoi(e) : 1;
+    }();
+    return contig ? vc : vs;
+}
+
+template <int LOGN>
+int launch_axis(bool prune_out, int isign, const float2 *in, float2 *out, const AxisArgs &a,
+                hipStream_t s) {
+    constexpr int TI = fp_ti(LOGN);
+    const int shift = fp_ti_shift(a.inner == 1);
+    if constexpr (TI >= 8) {
+        if (shift >= 3) return launch_axis_ti<LOGN, TI / 8>(prune_out, isign, in, out, a, s);
+    }
+    if constexpr (TI >= 4) {
+        if (shift == 2) return launch_axis_ti<LOGN, TI / 4>(prune_out, isign, in, out, a, s);
+    }
+    if constexpr (TI >= 2) {
+        if (shift == 1) return launch_axis_ti<LOGN, TI / 2>(prune_out, isign, in, out, a, s);
+    }
+    return launch_axis_ti<LOGN, TI>(prune_out, isign, in, out, a, s);
 }
 
 constexpr int kMinLog = 4, kMaxLog = 12;
