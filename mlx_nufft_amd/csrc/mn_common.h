@@ -100,13 +100,16 @@ inline Geom make_geom(const mn_bins *g) {
 // ---- device helpers -------------------------------------------------------
 
 // ES kernel psi(d) = exp(beta*(sqrt(1 - (2d/w)^2) - 1)) on |d| <= w/2.
-// Written as 2^(beta*log2(e)*(sqrt(t)-1)) so it maps onto one v_exp_f32;
-// bl2e = beta*log2(e), inv_hw = 2/w. The argument of exp2 is <= 0, so the
-// relative error of the product feeds only the (tiny) tail weights.
+// Written as 2^(beta*log2(e)*(sqrt(t)-1)) on the hardware v_sqrt_f32 and
+// v_exp_f32 (about 1 ulp each); bl2e = beta*log2(e), inv_hw = 2/w. The exp2
+// argument lies in [-bl2e, 0] (bl2e <= 0.97*pi*log2(e)*16, about 71), so no
+// denormal input or result arises and the libm wrappers' range fix-ups
+// (some 20 extra instructions per weight) are not needed. Callers mask taps
+// with |d| > w/2 themselves (t is clamped to 0 there, giving e^-beta).
 __device__ __forceinline__ float es_weight(float d, float bl2e, float inv_hw) {
-    float z = d * inv_hw;
-    float t = fmaxf(1.0f - z * z, 0.0f);
-    return exp2f(bl2e * (__builtin_sqrtf(t) - 1.0f));
+    const float z = d * inv_hw;
+    const float t = fmaxf(1.0f - z * z, 0.0f);
+    return __builtin_amdgcn_exp2f(bl2e * (__builtin_amdgcn_sqrtf(t) - 1.0f));
 }
 
 // Map a cell index that is at most one period outside [0, n) back into it.

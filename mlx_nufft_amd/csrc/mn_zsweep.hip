@@ -38,7 +38,15 @@ constexpr int UNR = 4;     // points per unrolled sweep step
 constexpr int NR = 4;      // key ranges per z: own, -x, -y, -xy
 constexpr int REC = 32;    // floats per table row
 
-template <int W>
+// Lane layout: the wave's 64 lanes form four 16-lane groups, one per 4x4
+// quadrant of the 8x8 column block; lane l owns column
+// (4*qx + ((l >> 2) & 3), 4*qy + (l & 3)) with (qx, qy) = (l >> 5, (l >> 4) & 1).
+__device__ __forceinline__ int lane_cx(int l) { return ((l >> 5) << 2) + ((l >> 2) & 3); }
+__device__ __forceinline__ int lane_cy(int l) { return (((l >> 4) & 1) << 2) + (l & 3); }
+
+// Stage the finished cell of each column; every ZST z-slices (or at the
+// segment end) the wave writes them out with 4 consecutive lanes per column
+// storing 4 consecutive z.
 __device__ __forceinline__ void store_stage(float2 (*stage)[64], float2 *__restrict__ grid,
                                             int lane, int s, int zw, int n1, int n2, int bx,
                                             int by, float wr, float wi, bool last) {
@@ -49,7 +57,7 @@ __device__ __forceinline__ void store_stage(float2 (*stage)[64], float2 *__restr
         for (int colb = 0; colb < 64; colb += 16) {
             const int col = colb + (lane >> 2), zo = lane & 3;
             if (zo < nz) {
-                const int gx = ZB * bx + (col >> 3), gy = ZB * by + (col & 7);
+                const int gx = ZB * bx + lane_cx(col), gy = ZB * by + lane_cy(col);
                 grid[((int64_t)gx * n1 + gy) * n2 + zb + zo] = stage[zo][col];
             }
         }
@@ -68,7 +76,11 @@ __global__ __launch_bounds__(64) void k_spread_zsweep(int n0, int n1, int n2, in
                                                       const float2 *__restrict__ c,
                                                       const float2 *__restrict__ pre,
                                                       float2 *__restrict__ grid) {
-    __shared__ float table[64 * REC];
+    // table rows: x-weights of the block's 8 columns times the strength
+    // (complex, 16 floats), y-weights of its 8 rows, W z-weights (padded to
+    // 8); row 64 stays zero and pads the quadrant lists.
+    __shared__ __align__(16) float table[(64 + 1) * REC];
+    __shared__ __align__(16) uint8_t lists[ZCH][4][64];
     __shared__ float2 stage[ZST][64];
     const int64_t nw = (int64_t)nbx * nby * nseg;
     int64_t wid = xcd_remap(blockIdx.x, nw);
@@ -76,7 +88,10 @@ __global__ __launch_bounds__(64) void k_spread_zsweep(int n0, int n1, int n2, in
     wid /= nseg;
     const int by = (int)(wid % nby), bx = (int)(wid / nby);
     const int z0 = seg * zseg, zend = min(z0 + zseg, n2);
-    const int lane = threadIdx.x, lx = lane >> 3, ly = lane & 7;
+    const int lane = threadIdx.x, grp = lane >> 4;
+    const int cxl = lane_cx(lane), cyl = lane_cy(lane);
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    if (lane < REC) table[64 * REC + lane] = 0.f;
     const int bxm = bx == 0 ? nbx - 1 : bx - 1, bym = by == 0 ? nby - 1 : by - 1;
     const int blk[NR] = {bx * nby + by, bxm * nby + by, bx * nby + bym, bxm * nby + bym};
     const int clo[NR] = {0, 2, 1, 2}, chi[NR] = {3, 3, 2, 2};
@@ -108,7 +123,11 @@ __global__ __launch_bounds__(64) void k_spread_zsweep(int n0, int n1, int n2, in
         for (int bat = 0; bat < tot; bat += 64) {
             const int nb = min(64, tot - bat);
             __syncthreads();
-            if (lane < nb) {
+            reinterpret_cast<uint32_t *>(lists)[lane] = 0x40404040u;
+            reinterpret_cast<uint32_t *>(lists)[lane + 64] = 0x40404040u;
+            const bool valid = lane < nb;
+            int tsel = -1, touch = 0;
+            if (valid) {
                 const int e = bat + lane;
                 int i = 0;
 #pragma unroll
@@ -120,6 +139,7 @@ __global__ __launch_bounds__(64) void k_spread_zsweep(int n0, int n1, int n2, in
                         st = rs[q];
                         p0 = pf[q];
                     }
+                tsel = i / NR;
                 const int64_t j = (int64_t)st + (e - p0);
                 // first tap relative to this block: the word's in-block cell,
                 // minus 8 for points of the -x / -y neighbour blocks
@@ -133,33 +153,53 @@ __global__ __launch_bounds__(64) void k_spread_zsweep(int n0, int n1, int n2, in
                     const float2 pv = pre[j];
                     cv = make_float2(cv.x * pv.x - cv.y * pv.y, cv.x * pv.y + cv.y * pv.x);
                 }
-                float *rec = table + lane * REC;
+                float4 *rec = reinterpret_cast<float4 *>(table + lane * REC);
+                float wx[ZB], wy[ZB], wz[ZB];
 #pragma unroll
-                for (int q = 0; q < 24; ++q) rec[q] = 0.f;
+                for (int q = 0; q < ZB; ++q) {
+                    const int ax = q - ox, ay = q - oy;
+                    wx[q] = ((unsigned)ax < (unsigned)W) ? es_weight((float)ax - fx, bl2e, inv_hw) : 0.f;
+                    wy[q] = ((unsigned)ay < (unsigned)W) ? es_weight((float)ay - fy, bl2e, inv_hw) : 0.f;
+                    wz[q] = q < W ? es_weight((float)q - fz, bl2e, inv_hw) : 0.f;
+                }
 #pragma unroll
-                for (int a = 0; a < W; ++a) {
-                    const int qx = ox + a, qy = oy + a;
-                    const float wx = es_weight((float)a - fx, bl2e, inv_hw);
-                    const float wy = es_weight((float)a - fy, bl2e, inv_hw);
-                    if ((unsigned)qx < (unsigned)ZB) {
-                        rec[2 * qx] = cv.x * wx;
-                        rec[2 * qx + 1] = cv.y * wx;
-                    }
-                    if ((unsigned)qy < (unsigned)ZB) rec[16 + qy] = wy;
-                    rec[24 + a] = es_weight((float)a - fz, bl2e, inv_hw);
+                for (int q = 0; q < ZB; q += 2)
+                    rec[q / 2] = make_float4(cv.x * wx[q], cv.y * wx[q], cv.x * wx[q + 1],
+                                             cv.y * wx[q + 1]);
+                rec[4] = make_float4(wy[0], wy[1], wy[2], wy[3]);
+                rec[5] = make_float4(wy[4], wy[5], wy[6], wy[7]);
+                rec[6] = make_float4(wz[0], wz[1], wz[2], wz[3]);
+                rec[7] = make_float4(wz[4], wz[5], wz[6], wz[7]);
+                // quadrants (qx, qy) the footprint [ox, ox + W) x [oy, oy + W) meets
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int qx = q >> 1, qy = q & 1;
+                    const bool hit = ox < 4 * qx + 4 && ox + W > 4 * qx && oy < 4 * qy + 4 &&
+                                     oy + W > 4 * qy;
+                    touch |= hit ? (1 << q) : 0;
                 }
             }
+            // per z-step and quadrant: the batch rows that touch it, in order
+            int cnt[ZCH][4];
+#pragma unroll
+            for (int t = 0; t < ZCH; ++t)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const bool mine = tsel == t && ((touch >> q) & 1);
+                    const uint64_t bq = __ballot(mine);
+                    cnt[t][q] = __popcll(bq);
+                    if (mine) lists[t][q][__popcll(bq & lt_mask)] = (uint8_t)lane;
+                }
             __syncthreads();
-            // rows of z-step t occupy [pf[t*NR], pf[(t+1)*NR]) of the chunk
 #pragma unroll
             for (int t = 0; t < ZCH; ++t) {
-                const int kb = max(pf[t * NR] - bat, 0), ke = min(pf[(t + 1) * NR] - bat, nb);
-                if (kb >= ke) continue;
+                const int nit = max(max(cnt[t][0], cnt[t][1]), max(cnt[t][2], cnt[t][3]));
+                if (nit == 0) continue;
                 const int ze = zc + t;
                 while (zw < ze) {
                     if (zw >= z0)
-                        store_stage<W>(stage, grid, lane, (zw - z0) % ZST, zw, n1, n2, bx, by,
-                                       wre[0], wim[0], zw == zend - 1);
+                        store_stage(stage, grid, lane, (zw - z0) % ZST, zw, n1, n2, bx, by,
+                                    wre[0], wim[0], zw == zend - 1);
 #pragma unroll
                     for (int a = 0; a < W - 1; ++a) {
                         wre[a] = wre[a + 1];
@@ -168,25 +208,26 @@ __global__ __launch_bounds__(64) void k_spread_zsweep(int n0, int n1, int n2, in
                     wre[W - 1] = wim[W - 1] = 0.f;
                     ++zw;
                 }
-                for (int k = kb; k < ke; k += UNR) {
-                    float vr[UNR], vi[UNR], wz[UNR][W];
+                const uint32_t *lw = reinterpret_cast<const uint32_t *>(lists[t][grp]);
+                for (int it = 0; it < nit; it += UNR) {
+                    const uint32_t pk = lw[it >> 2];
+                    float vr[UNR], vi[UNR], wzz[UNR][W];
 #pragma unroll
                     for (int u = 0; u < UNR; ++u) {
-                        const int kk = min(k + u, ke - 1);
-                        const float *rec = table + kk * REC;
-                        const float2 wxc = *(const float2 *)(rec + 2 * lx);
-                        const float wy = (k + u < ke) ? rec[16 + ly] : 0.f;
-                        vr[u] = wxc.x * wy;
-                        vi[u] = wxc.y * wy;
+                        const float *rec = table + ((pk >> (8 * u)) & 0xffu) * REC;
+                        const float2 wxc = *reinterpret_cast<const float2 *>(rec + 2 * cxl);
+                        const float wyv = rec[16 + cyl];
+                        vr[u] = wxc.x * wyv;
+                        vi[u] = wxc.y * wyv;
 #pragma unroll
-                        for (int a = 0; a < W; ++a) wz[u][a] = rec[24 + a];
+                        for (int a = 0; a < W; ++a) wzz[u][a] = rec[24 + a];
                     }
 #pragma unroll
                     for (int u = 0; u < UNR; ++u)
 #pragma unroll
                         for (int a = 0; a < W; ++a) {
-                            wre[a] = fmaf(vr[u], wz[u][a], wre[a]);
-                            wim[a] = fmaf(vi[u], wz[u][a], wim[a]);
+                            wre[a] = fmaf(vr[u], wzz[u][a], wre[a]);
+                            wim[a] = fmaf(vi[u], wzz[u][a], wim[a]);
                         }
                 }
             }
@@ -194,8 +235,8 @@ __global__ __launch_bounds__(64) void k_spread_zsweep(int n0, int n1, int n2, in
     }
     while (zw < zend) {  // drain the window up to the segment end
         if (zw >= z0)
-            store_stage<W>(stage, grid, lane, (zw - z0) % ZST, zw, n1, n2, bx, by, wre[0], wim[0],
-                           zw == zend - 1);
+            store_stage(stage, grid, lane, (zw - z0) % ZST, zw, n1, n2, bx, by, wre[0], wim[0],
+                        zw == zend - 1);
 #pragma unroll
         for (int a = 0; a < W - 1; ++a) {
             wre[a] = wre[a + 1];
