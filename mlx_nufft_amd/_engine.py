@@ -52,6 +52,11 @@ def bin_sizes(dim, w, n_up, cell_bytes=SPREAD_CELL_BYTES):
         m = [1024]
     elif dim == 2:
         m = [32, 32]
+    elif cell_bytes == INTERP_CELL_BYTES:
+        # interp is bound by staging tiles: small bins keep about 9
+        # workgroups resident per CU, which beats the smaller halo re-read of
+        # big tiles (MI355X, 3D type 2 at 512^3: 2.0 ms at m = 8, 3.1 ms at 16)
+        m = [8, 8, 8]
     else:
         side = int(round((budget / cell_bytes) ** (1.0 / 3.0) - 1e-9))
         while cell_bytes * side ** 3 > budget:

@@ -11,6 +11,8 @@
 // gpu_t3.py:653-693 (type-3 gather x post).
 #include "mn_common.h"
 
+#include <stdlib.h>
+
 namespace mn {
 namespace {
 
@@ -58,17 +60,29 @@ __global__ __launch_bounds__(256) void k_interp_tiled(Geom g, float bl2e, float 
     const int o0 = b[0] * g.m[0] - W / 2;
     const int o1 = DIM >= 2 ? b[1] * g.m[1] - W / 2 : 0;
     const int o2 = DIM >= 3 ? b[2] * g.m[2] - W / 2 : 0;
-    for (int q = threadIdx.x; q < T; q += 256) {
-        const int q2 = q % p2, r12 = q / p2;
-        const int q1 = r12 % p1, q0 = r12 / p1;
-        const int g0 = wrap_tile_i(o0 + q0, g.n[0]);
-        const int g1 = DIM >= 2 ? wrap_tile_i(o1 + q1, g.n[1]) : 0;
-        const int g2 = DIM >= 3 ? wrap_tile_i(o2 + q2, g.n[2]) : 0;
-        tile[q] = grid[((int64_t)g0 * g.n[1] + g1) * g.n[2] + g2];
+    {
+        // Tile cell q = (q0*p1 + q1)*p2 + q2, walked with a stride of nt as a
+        // mixed-radix counter (no division per cell).
+        const int nt = blockDim.x;
+        const int s2 = nt % p2, s12 = nt / p2, s1 = s12 % p1, s0 = s12 / p1;
+        int q2 = threadIdx.x % p2, q1 = (threadIdx.x / p2) % p1, q0 = threadIdx.x / (p2 * p1);
+        for (int q = threadIdx.x; q < T; q += nt) {
+            const int g0 = wrap_tile_i(o0 + q0, g.n[0]);
+            const int g1 = DIM >= 2 ? wrap_tile_i(o1 + q1, g.n[1]) : 0;
+            const int g2 = DIM >= 3 ? wrap_tile_i(o2 + q2, g.n[2]) : 0;
+            tile[q] = grid[((int64_t)g0 * g.n[1] + g1) * g.n[2] + g2];
+            q2 += s2;
+            int c = q2 >= p2;
+            q2 -= c ? p2 : 0;
+            q1 += s1 + c;
+            c = q1 >= p1;
+            q1 -= c ? p1 : 0;
+            q0 += s0 + c;
+        }
     }
     __syncthreads();
 
-    for (int t = threadIdx.x; t < cnt; t += 256) {
+    for (int t = threadIdx.x; t < cnt; t += blockDim.x) {
         const int64_t j = (int64_t)s0 + t;
         float wt[DIM][W];
         int loc[3] = {0, 0, 0};
@@ -135,6 +149,15 @@ __global__ __launch_bounds__(256) void k_interp_tiled(Geom g, float bl2e, float 
     }
 }
 
+int interp_threads() {
+    static const int v = [] {
+        const char *e = getenv("MN_INTERP_THREADS");
+        const int n = e ? atoi(e) : 256;
+        return (n == 64 || n == 128 || n == 256) ? n : 256;
+    }();
+    return v;
+}
+
 template <int DIM, int W>
 struct InterpLaunch {
     static int run(const InterpArgs &a) {
@@ -151,7 +174,7 @@ struct InterpLaunch {
         if (lds > 65536)
             MN_HIP_CHECK(hipFuncSetAttribute((const void *)kern,
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        kern<<<(unsigned)a.nsub, 256, lds, a.s>>>(g, bl2e, inv_hw, a.nsub, a.info, a.perm, a.i1s,
+        kern<<<(unsigned)a.nsub, interp_threads(), lds, a.s>>>(g, bl2e, inv_hw, a.nsub, a.info, a.perm, a.i1s,
                                                   a.frs, a.grid, a.post, a.out);
         MN_LAUNCH_CHECK("interp");
         return MN_OK;
