@@ -104,10 +104,16 @@ __global__ __launch_bounds__(RS_THREADS) void k_radix_hist(const uint32_t *__res
     h[threadIdx.x] = 0;
     __syncthreads();
     int64_t base = (int64_t)blockIdx.x * RS_TILE;
-#pragma unroll 4
+    uint32_t kv[RS_ITEMS];
+#pragma unroll
     for (int i = 0; i < RS_ITEMS; ++i) {
         int64_t idx = base + (int64_t)i * RS_THREADS + threadIdx.x;
-        if (idx < P) atomicAdd(&h[digit_of(keys[idx], kmask, shift)], 1u);
+        kv[i] = idx < P ? keys[idx] : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < RS_ITEMS; ++i) {
+        int64_t idx = base + (int64_t)i * RS_THREADS + threadIdx.x;
+        if (idx < P) atomicAdd(&h[digit_of(kv[i], kmask, shift)], 1u);
     }
     __syncthreads();
     hist[(int64_t)threadIdx.x * nblk + blockIdx.x] = h[threadIdx.x];
@@ -121,12 +127,14 @@ struct SortCols {
 // Stable scatter of one 4096-element tile: the key, its value (the caller
 // index; implicit on the first pass) and up to MN_SORT_MAX_COLS payload
 // columns.
-//  1. Rank: 16 rounds of 256 consecutive elements; in a round wave w holds
-//     [64w, 64w+64) and ranks lanes with equal digits by a ballot match;
-//     run[d] counts the tile's earlier elements of digit d. Index order is
-//     kept, so the pass is stable.
-//  2. The tile's digit counts are scanned into lstart; an element's slot in
-//     the tile-local sorted order is lstart[d] + its rank.
+//  1. Rank: wave w owns the tile's elements [1024w, 1024w + 1024) and visits
+//     them in 16 rounds of 64 consecutive elements; lanes with equal digits
+//     find each other with a ballot match and a wave-private LDS counter per
+//     digit gives the count of the wave's earlier elements with that digit.
+//     No barrier is needed inside a wave (its LDS accesses stay in order).
+//  2. One scan over the 4 x 256 wave counters gives each (wave, digit) its
+//     start in the tile-local sorted order; an element's slot is that start
+//     plus its rank. Index order is kept, so the pass is stable.
 //  3. Every column goes through LDS: written at the slots, read back in slot
 //     order and stored at gbase[d] + slot - lstart[d], so consecutive lanes
 //     store consecutive addresses inside each digit run.
@@ -136,26 +144,33 @@ __global__ __launch_bounds__(RS_THREADS) void k_radix_scatter(
     const uint32_t *__restrict__ kin, const uint32_t *__restrict__ vin, int64_t P, int shift,
     uint32_t kmask, const uint32_t *__restrict__ offs, int64_t nblk,
     uint32_t *__restrict__ kout, uint32_t *__restrict__ vout, int ncols, SortCols cols) {
-    __shared__ uint32_t run[RS_RADIX];
+    constexpr int NWV = RS_THREADS / 64;
     __shared__ uint32_t gbase[RS_RADIX];
-    __shared__ uint32_t wcnt[RS_THREADS / 64][RS_RADIX];
+    __shared__ uint32_t lstart[RS_RADIX];
+    __shared__ uint32_t wcnt[NWV][RS_RADIX];
     __shared__ uint32_t stage[RS_TILE];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int64_t tile = xcd_remap(blockIdx.x, nblk);
     const int64_t base = tile * RS_TILE;
     const int nvalid = (int)((P - base) < RS_TILE ? (P - base) : RS_TILE);
-    run[tid] = 0;
     gbase[tid] = offs[(int64_t)tid * nblk + tile];
 #pragma unroll
-    for (int w = 0; w < RS_THREADS / 64; ++w) wcnt[w][tid] = 0;
+    for (int w = 0; w < NWV; ++w) wcnt[w][tid] = 0;
     __syncthreads();
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     uint32_t kv[RS_ITEMS], rk[RS_ITEMS];
+    const int wbase = wv * (RS_TILE / NWV);
+    // all key loads first: one memory latency per tile, not one per round
 #pragma unroll
     for (int r = 0; r < RS_ITEMS; ++r) {
-        const int q = r * RS_THREADS + tid;
+        const int q = wbase + r * 64 + lane;
+        kv[r] = q < nvalid ? kin[base + q] : 0u;
+    }
+#pragma unroll
+    for (int r = 0; r < RS_ITEMS; ++r) {
+        const int q = wbase + r * 64 + lane;
         const bool valid = q < nvalid;
-        const uint32_t k = valid ? kin[base + q] : 0u;
+        const uint32_t k = kv[r];
         const uint32_t dg = digit_of(k, kmask, shift);
         uint64_t peers = __ballot(valid);
 #pragma unroll
@@ -165,32 +180,34 @@ __global__ __launch_bounds__(RS_THREADS) void k_radix_scatter(
             peers &= bit ? bal : ~bal;
         }
         const uint32_t rank = (uint32_t)__popcll(peers & lt_mask);
-        if (valid && rank == 0) wcnt[wv][dg] = (uint32_t)__popcll(peers);
-        __syncthreads();
-        uint32_t pre = run[dg];
-        for (int w = 0; w < wv; ++w) pre += wcnt[w][dg];
-        kv[r] = k;
-        rk[r] = valid ? ((dg << 16) | (pre + rank)) : 0xFFFFFFFFu;
-        __syncthreads();
-        uint32_t add = 0;
-#pragma unroll
-        for (int w = 0; w < RS_THREADS / 64; ++w) {
-            add += wcnt[w][tid];
-            wcnt[w][tid] = 0;
-        }
-        run[tid] += add;
-        __syncthreads();
+        const uint32_t before = valid ? wcnt[wv][dg] : 0u;
+        if (valid && rank == 0) wcnt[wv][dg] = before + (uint32_t)__popcll(peers);
+        rk[r] = valid ? ((dg << 16) | (before + rank)) : 0xFFFFFFFFu;
     }
-    // Tile-local digit starts (wcnt[0] is free again).
-    uint32_t *lstart = wcnt[0];
-    uint32_t tot;
-    const uint32_t ex = block_excl_scan(run[tid], &tot);
-    lstart[tid] = ex;
+    __syncthreads();
+    // Tile-local starts: digit-major over (digit, wave).
+    {
+        uint32_t c[NWV], s = 0;
+#pragma unroll
+        for (int w = 0; w < NWV; ++w) {
+            c[w] = wcnt[w][tid];
+            s += c[w];
+        }
+        uint32_t tot;
+        const uint32_t ex = block_excl_scan(s, &tot);
+        lstart[tid] = ex;
+        uint32_t run = ex;
+#pragma unroll
+        for (int w = 0; w < NWV; ++w) {
+            wcnt[w][tid] = run;
+            run += c[w];
+        }
+    }
     __syncthreads();
     int slot[RS_ITEMS];
 #pragma unroll
     for (int r = 0; r < RS_ITEMS; ++r)
-        slot[r] = rk[r] == 0xFFFFFFFFu ? -1 : (int)(lstart[rk[r] >> 16] + (rk[r] & 0xFFFFu));
+        slot[r] = rk[r] == 0xFFFFFFFFu ? -1 : (int)(wcnt[wv][rk[r] >> 16] + (rk[r] & 0xFFFFu));
     // Keys: stage, then derive each slot's destination from its digit.
 #pragma unroll
     for (int r = 0; r < RS_ITEMS; ++r)
@@ -209,18 +226,28 @@ __global__ __launch_bounds__(RS_THREADS) void k_radix_scatter(
         }
     }
     __syncthreads();
-    // Values and payload columns, one LDS round trip each.
+    // Values and payload columns, one LDS round trip each; the next
+    // column's loads are issued before the current one is written out.
+    uint32_t cur[RS_ITEMS];
+#pragma unroll
+    for (int r = 0; r < RS_ITEMS; ++r) {
+        const int64_t idx = base + wbase + r * 64 + lane;
+        cur[r] = slot[r] >= 0 ? (vin ? vin[idx] : (uint32_t)idx) : 0u;
+    }
     for (int c = -1; c < ncols; ++c) {
-        const uint32_t *src = c < 0 ? vin : cols.in[c];
         uint32_t *out = c < 0 ? vout : cols.out[c];
 #pragma unroll
-        for (int r = 0; r < RS_ITEMS; ++r) {
-            if (slot[r] >= 0) {
-                const int64_t idx = base + r * RS_THREADS + tid;
-                stage[slot[r]] = src ? src[idx] : (uint32_t)idx;
+        for (int r = 0; r < RS_ITEMS; ++r)
+            if (slot[r] >= 0) stage[slot[r]] = cur[r];
+        __syncthreads();
+        if (c + 1 < ncols) {
+            const uint32_t *src = cols.in[c + 1];
+#pragma unroll
+            for (int r = 0; r < RS_ITEMS; ++r) {
+                const int64_t idx = base + wbase + r * 64 + lane;
+                cur[r] = slot[r] >= 0 ? src[idx] : 0u;
             }
         }
-        __syncthreads();
 #pragma unroll
         for (int r = 0; r < RS_ITEMS; ++r) {
             const int q = r * RS_THREADS + tid;
