@@ -199,6 +199,29 @@ int mn_permute_c64(int64_t P, const uint32_t *perm, const void *in, void *out,
                    mn_stream_t stream);
 
 /*
+ * Start index of every bin in the sorted order: starts[b] = first sorted
+ * position whose bin key is >= b, for b in [0, nbins] (nbins + 1 int32).
+ * ref: nd.py:347-372 (_od_finish bin ranges).
+ */
+int mn_bin_starts(const mn_bins *g, int64_t P, const uint32_t *sorted_key, int32_t *starts,
+                  mn_stream_t stream);
+
+/*
+ * Streaming 3D interpolation: as mn_interp, for 3D grids with bins of
+ * m = (16, 16, 8) and 2 <= w <= 12. One workgroup owns a 16 x 16 column
+ * block and walks its z-bins in order with a sliding LDS window of the grid
+ * (the block's columns plus the kernel halo, 8 + w - 1 z-cells deep); each
+ * grid cell is read (16 + w - 1)^2 / 256 times. Points sorted by bin key
+ * with bin_start from mn_bin_starts; out[perm[j]] receives point j (times
+ * post[j] when post is not NULL).
+ * ref: nd.py:974-1073 (OD gather), gpu_t3.py:653-693 (type-3 gather x post).
+ */
+int mn_interp_zstream(const mn_bins *g, float beta, int64_t P, const int32_t *bin_start,
+                      const uint32_t *perm, const int32_t *const i1s[3],
+                      const float *const frs[3], const void *grid, const void *post, void *out,
+                      mn_stream_t stream);
+
+/*
  * Batched spread: B strength vectors cs (B x P, caller order, row-major)
  * over the same points into B grids (B x prod n, overwritten); the ES
  * weights are computed once per point and applied to every vector.

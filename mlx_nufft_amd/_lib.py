@@ -77,6 +77,9 @@ _SIGS = [
                                 VP3, c_int64, c_vp, c_vp, c_vp]),
     ("mn_interp", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int64, c_vp, c_vp, VP3, VP3,
                           c_vp, c_vp, c_vp, c_vp]),
+    ("mn_bin_starts", c_int, [ctypes.POINTER(Bins), c_int64, c_vp, c_vp, c_vp]),
+    ("mn_interp_zstream", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_vp, c_vp, VP3, VP3,
+                                  c_vp, c_vp, c_vp, c_vp]),
     ("mn_crop_deconv", c_int, [c_int, I64x3, I64x3, c_int64, c_vp, VP3, c_vp, c_vp]),
     ("mn_pad_deconv", c_int, [c_int, I64x3, I64x3, c_int64, c_vp, VP3, c_vp, c_vp]),
     ("mn_t3_setpts_src", c_int, [ctypes.POINTER(Bins), c_int64, VP3, D3, D3, D3, D3, c_int, c_int,

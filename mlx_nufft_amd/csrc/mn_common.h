@@ -70,6 +70,11 @@ int fill_zero(void *ptr, int64_t bytes, hipStream_t s);
 int64_t scan_partials_elems(int64_t n);
 int scan_exclusive_u32(uint32_t *data, int64_t n, uint32_t *partials, hipStream_t s);
 
+// starts[k] = first index of the sorted keys whose key & kmask is >= k, for
+// k in [0, K] (K + 1 entries); keys must be < K after masking.
+int key_starts(const uint32_t *sorted_key, int64_t P, int64_t K, uint32_t kmask, int32_t *starts,
+               hipStream_t s);
+
 constexpr int kMaxW = 16;
 constexpr double kTwoPi = 6.283185307179586;  // fl64(2*pi)
 

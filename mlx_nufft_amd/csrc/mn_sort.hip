@@ -257,6 +257,34 @@ __global__ __launch_bounds__(RS_THREADS) void k_radix_scatter(
     }
 }
 
+// starts[k] = first sorted index whose key (masked by kmask) is >= k, for k
+// in [0, K]: the thread of sorted position j (j in [0, P]) writes j for
+// every key in (key[j-1], key[j]] (from 0 for j = 0, up to K for j = P).
+// Short ranges are written by their lane; long ones (sparse or clustered
+// points) by the whole wave, 64 consecutive entries per store.
+__global__ __launch_bounds__(256) void k_key_starts(const uint32_t *__restrict__ key, int64_t P,
+                                                    int64_t K, uint32_t kmask,
+                                                    int32_t *__restrict__ starts) {
+    const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    int64_t lo = 0, hi = -1;  // inclusive key range to fill with j
+    if (j <= P) {
+        lo = (j == 0) ? 0 : (int64_t)(key[j - 1] & kmask) + 1;
+        hi = (j == P) ? K : (int64_t)(key[j] & kmask);
+    }
+    const bool big = hi - lo >= 16;
+    if (!big)
+        for (int64_t k = lo; k <= hi; ++k) starts[k] = (int32_t)j;
+    uint64_t todo = __ballot(big);
+    while (todo) {
+        const int src = __ffsll((unsigned long long)todo) - 1;
+        todo &= todo - 1;
+        const int64_t blo = __shfl(lo, src, 64), bhi = __shfl(hi, src, 64);
+        const int32_t v = (int32_t)__shfl(j, src, 64);
+        for (int64_t k = blo + lane; k <= bhi; k += 64) starts[k] = v;
+    }
+}
+
 // --------------------------------------------------------- subproblems ----
 
 __global__ void k_bin_bounds(const uint32_t *__restrict__ skey, int64_t P, int64_t nbins,
@@ -324,6 +352,14 @@ int scan_exclusive_u32(uint32_t *data, int64_t n, uint32_t *partials, hipStream_
     if (rc) return rc;
     k_tile_scan<<<(unsigned)nt, SC_THREADS, 0, s>>>(data, n, partials);
     MN_LAUNCH_CHECK("scan");
+    return MN_OK;
+}
+
+int key_starts(const uint32_t *sorted_key, int64_t P, int64_t K, uint32_t kmask, int32_t *starts,
+               hipStream_t s) {
+    k_key_starts<<<(unsigned)((P + 1 + 255) / 256), 256, 0, s>>>(sorted_key, P, K, kmask,
+                                                                 starts);
+    MN_LAUNCH_CHECK("key starts");
     return MN_OK;
 }
 
@@ -478,6 +514,16 @@ int mn_build_subproblems(const mn_bins *g, int64_t P, const uint32_t *sorted_key
     MN_LAUNCH_CHECK("subproblem fill");
     *nsub_out = (int64_t)total;
     return MN_OK;
+}
+
+int mn_bin_starts(const mn_bins *g, int64_t P, const uint32_t *sorted_key, int32_t *starts,
+                  mn_stream_t stream) {
+    clear_error();
+    int rc = check_bins(g);
+    if (rc) return rc;
+    MN_REQUIRE(P >= 1 && P < (int64_t(1) << 31), "bin starts: P must be in [1, 2^31)");
+    MN_REQUIRE(sorted_key && starts, "bin starts: NULL pointer");
+    return key_starts(sorted_key, P, nbins_total(g), 0xFFFFFFFFu, starts, as_stream(stream));
 }
 
 }  // extern "C"

@@ -247,33 +247,6 @@ __global__ __launch_bounds__(64) void k_spread_zsweep(int n0, int n1, int n2, in
     }
 }
 
-// zstart[k] = first sorted index whose key is >= k, for k in [0, K]: the
-// thread of sorted position j (j in [0, P]) writes j for every key in
-// (key[j-1], key[j]] (from 0 for j = 0, up to K for j = P). Short ranges are
-// written by their lane; long ones (sparse or clustered points) by the whole
-// wave, 64 consecutive entries per store.
-__global__ __launch_bounds__(256) void k_zs_starts(const uint32_t *__restrict__ word, int64_t P,
-                                                   int64_t K, int32_t *__restrict__ zstart) {
-    const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int lane = threadIdx.x & 63;
-    int64_t lo = 0, hi = -1;  // inclusive key range to fill with j
-    if (j <= P) {
-        lo = (j == 0) ? 0 : (int64_t)(word[j - 1] & kZsKeyMask) + 1;
-        hi = (j == P) ? K : (int64_t)(word[j] & kZsKeyMask);
-    }
-    const bool big = hi - lo >= 16;
-    if (!big)
-        for (int64_t k = lo; k <= hi; ++k) zstart[k] = (int32_t)j;
-    uint64_t todo = __ballot(big);
-    while (todo) {
-        const int src = __ffsll((unsigned long long)todo) - 1;
-        todo &= todo - 1;
-        const int64_t blo = __shfl(lo, src, 64), bhi = __shfl(hi, src, 64);
-        const int32_t v = (int32_t)__shfl(j, src, 64);
-        for (int64_t k = blo + lane; k <= bhi; k += 64) zstart[k] = v;
-    }
-}
-
 }  // namespace
 
 int zsweep_check(const mn_bins *g) {
@@ -346,11 +319,7 @@ int mn_zsweep_starts(const mn_bins *g, int64_t P, const uint32_t *sorted_word, i
     if (rc) return rc;
     MN_REQUIRE(P >= 1 && P < (int64_t(1) << 31), "zsweep starts: P must be in [1, 2^31)");
     MN_REQUIRE(sorted_word && zstart, "zsweep starts: NULL pointer");
-    const int64_t K = zsweep_nkeys(g);
-    k_zs_starts<<<(unsigned)((P + 1 + 255) / 256), 256, 0, as_stream(stream)>>>(sorted_word, P, K,
-                                                                               zstart);
-    MN_LAUNCH_CHECK("zsweep starts");
-    return MN_OK;
+    return key_starts(sorted_word, P, zsweep_nkeys(g), kZsKeyMask, zstart, as_stream(stream));
 }
 
 int mn_spread_zsweep(const mn_bins *g, float beta, int64_t P, int zseg, const int32_t *zstart,

@@ -66,7 +66,11 @@ class _PointsND:
         self.device = L.require_gpu()
         x64 = self._coords(x)
         self.P = x64[0].numel()
-        self.bins = E.make_bins(self.dim, self.w, self.n_up, cell_bytes=self._cell_bytes)
+        self._stream_interp = self._use_zstream and E.zstream_eligible(self.dim, self.w)
+        if self._stream_interp:
+            self.bins = E.make_bins(3, self.w, self.n_up, m=E.ZSTREAM_M)
+        else:
+            self.bins = E.make_bins(self.dim, self.w, self.n_up, cell_bytes=self._cell_bytes)
         self._zsweep = self._use_zsweep and E.zsweep_eligible(self.dim, self.w, self.n_up)
         if self._zsweep:
             self._zbins = E.make_bins(3, self.w, self.n_up, m=(8, 8, 1))
@@ -119,7 +123,7 @@ class _PointsND:
             with tm("setpts"):
                 i1, fr, key = E.setpts_t12(self.bins, x64, self.prec == "crit64")
             with tm("sort+tables"):
-                self.pts = E.SortedPoints(self.bins, i1, fr, key)
+                self.pts = E.SortedPoints(self.bins, i1, fr, key, stream=self._stream_interp)
                 del i1, fr, key
         self.sorted = True
         self._od = True
@@ -168,6 +172,7 @@ class Type1PlanND(_PointsND):
 
     _cell_bytes = E.SPREAD_CELL_BYTES
     _use_zsweep = True
+    _use_zstream = False
 
     def __init__(self, x, n_modes, eps=1e-6, isign=+1, upsampfac=2.0, prec="crit64",
                  sort_points=True, spread_method="auto"):
@@ -282,6 +287,7 @@ class Type2PlanND(_PointsND):
 
     _cell_bytes = E.INTERP_CELL_BYTES
     _use_zsweep = False
+    _use_zstream = True
 
     def __init__(self, x, n_modes, eps=1e-6, isign=-1, upsampfac=2.0, prec="crit64",
                  sort_points=False, spread_method="auto"):

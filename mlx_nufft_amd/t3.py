@@ -101,7 +101,9 @@ class GpuT3Plan:
         self.slab_mode = False
 
         # ---- targets: rescale, post factor, bin sort (device fp64) ----------
-        self.bins_trg = E.make_bins(3, self.w2, self.n_up, cell_bytes=E.INTERP_CELL_BYTES)
+        stream = E.zstream_eligible(3, self.w2)
+        self.bins_trg = (E.make_bins(3, self.w2, self.n_up, m=E.ZSTREAM_M) if stream else
+                         E.make_bins(3, self.w2, self.n_up, cell_bytes=E.INTERP_CELL_BYTES))
         hd = [2.0 * PI / nf for nf in self.nf]
         hg = [hd[d] * self.gam[d] for d in range(3)]
         h2 = [2.0 * PI / n for n in self.n_up]
@@ -116,7 +118,7 @@ class GpuT3Plan:
             L.d3(self.C), self.isign, self._flags, L.ptr(quad), len(dq),
             L.ptr3([t_i1[d] for d in range(3)]), L.ptr3([t_fr[d] for d in range(3)]),
             L.ptr(t_key), L.ptr(post), L.stream()), "t3 targets")
-        self.trg = E.SortedPoints(self.bins_trg, t_i1, t_fr, t_key, extra=post)
+        self.trg = E.SortedPoints(self.bins_trg, t_i1, t_fr, t_key, extra=post, stream=stream)
         del t_i1, t_fr, t_key, post
 
         # ---- mode deconvolution (-1)^|q| / phihat(2 pi q / n_up), q in

@@ -279,3 +279,35 @@ def test_pruned_equals_rocfft_path(mn, monkeypatch):
     b1, b2 = q1.execute(c), q2.execute(fk)
     assert np.linalg.norm(a1 - b1) / np.linalg.norm(b1) < 2e-6
     assert np.linalg.norm(a2 - b2) / np.linalg.norm(b2) < 2e-6
+
+
+@pytest.mark.parametrize("N,eps,cluster", [((21, 18, 14), 1e-5, False), ((8, 8, 8), 1e-6, True),
+                                           ((40, 33, 70), 1e-9, False),
+                                           ((24, 24, 24), 1e-1, False),
+                                           ((30, 20, 10), 1e-11, True)])
+def test_interp_zstream_vs_tiles(N, eps, cluster, mn, monkeypatch):
+    """The streaming 3D interpolation (sliding z window) equals the
+    independent-tile interpolation on the same plan inputs: partial blocks in
+    every dim, grids smaller than the window, clustered points at the
+    periodic corner, w = 2 .. 12."""
+    from mlx_nufft_amd import _engine as E
+
+    print(f"case interp zstream N={N} eps={eps} cluster={cluster}", flush=True)
+    rng = np.random.default_rng(17)
+    M = 60_000
+    if cluster:
+        x = [np.concatenate([-np.pi + rng.uniform(0, 0.2, M // 2),
+                             np.pi - rng.uniform(0, 0.2, M - M // 2)]) for _ in range(3)]
+    else:
+        x = _pts(rng, 3, M)
+    monkeypatch.setenv("MN_INTERP", "zstream")
+    pz = mn.Type2PlanND(tuple(x), N, eps=eps)
+    monkeypatch.setenv("MN_INTERP", "tiles")
+    pt = mn.Type2PlanND(tuple(x), N, eps=eps)
+    assert pz.pts.kind == "zstream" and pt.pts.kind == "tiles"
+    g = torch.from_numpy(_cplx(rng, tuple(pz.n_up))).cuda()
+    oz = torch.empty(M, dtype=torch.complex64, device="cuda")
+    ot = torch.empty(M, dtype=torch.complex64, device="cuda")
+    E.interp(pz.pts, pz.beta, g, oz)
+    E.interp(pt.pts, pt.beta, g, ot)
+    assert float((oz - ot).abs().max() / ot.abs().max()) < 1e-6
