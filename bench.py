@@ -6,9 +6,11 @@ re/im i.i.d. N(0,1) (numpy default_rng(0)), N = 256^3 modes, eps = 1e-5,
 isign = +1, upsampfac 2 (w = 6, fine grid 512^3).
 
 A step is one end-to-end pass with inputs already resident in HBM:
-set_sources (fp64 fold/rescale, stable bin sort, subproblem table) +
-execute (zero grid, spread, 512^3 FFT, crop/deconvolve). W untimed warmup
-steps, then K steps between torch.cuda.synchronize() calls.
+set_sources (fp64 fold/rescale, stable sort, z-sweep key starts) + execute
+(spread, pruned 512^3 FFT with crop/deconvolution). W untimed warmup steps,
+then K steps between torch.cuda.synchronize() calls; HIP events recorded on
+the launch stream inside the timed region give per-step min/median/max and
+per-stage times (read after the region, so nothing synchronises inside it).
 
 One JSON line is printed:
   value      = M / (ms_per_step) in NU pts/s (end to end, device-resident)
@@ -120,21 +122,27 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    plan.profile = True
-    stage_sum = {}
+    # Timed region: K steps between two synchronisations. HIP events on the
+    # launch stream bracket every step and every stage (the spread kernel is
+    # one launch per step); they are read only after the region ends.
+    step_ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(args.steps)]
+    plan.profile = plan.profile_deferred = True
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for a, b in step_ev:
+        a.record()
         step()
-        prof = dict(plan.last_profile)
-        if not args.exec_only:
-            prof.update(plan.last_setpts_profile)
-        for k, v in prof.items():
-            stage_sum[k] = stage_sum.get(k, 0.0) + v
+        b.record()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    plan.profile = False
+    plan.profile = plan.profile_deferred = False
     ms = (t1 - t0) * 1e3 / args.steps
+    step_ms = sorted(a.elapsed_time(b) for a, b in step_ev)
+    stage_sum = {}
+    for _, prof in plan.drain_profiles():
+        for k, v in prof.items():
+            stage_sum[k] = stage_sum.get(k, 0.0) + v
     stages = {k: v / args.steps for k, v in stage_sum.items()}
 
     spread_ms = stages.get("spread", float("nan"))
@@ -192,6 +200,8 @@ def main():
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "kernel": spread_kernel, "alg_bytes_per_launch": alg_bytes,
                      "ms_per_launch": spread_ms},
+        "step_ms": {"min": step_ms[0], "median": step_ms[len(step_ms) // 2],
+                    "max": step_ms[-1]},
         "stages_ms": {k: round(v, 4) for k, v in stages.items()},
         "exec_ms": exec_ms,
         "exec_pts_per_s": M / (exec_ms * 1e-3) if exec_ms else None,

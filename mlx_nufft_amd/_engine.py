@@ -362,8 +362,9 @@ class StageTimer:
         b.record()
         self.events.append((name, a, b))
 
-    def times_ms(self):
-        torch.cuda.synchronize()
+    def times_ms(self, sync=True):
+        if sync:
+            torch.cuda.synchronize()
         out = {}
         for name, a, b in self.events:
             out[name] = out.get(name, 0.0) + a.elapsed_time(b)

@@ -61,7 +61,9 @@ class _PointsND:
         self.n_up = [next235even(max(2 * self.w, int(np.ceil(upsampfac * n)))) for n in self.N]
         self._sort_points = bool(sort_points)
         self.profile = False
+        self.profile_deferred = False
         self.last_profile = {}
+        self._deferred = []
 
         self.device = L.require_gpu()
         x64 = self._coords(x)
@@ -127,7 +129,7 @@ class _PointsND:
                 del i1, fr, key
         self.sorted = True
         self._od = True
-        self._finish_profile(tm)
+        self._finish_profile(tm, "setpts")
         self.last_setpts_profile = dict(self.last_profile) if self.profile else {}
 
     @property
@@ -159,9 +161,26 @@ class _PointsND:
     def _timer(self):
         return E.StageTimer(self.profile)
 
-    def _finish_profile(self, tm):
-        if self.profile:
+    def _finish_profile(self, tm, kind="execute"):
+        """With profile on, per-stage HIP-event times of the last call land in
+        last_profile (one stream synchronisation). With profile_deferred as
+        well, the events are kept unread (no synchronisation) until
+        drain_profiles()."""
+        if not self.profile:
+            return
+        if self.profile_deferred:
+            self._deferred.append((kind, tm))
+            self.last_profile = {}
+        else:
             self.last_profile = tm.times_ms()
+
+    def drain_profiles(self):
+        """[(kind, {stage: ms})] of the deferred calls, in call order (one
+        synchronisation); kind is "setpts" or "execute"."""
+        torch.cuda.synchronize()
+        out = [(kind, tm.times_ms(sync=False)) for kind, tm in self._deferred]
+        self._deferred = []
+        return out
 
 
 class Type1PlanND(_PointsND):
