@@ -11,6 +11,10 @@ set_sources (fp64 fold/rescale, stable sort, z-sweep key starts) + execute
 then K steps between torch.cuda.synchronize() calls; HIP events recorded on
 the launch stream inside the timed region give per-step min/median/max and
 per-stage times (read after the region, so nothing synchronises inside it).
+The Python heap is collected and frozen (gc.collect + gc.freeze) before the
+region: a full collection of the interpreter's import-time objects costs
+30-40 ms of host time, and one that lands inside the region leaves the GPU
+idle for that long. Collector pauses inside the region are reported.
 
 One JSON line is printed:
   value      = M / (ms_per_step) in NU pts/s (end to end, device-resident)
@@ -22,6 +26,7 @@ One JSON line is printed:
 """
 
 import argparse
+import gc
 import json
 import os
 import pathlib
@@ -128,17 +133,35 @@ def main():
     step_ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                for _ in range(args.steps)]
     plan.profile = plan.profile_deferred = True
+    host_ms, gc_ms, gc_t = [], [], [0.0]
+
+    def gc_cb(phase, info):
+        if phase == "start":
+            gc_t[0] = time.perf_counter()
+        else:
+            gc_ms.append((time.perf_counter() - gc_t[0]) * 1e3)
+
+    # A full collection of the interpreter's import-time objects takes 30-40 ms
+    # of host time; landing in the timed region it starves the GPU for that
+    # long. Collect and freeze them first (GC stays on; pauses are reported).
+    gc.collect()
+    gc.freeze()
+    gc.callbacks.append(gc_cb)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for a, b in step_ev:
         a.record()
+        h = time.perf_counter()
         step()
+        host_ms.append((time.perf_counter() - h) * 1e3)
         b.record()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
+    gc.callbacks.remove(gc_cb)
     plan.profile = plan.profile_deferred = False
     ms = (t1 - t0) * 1e3 / args.steps
-    step_ms = sorted(a.elapsed_time(b) for a, b in step_ev)
+    step_raw = [a.elapsed_time(b) for a, b in step_ev]
+    step_ms = sorted(step_raw)
     stage_sum = {}
     for _, prof in plan.drain_profiles():
         for k, v in prof.items():
@@ -201,7 +224,10 @@ def main():
                      "kernel": spread_kernel, "alg_bytes_per_launch": alg_bytes,
                      "ms_per_launch": spread_ms},
         "step_ms": {"min": step_ms[0], "median": step_ms[len(step_ms) // 2],
-                    "max": step_ms[-1]},
+                    "max": step_ms[-1], "argmax": step_raw.index(step_ms[-1])},
+        "host_ms_per_step": {"median": sorted(host_ms)[len(host_ms) // 2], "max": max(host_ms),
+                             "argmax": host_ms.index(max(host_ms))},
+        "gc_pauses_ms": [round(v, 2) for v in gc_ms],
         "stages_ms": {k: round(v, 4) for k, v in stages.items()},
         "exec_ms": exec_ms,
         "exec_pts_per_s": M / (exec_ms * 1e-3) if exec_ms else None,

@@ -102,17 +102,19 @@ def sort_keys(key, nbits):
     return skey, perm
 
 
-def sort_pairs(key, nbits, cols, outs=None):
+def sort_pairs(key, nbits, cols, outs=None, skey=None, perm=None, ws=None):
     """Stable sort of uint32 keys on their low nbits bits, carrying 32-bit
-    payload columns (int32/float32 tensors of P elements) into outs (new
-    tensors if None): (sorted keys, perm, sorted columns)."""
+    payload columns (int32/float32 tensors of P elements) into outs:
+    (sorted keys, perm, sorted columns). Outputs and the workspace are new
+    tensors unless given."""
     P = key.numel()
     lib = L.lib()
     ncols = len(cols)
-    ws = torch.empty(int(lib.mn_sort_pairs_workspace_bytes(P, ncols)), dtype=torch.uint8,
-                     device=key.device)
-    skey = torch.empty_like(key)
-    perm = torch.empty_like(key)
+    ws_bytes = int(lib.mn_sort_pairs_workspace_bytes(P, ncols))
+    if ws is None or ws.numel() < ws_bytes:
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=key.device)
+    skey = torch.empty_like(key) if skey is None else skey
+    perm = torch.empty_like(key) if perm is None else perm
     if outs is None:
         outs = [torch.empty_like(c) for c in cols]
     cin = (ctypes.c_void_p * max(1, ncols))(*[c.data_ptr() for c in cols])
@@ -220,27 +222,39 @@ def zsweep_eligible(dim, w, n_up):
 class ZSweepPoints:
     """Point state for the z-sweep spread: packed point words and fractions
     (setpts), stably sorted together by the z-sweep key, and the key start
-    table."""
+    table. Given the previous point set of the same plan (prev) with the
+    same P and geometry, its device buffers are reused, so re-pointing
+    allocates nothing; prev's contents are overwritten in stream order."""
 
     kind = "zsweep"
 
-    def __init__(self, bins, x64, prec64):
+    def __init__(self, bins, x64, prec64, prev=None):
         lib = L.lib()
         dev = x64[0].device
         self.bins = bins
         self.P = P = x64[0].numel()
-        word = torch.empty(P, dtype=torch.int32, device=dev)
-        fr = torch.empty((3, P), dtype=torch.float32, device=dev)
+        self.K = K = int(lib.mn_zsweep_nkeys(ctypes.byref(bins)))
+        same = (prev is not None and prev.P == P and prev.K == K and prev.dev == dev)
+        self.dev = dev
+        self._bufs = bufs = prev._bufs if same else {}
+
+        def buf(name, shape, dtype):
+            if name not in bufs:
+                bufs[name] = torch.empty(shape, dtype=dtype, device=dev)
+            return bufs[name]
+
+        word = buf("word_in", P, torch.int32)
+        fr = buf("fr_in", (3, P), torch.float32)
         L.check(lib.mn_zsweep_setpts(ctypes.byref(bins), P, L.ptr3(x64), int(bool(prec64)),
                                      L.ptr(word), L.ptr3(_rows(fr, 3)), L.stream()),
                 "zsweep setpts")
-        K = int(lib.mn_zsweep_nkeys(ctypes.byref(bins)))
-        self.K = K
-        self.frs = torch.empty_like(fr)
-        self.word, self.perm, _ = sort_pairs(word, max(1, (K - 1).bit_length()), _rows(fr, 3),
-                                             _rows(self.frs, 3))
-        del word, fr
-        self.zstart = torch.empty(K + 1, dtype=torch.int32, device=dev)
+        self.frs = buf("frs", (3, P), torch.float32)
+        ws_bytes = int(lib.mn_sort_pairs_workspace_bytes(P, 3))
+        self.word, self.perm, _ = sort_pairs(
+            word, max(1, (K - 1).bit_length()), _rows(fr, 3), _rows(self.frs, 3),
+            skey=buf("word", P, torch.int32), perm=buf("perm", P, torch.int32),
+            ws=buf("ws", ws_bytes, torch.uint8))
+        self.zstart = buf("zstart", K + 1, torch.int32)
         L.check(lib.mn_zsweep_starts(ctypes.byref(bins), P, L.ptr(self.word), L.ptr(self.zstart),
                                      L.stream()), "zsweep starts")
 

@@ -120,7 +120,10 @@ class _PointsND:
         tm = self._timer()
         if self._zsweep:
             with tm("setpts+sort+tables"):
-                self.pts = E.ZSweepPoints(self._zbins, x64, self.prec == "crit64")
+                prev = getattr(self, "pts", None)
+                self.pts = E.ZSweepPoints(self._zbins, x64, self.prec == "crit64",
+                                          prev=prev if isinstance(prev, E.ZSweepPoints) else None)
+                del prev
         else:
             with tm("setpts"):
                 i1, fr, key = E.setpts_t12(self.bins, x64, self.prec == "crit64")
@@ -276,7 +279,8 @@ class Type1PlanND(_PointsND):
         if P < 1 or not all(v.numel() == P for v in x64):
             raise ValueError("coordinate arrays must be non-empty, equal length")
         self.P = P
-        self.pts = None
+        if not (isinstance(self.pts, E.ZSweepPoints) and self.pts.P == P):
+            self.pts = None  # nothing to reuse: free the old point state first
         self._set_points(x64)
         return self
 

@@ -201,6 +201,28 @@ def test_set_sources_equals_fresh(dim, N, mn):
         p.set_sources(x3, backend="cuda")
 
 
+def test_set_sources_reuses_zsweep_buffers(mn):
+    """Re-pointing a 3D z-sweep plan with the same P keeps its device point
+    buffers (no allocation per set_sources) and still equals a fresh plan;
+    a different P allocates anew."""
+    print("case set_sources zsweep buffer reuse", flush=True)
+    rng = np.random.default_rng(21)
+    N, P = (32, 24, 20), 60_000
+    c = _cplx(rng, P)
+    p = mn.Type1PlanND(tuple(_pts(rng, 3, P)), N, eps=1e-5)
+    assert p.pts.kind == "zsweep"
+    ptrs = {k: t.data_ptr() for k, t in p.pts._bufs.items()}
+    for _ in range(2):
+        x = _pts(rng, 3, P)
+        p.set_sources(x)
+        assert {k: t.data_ptr() for k, t in p.pts._bufs.items()} == ptrs
+        f_rp = p.execute(c)
+        f_fr = mn.Type1PlanND(tuple(x), N, eps=1e-5).execute(c)
+        assert np.array_equal(f_rp, f_fr)
+    p.set_sources(_pts(rng, 3, P - 1000))
+    assert p.pts.perm.numel() == P - 1000
+
+
 @pytest.mark.parametrize("dim,N", [(1, (90,)), (2, (40, 36)), (3, (24, 20, 16))])
 def test_adjoint_identity(dim, N, mn):
     """<T1 c, f> == <c, T2 f> with T2 at the negated sign (ref:
