@@ -117,6 +117,14 @@ __device__ __forceinline__ float es_weight(float d, float bl2e, float inv_hw) {
     return __builtin_amdgcn_exp2f(bl2e * (__builtin_amdgcn_sqrtf(t) - 1.0f));
 }
 
+// The same kernel at the scaled distance z = 2d/w: the exp2 argument
+// bl2e*(sqrt(t) - 1) is one fma. For |z| > 1 it returns e^-beta (t clamped
+// to 0); callers mask those taps.
+__device__ __forceinline__ float es_weight_z(float z, float bl2e) {
+    const float t = fmaxf(fmaf(-z, z, 1.0f), 0.0f);
+    return __builtin_amdgcn_exp2f(fmaf(bl2e, __builtin_amdgcn_sqrtf(t), -bl2e));
+}
+
 // Map a cell index that is at most one period outside [0, n) back into it.
 __device__ __forceinline__ int wrap1(int i, int n) {
     i += (i < 0) ? n : 0;

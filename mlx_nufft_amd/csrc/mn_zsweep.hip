@@ -22,7 +22,9 @@
 // Per batch of up to 64 points (two z-steps), a lane-per-point prologue
 // evaluates the ES weights once and writes a table row: the 8 x-weights of
 // the block's columns times the strength (complex), the 8 y-weights and the
-// W z-weights. The sweep then costs each point 2*W FMAs per lane.
+// W z-weights. Per z-step and 4x4 column quadrant, a list holds the byte
+// offsets of the rows of the points that touch the quadrant; the 16 lanes
+// of the quadrant walk it, each point costing 2 MULs and 2*W FMAs per lane.
 //
 // ref: nd.py:492-579 (the reference's output-driven spread this replaces),
 // nd.py:298-372 (its bin sort and subproblem tables).
@@ -34,9 +36,9 @@ namespace {
 constexpr int ZB = kZsBlock;  // block size along x and y (lanes: 8 x 8)
 constexpr int ZST = 4;     // z-slices staged in LDS per store
 constexpr int ZCH = 2;     // z-steps per prologue batch
-constexpr int UNR = 4;     // points per unrolled sweep step
+constexpr int UNR = 4;     // points per unrolled sweep step (then one at a time)
 constexpr int NR = 4;      // key ranges per z: own, -x, -y, -xy
-constexpr int REC = 32;    // floats per table row
+constexpr int REC = 36;    // floats per table row (32 used; the pad spreads rows over banks)
 
 // Lane layout: the wave's 64 lanes form four 16-lane groups, one per 4x4
 // quadrant of the 8x8 column block; lane l owns column
@@ -45,17 +47,18 @@ __device__ __forceinline__ int lane_cx(int l) { return ((l >> 5) << 2) + ((l >> 
 __device__ __forceinline__ int lane_cy(int l) { return (((l >> 4) & 1) << 2) + (l & 3); }
 
 // Stage the finished cell of each column; every ZST z-slices (or at the
-// segment end) the wave writes them out with 4 consecutive lanes per column
-// storing 4 consecutive z.
+// segment end) the wave writes them out with ZST consecutive lanes per
+// column storing ZST consecutive z.
 __device__ __forceinline__ void store_stage(float2 (*stage)[64], float2 *__restrict__ grid,
                                             int lane, int s, int zw, int n1, int n2, int bx,
                                             int by, float wr, float wi, bool last) {
+    static_assert(ZST == 2 || ZST == 4 || ZST == 8, "ZST lanes per column");
     stage[s][lane] = make_float2(wr, wi);
     if (s == ZST - 1 || last) {
         __syncthreads();
         const int zb = zw - s, nz = s + 1;
-        for (int colb = 0; colb < 64; colb += 16) {
-            const int col = colb + (lane >> 2), zo = lane & 3;
+        for (int colb = 0; colb < 64; colb += 64 / ZST) {
+            const int col = colb + lane / ZST, zo = lane % ZST;
             if (zo < nz) {
                 const int gx = ZB * bx + lane_cx(col), gy = ZB * by + lane_cy(col);
                 grid[((int64_t)gx * n1 + gy) * n2 + zb + zo] = stage[zo][col];
@@ -63,6 +66,156 @@ __device__ __forceinline__ void store_stage(float2 (*stage)[64], float2 *__restr
         }
         __syncthreads();
     }
+}
+
+// One point of a quadrant list: the lane's column weight times the strength
+// (vr, vi) and the point's z-weights, read from its table row at rec.
+template <int W>
+__device__ __forceinline__ void sweep_load(const char *rec, int xo, int yo, float &vr, float &vi,
+                                           float (&wz)[ZB]) {
+    const float2 wxc = *reinterpret_cast<const float2 *>(rec + xo);
+    const float wyv = *reinterpret_cast<const float *>(rec + yo);
+    const float4 z0 = *reinterpret_cast<const float4 *>(rec + 4 * 3 * ZB);
+    wz[0] = z0.x, wz[1] = z0.y, wz[2] = z0.z, wz[3] = z0.w;
+    if constexpr (W > 4) {
+        const float4 z1 = *reinterpret_cast<const float4 *>(rec + 4 * (3 * ZB + 4));
+        wz[4] = z1.x, wz[5] = z1.y, wz[6] = z1.z, wz[7] = z1.w;
+    }
+    vr = wxc.x * wyv;
+    vi = wxc.y * wyv;
+}
+
+template <int W>
+__device__ __forceinline__ void sweep_fma(float vr, float vi, const float (&wz)[ZB],
+                                          float (&wre)[W], float (&wim)[W]) {
+#pragma unroll
+    for (int a = 0; a < W; ++a) {
+        wre[a] = fmaf(vr, wz[a], wre[a]);
+        wim[a] = fmaf(vi, wz[a], wim[a]);
+    }
+}
+
+// The wave's position in the key ranges of one z-step pair (ZCH z-steps x
+// NR source ranges): the pair's first z, the next batch element and the
+// number of elements. All uniform across the wave.
+struct ZCursor {
+    int zc, bat, tot;
+};
+
+// The ranges themselves, in LDS (the wave reads them back with broadcast
+// loads): element e of range q, with pf[q] <= e < pf[q + 1], is sorted
+// point e + dj[q]; pf is the running sum of the range sizes.
+struct __align__(16) ZRanges {
+    int pf[ZCH * NR];
+    int dj[ZCH * NR];
+};
+static_assert(ZCH * NR == 8, "ranges are read as two int4");
+
+// The four source blocks of a block (itself, -x, -y, -xy) and the segment end.
+struct ZBlocks {
+    int bx, by, bxm, bym, nby;
+    int n2, zend;
+};
+
+// Load the ranges of the pair starting at zc: lane i < 8 takes range
+// q = i (z-step i / NR, source i % NR), then a shuffle scan forms pf.
+__device__ __forceinline__ void zc_load(ZCursor &k, int zc, const ZBlocks b,
+                                        const int32_t *__restrict__ zstart, ZRanges &rg,
+                                        int lane) {
+    k.zc = zc;
+    k.bat = 0;
+    int st = 0, cnt = 0;
+    if (lane < ZCH * NR) {
+        const int r = lane % NR, z = zc + lane / NR;
+        if (z < b.zend) {
+            const int zz = z < 0 ? z + b.n2 : z;
+            // source r: bit 0 = -x neighbour, bit 1 = -y neighbour; its key
+            // classes [lo, hi] are those that reach this block
+            const int blk = ((r & 1) ? b.bxm : b.bx) * b.nby + ((r & 2) ? b.bym : b.by);
+            const int lo = r == 0 ? 0 : (r == 2 ? 1 : 2), hi = (r & 2) ? 2 : 3;
+            const int64_t kb = ((int64_t)blk * b.n2 + zz) * 4;
+            st = zstart[kb + lo];
+            cnt = zstart[kb + hi + 1] - st;
+        }
+    }
+    int incl = cnt;
+#pragma unroll
+    for (int d = 1; d < ZCH * NR; d <<= 1) {
+        const int v = __shfl_up(incl, d, 64);
+        incl += (lane >= d) ? v : 0;
+    }
+    if (lane < ZCH * NR) {
+        rg.pf[lane] = incl - cnt;
+        rg.dj[lane] = st - (incl - cnt);
+    }
+    k.tot = __shfl(incl, ZCH * NR - 1, 64);
+}
+
+// Advance past exhausted (or empty) pairs; stops at the segment end.
+__device__ __forceinline__ void zc_settle(ZCursor &k, const ZBlocks b,
+                                          const int32_t *__restrict__ zstart, ZRanges &rg,
+                                          int lane) {
+    while (k.bat >= k.tot && k.zc < b.zend) zc_load(k, k.zc + ZCH, b, zstart, rg, lane);
+}
+
+// One lane's point of a batch, its loads issued (the strength, which needs
+// src, is loaded one batch later).
+struct ZPoint {
+    int zc, nb;          // the batch's pair and size (uniform; nb = 0: done)
+    bool valid;
+    int tsel, r;         // z-step within the pair and source range
+    uint32_t wd, src;    // sorted word; index of the strength in c
+    float fx, fy, fz;
+    float2 pv;           // prephase (1 if none)
+};
+
+__device__ __forceinline__ ZPoint zp_issue(ZCursor &k, const ZBlocks b, int lane,
+                                           const int32_t *__restrict__ zstart, ZRanges &rg,
+                                           const uint32_t *__restrict__ perm,
+                                           const uint32_t *__restrict__ word, const CF3s &frs,
+                                           const float2 *__restrict__ pre) {
+    ZPoint q;
+    q.zc = k.zc;
+    q.nb = k.zc < b.zend ? min(64, k.tot - k.bat) : 0;
+    q.valid = lane < q.nb;
+    q.tsel = -1;
+    q.r = 0;
+    q.wd = 0;
+    q.src = 0;
+    q.fx = q.fy = q.fz = 0.f;
+    q.pv = make_float2(1.f, 0.f);
+    if (q.valid) {
+        // the element's range: the last q with pf[q] <= e (empty ranges
+        // repeat pf and are passed over)
+        const int4 pa = *reinterpret_cast<const int4 *>(rg.pf);
+        const int4 pb = *reinterpret_cast<const int4 *>(rg.pf + 4);
+        const int4 da = *reinterpret_cast<const int4 *>(rg.dj);
+        const int4 db = *reinterpret_cast<const int4 *>(rg.dj + 4);
+        const int pf[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+        const int djs[8] = {da.x, da.y, da.z, da.w, db.x, db.y, db.z, db.w};
+        const int e = k.bat + lane;
+        int i = 0, dj = djs[0];
+#pragma unroll
+        for (int s = 1; s < ZCH * NR; ++s) {
+            const bool ge = e >= pf[s];
+            i += ge ? 1 : 0;
+            dj = ge ? djs[s] : dj;
+        }
+        q.tsel = i / NR;
+        q.r = i % NR;
+        const uint32_t j = (uint32_t)(e + dj);
+        q.wd = word[j];
+        q.fx = frs.p[0][j];
+        q.fy = frs.p[1][j];
+        q.fz = frs.p[2][j];
+        q.src = perm ? perm[j] : j;
+        if (pre) q.pv = pre[j];
+    }
+    if (k.zc < b.zend) {
+        k.bat += 64;
+        zc_settle(k, b, zstart, rg, lane);
+    }
+    return q;
 }
 
 template <int W>
@@ -78,10 +231,13 @@ __global__ __launch_bounds__(64) void k_spread_zsweep(int n0, int n1, int n2, in
                                                       float2 *__restrict__ grid) {
     // table rows: x-weights of the block's 8 columns times the strength
     // (complex, 16 floats), y-weights of its 8 rows, W z-weights (padded to
-    // 8); row 64 stays zero and pads the quadrant lists.
+    // 8); row 64 stays zero and pads the shorter quadrant lists, whose
+    // entries are row byte offsets.
     __shared__ __align__(16) float table[(64 + 1) * REC];
-    __shared__ __align__(16) uint8_t lists[ZCH][4][64];
+    __shared__ __align__(16) uint16_t lists[ZCH][4][64];
+    constexpr uint32_t kPad = 64u * REC * 4u;  // byte offset of the zero row
     __shared__ float2 stage[ZST][64];
+    __shared__ ZRanges rg;
     const int64_t nw = (int64_t)nbx * nby * nseg;
     int64_t wid = xcd_remap(blockIdx.x, nw);
     const int seg = (int)(wid % nseg);
@@ -90,148 +246,131 @@ __global__ __launch_bounds__(64) void k_spread_zsweep(int n0, int n1, int n2, in
     const int z0 = seg * zseg, zend = min(z0 + zseg, n2);
     const int lane = threadIdx.x, grp = lane >> 4;
     const int cxl = lane_cx(lane), cyl = lane_cy(lane);
+    const int xo = 8 * cxl, yo = 4 * (2 * ZB + cyl);  // byte offsets of this lane's x / y weight
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     if (lane < REC) table[64 * REC + lane] = 0.f;
-    const int bxm = bx == 0 ? nbx - 1 : bx - 1, bym = by == 0 ? nby - 1 : by - 1;
-    const int blk[NR] = {bx * nby + by, bxm * nby + by, bx * nby + bym, bxm * nby + bym};
-    const int clo[NR] = {0, 2, 1, 2}, chi[NR] = {3, 3, 2, 2};
+    ZBlocks bk;
+    bk.bx = bx;
+    bk.by = by;
+    bk.bxm = bx == 0 ? nbx - 1 : bx - 1;
+    bk.bym = by == 0 ? nby - 1 : by - 1;
+    bk.nby = nby;
+    bk.n2 = n2;
+    bk.zend = zend;
     float wre[W], wim[W];
 #pragma unroll
     for (int a = 0; a < W; ++a) wre[a] = wim[a] = 0.f;
     int zw = z0 - (W - 1);  // z of window cell 0
-    for (int zc = z0 - (W - 1); zc < zend; zc += ZCH) {
-        int pf[ZCH * NR + 1], rs[ZCH * NR];
-        pf[0] = 0;
+
+    // Software pipeline over batches: while batch p1 is built and swept,
+    // the strengths of p2 and the words / fractions / perm of p3 load.
+    ZCursor cur;
+    zc_load(cur, z0 - (W - 1), bk, zstart, rg, lane);
+    zc_settle(cur, bk, zstart, rg, lane);
+    ZPoint p1 = zp_issue(cur, bk, lane, zstart, rg, perm, word, frs, pre);
+    float2 c1 = p1.valid ? c[p1.src] : make_float2(0.f, 0.f);
+    ZPoint p2 = zp_issue(cur, bk, lane, zstart, rg, perm, word, frs, pre);
+    while (p1.nb > 0) {
+        const float2 c2 = p2.valid ? c[p2.src] : make_float2(0.f, 0.f);
+        const ZPoint p3 = zp_issue(cur, bk, lane, zstart, rg, perm, word, frs, pre);
+        const int zc = p1.zc;
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < ZCH * 4 * 32; k += 64)
+            reinterpret_cast<uint32_t *>(lists)[k + lane] = kPad | (kPad << 16);
+        int touch = 0;
+        if (p1.valid) {
+            // first tap relative to this block: the word's in-block cell,
+            // minus 8 for points of the -x / -y neighbour blocks
+            const int ox = (int)((p1.wd >> kZsKeyBits) & 7u) - ((p1.r & 1) ? ZB : 0);
+            const int oy = (int)((p1.wd >> (kZsKeyBits + 3)) & 7u) - ((p1.r & 2) ? ZB : 0);
+            const float2 cv = make_float2(c1.x * p1.pv.x - c1.y * p1.pv.y,
+                                          c1.x * p1.pv.y + c1.y * p1.pv.x);
+            float4 *rec = reinterpret_cast<float4 *>(table + lane * REC);
+            float wx[ZB], wy[ZB], wz[ZB];
+            // scaled distance of column q from the point:
+            // (q - (ox + fx)) * 2/W = q*2/W - (ox + fx)*2/W
+            constexpr float ih = 2.0f / W;
+            const float sx = ((float)ox + p1.fx) * ih, sy = ((float)oy + p1.fy) * ih;
+            const float sz = p1.fz * ih;
+#pragma unroll
+            for (int q = 0; q < ZB; ++q) {
+                const float ex = es_weight_z((float)q * ih - sx, bl2e);
+                const float ey = es_weight_z((float)q * ih - sy, bl2e);
+                wx[q] = ((unsigned)(q - ox) < (unsigned)W) ? ex : 0.f;
+                wy[q] = ((unsigned)(q - oy) < (unsigned)W) ? ey : 0.f;
+                wz[q] = q < W ? es_weight_z((float)q * ih - sz, bl2e) : 0.f;
+            }
+#pragma unroll
+            for (int q = 0; q < ZB; q += 2)
+                rec[q / 2] = make_float4(cv.x * wx[q], cv.y * wx[q], cv.x * wx[q + 1],
+                                         cv.y * wx[q + 1]);
+            rec[4] = make_float4(wy[0], wy[1], wy[2], wy[3]);
+            rec[5] = make_float4(wy[4], wy[5], wy[6], wy[7]);
+            rec[6] = make_float4(wz[0], wz[1], wz[2], wz[3]);
+            rec[7] = make_float4(wz[4], wz[5], wz[6], wz[7]);
+            // quadrants (qx, qy) the footprint [ox, ox + W) x [oy, oy + W) meets
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int qx = q >> 1, qy = q & 1;
+                const bool hit = ox < 4 * qx + 4 && ox + W > 4 * qx && oy < 4 * qy + 4 &&
+                                 oy + W > 4 * qy;
+                touch |= hit ? (1 << q) : 0;
+            }
+        }
+        // per z-step and quadrant: the batch rows that touch it, in order
+        int cnt[ZCH][4];
+#pragma unroll
+        for (int t = 0; t < ZCH; ++t)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const bool mine = p1.tsel == t && ((touch >> q) & 1);
+                const uint64_t bq = __ballot(mine);
+                cnt[t][q] = __popcll(bq);
+                if (mine) lists[t][q][__popcll(bq & lt_mask)] = (uint16_t)(lane * REC * 4);
+            }
+        __syncthreads();
 #pragma unroll
         for (int t = 0; t < ZCH; ++t) {
-            const int z = zc + t;
-            const int zz = z < 0 ? z + n2 : z;
+            const int nit = max(max(cnt[t][0], cnt[t][1]), max(cnt[t][2], cnt[t][3]));
+            if (nit == 0) continue;
+            const int ze = zc + t;
+            while (zw < ze) {
+                if (zw >= z0)
+                    store_stage(stage, grid, lane, (zw - z0) % ZST, zw, n1, n2, bx, by,
+                                wre[0], wim[0], zw == zend - 1);
 #pragma unroll
-            for (int r = 0; r < NR; ++r) {
-                const int i = t * NR + r;
-                int st = 0, cnt = 0;
-                if (z < zend) {
-                    const int64_t kb = ((int64_t)blk[r] * n2 + zz) * 4;
-                    st = zstart[kb + clo[r]];
-                    cnt = zstart[kb + chi[r] + 1] - st;
+                for (int a = 0; a < W - 1; ++a) {
+                    wre[a] = wre[a + 1];
+                    wim[a] = wim[a + 1];
                 }
-                rs[i] = st;
-                pf[i + 1] = pf[i] + cnt;
+                wre[W - 1] = wim[W - 1] = 0.f;
+                ++zw;
+            }
+            const uint16_t *lq = lists[t][grp];
+            const char *tb = reinterpret_cast<const char *>(table);
+            const int nit4 = nit & ~(UNR - 1);
+            int it = 0;
+            for (; it < nit4; it += UNR) {
+                const uint2 pk = *reinterpret_cast<const uint2 *>(lq + it);
+                const uint32_t off[UNR] = {pk.x & 0xffffu, pk.x >> 16, pk.y & 0xffffu,
+                                           pk.y >> 16};
+                float vr[UNR], vi[UNR], wzz[UNR][ZB];
+#pragma unroll
+                for (int u = 0; u < UNR; ++u)
+                    sweep_load<W>(tb + off[u], xo, yo, vr[u], vi[u], wzz[u]);
+#pragma unroll
+                for (int u = 0; u < UNR; ++u) sweep_fma<W>(vr[u], vi[u], wzz[u], wre, wim);
+            }
+            for (; it < nit; ++it) {
+                float vr, vi, wzz[ZB];
+                sweep_load<W>(tb + lq[it], xo, yo, vr, vi, wzz);
+                sweep_fma<W>(vr, vi, wzz, wre, wim);
             }
         }
-        const int tot = pf[ZCH * NR];
-        for (int bat = 0; bat < tot; bat += 64) {
-            const int nb = min(64, tot - bat);
-            __syncthreads();
-            reinterpret_cast<uint32_t *>(lists)[lane] = 0x40404040u;
-            reinterpret_cast<uint32_t *>(lists)[lane + 64] = 0x40404040u;
-            const bool valid = lane < nb;
-            int tsel = -1, touch = 0;
-            if (valid) {
-                const int e = bat + lane;
-                int i = 0;
-#pragma unroll
-                for (int q = 1; q < ZCH * NR; ++q) i += (e >= pf[q]) ? 1 : 0;
-                int st = rs[0], p0 = pf[0];
-#pragma unroll
-                for (int q = 1; q < ZCH * NR; ++q)
-                    if (q == i) {
-                        st = rs[q];
-                        p0 = pf[q];
-                    }
-                tsel = i / NR;
-                const int64_t j = (int64_t)st + (e - p0);
-                // first tap relative to this block: the word's in-block cell,
-                // minus 8 for points of the -x / -y neighbour blocks
-                const uint32_t wd = word[j];
-                const int r = i % NR;
-                const int ox = (int)((wd >> kZsKeyBits) & 7u) - ((r & 1) ? ZB : 0);
-                const int oy = (int)((wd >> (kZsKeyBits + 3)) & 7u) - ((r & 2) ? ZB : 0);
-                const float fx = frs.p[0][j], fy = frs.p[1][j], fz = frs.p[2][j];
-                float2 cv = perm ? c[perm[j]] : c[j];
-                if (pre) {
-                    const float2 pv = pre[j];
-                    cv = make_float2(cv.x * pv.x - cv.y * pv.y, cv.x * pv.y + cv.y * pv.x);
-                }
-                float4 *rec = reinterpret_cast<float4 *>(table + lane * REC);
-                float wx[ZB], wy[ZB], wz[ZB];
-#pragma unroll
-                for (int q = 0; q < ZB; ++q) {
-                    const int ax = q - ox, ay = q - oy;
-                    wx[q] = ((unsigned)ax < (unsigned)W) ? es_weight((float)ax - fx, bl2e, inv_hw) : 0.f;
-                    wy[q] = ((unsigned)ay < (unsigned)W) ? es_weight((float)ay - fy, bl2e, inv_hw) : 0.f;
-                    wz[q] = q < W ? es_weight((float)q - fz, bl2e, inv_hw) : 0.f;
-                }
-#pragma unroll
-                for (int q = 0; q < ZB; q += 2)
-                    rec[q / 2] = make_float4(cv.x * wx[q], cv.y * wx[q], cv.x * wx[q + 1],
-                                             cv.y * wx[q + 1]);
-                rec[4] = make_float4(wy[0], wy[1], wy[2], wy[3]);
-                rec[5] = make_float4(wy[4], wy[5], wy[6], wy[7]);
-                rec[6] = make_float4(wz[0], wz[1], wz[2], wz[3]);
-                rec[7] = make_float4(wz[4], wz[5], wz[6], wz[7]);
-                // quadrants (qx, qy) the footprint [ox, ox + W) x [oy, oy + W) meets
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int qx = q >> 1, qy = q & 1;
-                    const bool hit = ox < 4 * qx + 4 && ox + W > 4 * qx && oy < 4 * qy + 4 &&
-                                     oy + W > 4 * qy;
-                    touch |= hit ? (1 << q) : 0;
-                }
-            }
-            // per z-step and quadrant: the batch rows that touch it, in order
-            int cnt[ZCH][4];
-#pragma unroll
-            for (int t = 0; t < ZCH; ++t)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const bool mine = tsel == t && ((touch >> q) & 1);
-                    const uint64_t bq = __ballot(mine);
-                    cnt[t][q] = __popcll(bq);
-                    if (mine) lists[t][q][__popcll(bq & lt_mask)] = (uint8_t)lane;
-                }
-            __syncthreads();
-#pragma unroll
-            for (int t = 0; t < ZCH; ++t) {
-                const int nit = max(max(cnt[t][0], cnt[t][1]), max(cnt[t][2], cnt[t][3]));
-                if (nit == 0) continue;
-                const int ze = zc + t;
-                while (zw < ze) {
-                    if (zw >= z0)
-                        store_stage(stage, grid, lane, (zw - z0) % ZST, zw, n1, n2, bx, by,
-                                    wre[0], wim[0], zw == zend - 1);
-#pragma unroll
-                    for (int a = 0; a < W - 1; ++a) {
-                        wre[a] = wre[a + 1];
-                        wim[a] = wim[a + 1];
-                    }
-                    wre[W - 1] = wim[W - 1] = 0.f;
-                    ++zw;
-                }
-                const uint32_t *lw = reinterpret_cast<const uint32_t *>(lists[t][grp]);
-                for (int it = 0; it < nit; it += UNR) {
-                    const uint32_t pk = lw[it >> 2];
-                    float vr[UNR], vi[UNR], wzz[UNR][W];
-#pragma unroll
-                    for (int u = 0; u < UNR; ++u) {
-                        const float *rec = table + ((pk >> (8 * u)) & 0xffu) * REC;
-                        const float2 wxc = *reinterpret_cast<const float2 *>(rec + 2 * cxl);
-                        const float wyv = rec[16 + cyl];
-                        vr[u] = wxc.x * wyv;
-                        vi[u] = wxc.y * wyv;
-#pragma unroll
-                        for (int a = 0; a < W; ++a) wzz[u][a] = rec[24 + a];
-                    }
-#pragma unroll
-                    for (int u = 0; u < UNR; ++u)
-#pragma unroll
-                        for (int a = 0; a < W; ++a) {
-                            wre[a] = fmaf(vr[u], wzz[u][a], wre[a]);
-                            wim[a] = fmaf(vi[u], wzz[u][a], wim[a]);
-                        }
-                }
-            }
-        }
+        p1 = p2;
+        c1 = c2;
+        p2 = p3;
     }
     while (zw < zend) {  // drain the window up to the segment end
         if (zw >= z0)
