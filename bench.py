@@ -172,7 +172,7 @@ def main():
     alg_bytes = M * (8 + 8 * 3 + 4) + 8 * grid_cells
     achieved = alg_bytes / (spread_ms * 1e-3) / 1e9
     traffic = None
-    tf = ROOT / "profiles" / "spread_3d_t1_traffic.json"
+    tf = ROOT / "profiles" / "spread_zsweep_3d_t1_M2e7_N256_traffic.json"
     if tf.exists():
         try:
             traffic = json.loads(tf.read_text()).get("bytes_per_launch")
