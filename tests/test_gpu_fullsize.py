@@ -1,0 +1,135 @@
+"""GPU parity at the BASELINE.json configurations' full sizes.
+
+Gate (north star): rel_l2(GPU, exact direct sum) <= max(eps, 2 * ref_err) on
+the samples tests/fullsize_cases.py fixes, where ref_err is the CPU fp64
+oracle's own error on the same inputs and samples, computed once by
+tests/golden/make_fullsize_ref.py (minutes of CPU at these sizes) and
+committed in tests/golden/fullsize_ref.json. The direct sums on the samples
+are recomputed here by the oracle's C code.
+
+Size-independent properties are checked as well: batched == looped (the
+reference's 1e-5 gate), the type-1/type-2 adjoint identity, and the expi
+accuracy gate over 1e7 phases.
+"""
+
+import json
+import pathlib
+
+import numpy as np
+import pytest
+import torch
+
+import fullsize_cases as F
+
+pytestmark = pytest.mark.gpu
+
+REF = json.loads((pathlib.Path(__file__).resolve().parent / "golden" / "fullsize_ref.json")
+                 .read_text())
+
+
+def _sub(full, N, modes):
+    return np.asarray(full)[np.ix_(*[np.asarray(m) + n // 2 for m, n in zip(modes, N)])]
+
+
+def _gate(case, key=None):
+    r = REF[case]
+    ref = r["ref_err"] if key is None else r["ref_err"][key]
+    return max(r["eps"], 2.0 * ref)
+
+
+def test_cfg0_1d_t1_full(mn, oracle):
+    print("case full cfg0 1D t1 M=1e5 N=4096 eps=1e-6", flush=True)
+    k = F.cfg0_1d_t1()
+    f = mn.nufft1d1(k["x"][0], k["c"], k["N"], eps=k["eps"], isign=k["isign"])
+    fe = oracle.dft_t1(k["x"], k["c"], k["modes"], k["isign"])
+    err = oracle.rel_l2(f, fe)
+    print(f"  err={err:.3e} gate={_gate('cfg0_1d_t1'):.3e}")
+    assert err <= _gate("cfg0_1d_t1")
+
+
+def test_cfg1_2d_t1_batched_full(mn, oracle):
+    print("case full cfg1 2D t1 x8 M=1e7 N=1024^2 eps=1e-6", flush=True)
+    k = F.cfg1_2d_t1_batched()
+    dev = torch.device("cuda")
+    xd = tuple(torch.from_numpy(v).to(dev) for v in k["x"])
+    cs = torch.from_numpy(k["cs"]).to(dev)
+    plan = mn.Type1PlanND(xd, k["N"], eps=k["eps"], isign=k["isign"])
+    fb = plan.execute_batch(cs, return_np=False)
+    assert tuple(fb.shape) == (8, *k["N"])
+    for b in k["checked"]:
+        fe = oracle.dft_t1(k["x"], k["cs"][b], k["modes"], k["isign"])
+        err = oracle.rel_l2(_sub(fb[b].cpu().numpy(), k["N"], k["modes"]), fe)
+        gate = _gate("cfg1_2d_t1_batched", str(b))
+        print(f"  vector {b}: err={err:.3e} gate={gate:.3e}")
+        assert err <= gate
+    # batched == looped (ref gate harness/test_type1_batch.py:83)
+    fl = plan.execute(cs[3], return_np=False)
+    rel = float(torch.linalg.vector_norm(fb[3] - fl) / torch.linalg.vector_norm(fl))
+    print(f"  batched vs looped (vector 3): {rel:.3e}")
+    assert rel < 1e-5
+
+
+def test_cfg2_2d_t2_radial_full(mn, oracle):
+    print("case full cfg2 2D t2 radial 512x2048 N=1024^2 eps=1e-6", flush=True)
+    k = F.cfg2_2d_t2_radial()
+    c = mn.Type2PlanND(tuple(k["x"]), k["f"].shape, eps=k["eps"], isign=k["isign"]).execute(k["f"])
+    ce = oracle.dft_t2(k["x"], k["f"], k["isign"], k["points"])
+    err = oracle.rel_l2(c[k["points"]], ce)
+    print(f"  err={err:.3e} gate={_gate('cfg2_2d_t2_radial'):.3e}")
+    assert c.shape == (512 * 2048,)
+    assert err <= _gate("cfg2_2d_t2_radial")
+
+
+def test_cfg3_3d_t1_t2_full(mn, oracle):
+    """The north-star workload: type-1 on sampled modes against the direct
+    sum; the type-2 round trip of its output at 64 of the same points
+    against the direct type-2 sum of that output (gated by the type-1
+    oracle error at the same w, beta, n_up); and the adjoint identity
+    <T1 c, g> = <c, T2 g> at full size."""
+    print("case full cfg3 3D t1+t2 M=2e7 N=256^3 eps=1e-5", flush=True)
+    k = F.cfg3_3d_t1()
+    dev = torch.device("cuda")
+    xd = tuple(torch.from_numpy(v).to(dev) for v in k["x"])
+    cd = torch.from_numpy(k["c"]).to(dev)
+    fk = mn.Type1PlanND(xd, k["N"], eps=k["eps"], isign=k["isign"]).execute(cd, return_np=False)
+    fe = oracle.dft_t1(k["x"], k["c"], k["modes"], k["isign"])
+    err = oracle.rel_l2(_sub(fk.cpu().numpy(), k["N"], k["modes"]), fe)
+    gate = _gate("cfg3_3d_t1")
+    print(f"  t1 err={err:.3e} gate={gate:.3e}")
+    assert err <= gate
+
+    p2 = mn.Type2PlanND(xd, k["N"], eps=k["eps"], isign=-k["isign"])
+    c2 = p2.execute(fk, return_np=False)
+    fk_h = fk.cpu().numpy()
+    ce = oracle.dft_t2(k["x"], fk_h, -k["isign"], k["points"])
+    err2 = oracle.rel_l2(c2.cpu().numpy()[k["points"]], ce)
+    print(f"  t2 round-trip err={err2:.3e} gate={gate:.3e}")
+    assert err2 <= gate
+
+    # adjoint identity: T2 here has the negated sign of T1
+    rng = np.random.default_rng(5)
+    g = torch.from_numpy(F._cplx(rng, k["N"])).to(dev)
+    t2g = p2.execute(g, return_np=False)
+    lhs = torch.vdot(g.reshape(-1).to(torch.complex128), fk.reshape(-1).to(torch.complex128))
+    rhs = torch.vdot(t2g.to(torch.complex128), cd.to(torch.complex128))
+    scale = float(torch.linalg.vector_norm(fk.to(torch.complex128)) *
+                  torch.linalg.vector_norm(g.to(torch.complex128)))
+    adj = abs(complex(lhs - rhs)) / scale
+    print(f"  adjoint identity: {adj:.3e}")
+    assert adj <= k["eps"]
+
+
+def test_cfg4_3d_t3_and_expi_full(mn, oracle):
+    print("case full cfg4 3D t3 1e6 x 1e6 eps=1e-5 + expi 1e7", flush=True)
+    k = F.cfg4_3d_t3()
+    plan = mn.Type3Plan(tuple(k["x"]), tuple(k["s"]), eps=k["eps"], isign=k["isign"])
+    f = plan.execute(k["c"])
+    fe = oracle.dft_t3(k["x"], k["c"], k["s"], k["isign"], k["targets"])
+    err = oracle.rel_l2(np.asarray(f)[k["targets"]], fe)
+    print(f"  t3 err={err:.3e} gate={_gate('cfg4_3d_t3'):.3e}")
+    assert err <= _gate("cfg4_3d_t3")
+    phi = F.expi_phases()
+    e = mn.expi(phi, return_np=True)
+    worst = float(np.max(np.abs(e - np.exp(1j * phi))))
+    print(f"  expi max abs err over 1e7 phases in [-1e6, 1e6]: {worst:.3e}")
+    assert worst <= 5e-7
