@@ -158,6 +158,21 @@ int mn_spread_accumulate(const mn_bins *g, float beta, int64_t P, int64_t nsub,
                          mn_stream_t stream);
 
 /*
+ * mn_spread into a complex128 grid, with the strength times its prephase
+ * and every strength x weight product formed in fp64 and the tiles flushed
+ * with fp64 atomics (ES weights stay fp32): the type-3 source spread. Its
+ * grid is deconvolved by 1/phihat at the band edges and again by
+ * 1/phihat(theta) at the targets, which amplifies white rounding noise in
+ * the grid about 20x (fp32 tap products and flush add ~1e-5 relative error
+ * at 1e6 x 1e6 points, eps 1e-5); the fp32 weight error, a smooth function
+ * of the fraction, is not amplified. ref: gpu_t3.py:565-591.
+ */
+int mn_spread_c128(const mn_bins *g, float beta, int64_t P, int64_t nsub,
+                   const int32_t *sub_info, const uint32_t *perm,
+                   const int32_t *const i1s[3], const float *const frs[3], const void *c,
+                   const void *pre, void *grid, mn_stream_t stream);
+
+/*
  * Owner-computes 3D spread ("z-sweep"), the fast path for 3D type-1 grids
  * with n0, n1 multiples of 8 (>= 16), w <= 8 and n0*n1*n2/16 <= 2^26 keys.
  * Each wavefront owns an 8x8 (x, y) column block over a z-segment of zseg
@@ -338,6 +353,28 @@ int mn_fft_crop_deconv(int dim, const int64_t n_up[3], const int64_t N[3], int64
 int mn_pad_deconv_fft(int dim, const int64_t n_up[3], const int64_t N[3], int64_t batch,
                       int isign, const void *fk, const float *const dec[3], void *work,
                       int64_t work_bytes, void *grid, mn_stream_t stream);
+/*
+ * The same transform in double precision (complex128 data, rocFFT double).
+ * The type-3 pipeline runs its inner-grid FFT this way: its target
+ * deconvolution 1/phihat(theta) reaches ~1e2 at the band edges and
+ * amplifies an fp32 FFT's absolute roundoff there (cfg-5-like workloads:
+ * 7.5e-5 relative error in fp32 against 1.6e-5 in fp64).
+ * ref: gpu_t3.py:94-148 (the type-3 FFT stage).
+ */
+int mn_fft_exec_f64(int dim, const int64_t n[3], int64_t batch, int isign, void *data,
+                    mn_stream_t stream);
+
+/*
+ * pad/deconv in double precision: grid = pad(fk * dec0 x dec1 x dec2) with
+ * fk and grid complex128 and fp64 factors, ahead of mn_fft_exec_f64; and
+ * out = (complex64) in for n complex128 values, after it.
+ * ref: gpu_t3.py:630-651 (type-3 inner-grid pad + deconvolution).
+ */
+int mn_pad_deconv_c128(int dim, const int64_t n_up[3], const int64_t N[3], int64_t batch,
+                       const void *fk, const double *const dec[3], void *grid,
+                       mn_stream_t stream);
+int mn_round_c64(int64_t n, const void *in, void *out, mn_stream_t stream);
+
 /* Destroy all cached FFT plans (call with no transform in flight). */
 int mn_fft_cache_clear(void);
 

@@ -285,6 +285,14 @@ def spread(pts, beta, c, grid, pre=None, accumulate=False):
                L.ptr(pre), L.ptr(grid), L.stream()), "spread")
 
 
+def spread_c128(pts, beta, c, grid128, pre=None):
+    """grid128 (complex128) = spread(c) with fp64 products and accumulation."""
+    L.check(L.lib().mn_spread_c128(ctypes.byref(pts.bins), float(beta), pts.P, pts.nsub,
+                                   L.ptr(pts.info), L.ptr(pts.perm), L.ptr3(pts.i1_rows()),
+                                   L.ptr3(pts.fr_rows()), L.ptr(c), L.ptr(pre), L.ptr(grid128),
+                                   L.stream()), "spread_c128")
+
+
 def spread_batch(pts, beta, cs, grids):
     L.check(L.lib().mn_spread_batch(ctypes.byref(pts.bins), float(beta), pts.P, pts.nsub,
                                     L.ptr(pts.info), L.ptr(pts.perm), L.ptr3(pts.i1_rows()),
@@ -344,6 +352,24 @@ def pad_deconv_fft(n_up, N, fk, decs, grid, isign, work, batch=1):
                                       L.ptr(fk), L.ptr3(decs), L.ptr(work),
                                       0 if work is None else work.numel(), L.ptr(grid),
                                       L.stream()), "pad_deconv_fft")
+
+
+def pad_deconv_c128(n_up, N, fk128, decs64, grid128, batch=1):
+    """grid128 = pad(fk128 * prod_d dec_d), complex128 with fp64 factors."""
+    L.check(L.lib().mn_pad_deconv_c128(len(N), L.i64x3(n_up), L.i64x3(N), int(batch), L.ptr(fk128),
+                                       L.ptr3(decs64), L.ptr(grid128), L.stream()),
+            "pad_deconv_c128")
+
+
+def fft_f64(grid128, n_up, isign, batch=1):
+    """In-place complex128 FFT (rocFFT double precision)."""
+    L.check(L.lib().mn_fft_exec_f64(len(n_up), L.i64x3(n_up), int(batch), int(isign),
+                                    L.ptr(grid128), L.stream()), "fft_f64")
+
+
+def round_c64(src128, out64):
+    L.check(L.lib().mn_round_c64(src128.numel(), L.ptr(src128), L.ptr(out64), L.stream()),
+            "round_c64")
 
 
 def fft(grid, n_up, isign, batch=1):

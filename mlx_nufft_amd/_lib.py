@@ -67,6 +67,8 @@ _SIGS = [
                           c_vp, c_vp, c_vp, c_vp]),
     ("mn_spread_accumulate", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int64, c_vp, c_vp,
                                      VP3, VP3, c_vp, c_vp, c_vp, c_vp]),
+    ("mn_spread_c128", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int64, c_vp, c_vp, VP3,
+                               VP3, c_vp, c_vp, c_vp, c_vp]),
     ("mn_zsweep_nkeys", c_int64, [ctypes.POINTER(Bins)]),
     ("mn_zsweep_setpts", c_int, [ctypes.POINTER(Bins), c_int64, VP3, c_int, c_vp, VP3, c_vp]),
     ("mn_zsweep_starts", c_int, [ctypes.POINTER(Bins), c_int64, c_vp, c_vp, c_vp]),
@@ -89,6 +91,9 @@ _SIGS = [
     ("mn_expi", c_int, [c_int, ctypes.POINTER(c_vp), c_int64, c_int, c_vp, c_vp]),
     ("mn_fft_exec", c_int, [c_int, I64x3, c_int64, c_int, c_vp, c_vp]),
     ("mn_fft_cache_clear", c_int, []),
+    ("mn_fft_exec_f64", c_int, [c_int, I64x3, c_int64, c_int, c_vp, c_vp]),
+    ("mn_pad_deconv_c128", c_int, [c_int, I64x3, I64x3, c_int64, c_vp, VP3, c_vp, c_vp]),
+    ("mn_round_c64", c_int, [c_int64, c_vp, c_vp, c_vp]),
     ("mn_fftp_supported", c_int, [c_int, I64x3]),
     ("mn_fftp_work_bytes", c_int64, [c_int, I64x3, I64x3, c_int64]),
     ("mn_fft_crop_deconv", c_int, [c_int, I64x3, I64x3, c_int64, c_int, c_vp, VP3, c_vp, c_int64,

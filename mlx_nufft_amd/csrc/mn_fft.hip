@@ -1,5 +1,6 @@
-// Fine-grid FFT through rocFFT: in-place complex64 transforms with a plan
-// cache keyed by (device, dim, lengths, batch, direction). Each cached plan
+// Fine-grid FFT through rocFFT: in-place complex64 (or complex128) transforms
+// with a plan cache keyed by (device, dim, lengths, batch, direction,
+// precision). Each cached plan
 // owns its execution info and work buffer; execution is asynchronous on the
 // caller's stream. The cache is the only mutable library state, guarded by
 // a mutex.
@@ -20,9 +21,10 @@ struct FftKey {
     int dev, dim;
     int64_t n0, n1, n2, batch;
     int dir;
+    int f64;  // 1: complex128 (double precision)
     bool operator<(const FftKey &o) const {
-        return std::tie(dev, dim, n0, n1, n2, batch, dir) <
-               std::tie(o.dev, o.dim, o.n0, o.n1, o.n2, o.batch, o.dir);
+        return std::tie(dev, dim, n0, n1, n2, batch, dir, f64) <
+               std::tie(o.dev, o.dim, o.n0, o.n1, o.n2, o.batch, o.dir, o.f64);
     }
 };
 
@@ -61,7 +63,8 @@ int make_plan(const FftKey &k, FftPlan *out) {
     rocfft_status st = rocfft_plan_create(
         &p.plan, rocfft_placement_inplace,
         k.dir > 0 ? rocfft_transform_type_complex_inverse : rocfft_transform_type_complex_forward,
-        rocfft_precision_single, (size_t)k.dim, lengths, (size_t)k.batch, nullptr);
+        k.f64 ? rocfft_precision_double : rocfft_precision_single, (size_t)k.dim, lengths,
+        (size_t)k.batch, nullptr);
     if (st != rocfft_status_success) {
         set_error("rocfft_plan_create failed, status " + std::to_string((int)st));
         return MN_ERUNTIME;
@@ -100,13 +103,12 @@ int make_plan(const FftKey &k, FftPlan *out) {
 }  // namespace
 }  // namespace mn
 
-using namespace mn;
+namespace mn {
+namespace {
 
-extern "C" {
-
-int mn_fft_exec(int dim, const int64_t n[3], int64_t batch, int isign, void *data,
-                mn_stream_t stream) {
-    clear_error();
+// Look up (or create) the cached plan and execute it in place on the stream.
+int fft_exec(int dim, const int64_t n[3], int64_t batch, int isign, void *data, int f64,
+             mn_stream_t stream) {
     MN_REQUIRE(dim >= 1 && dim <= 3, "fft: dim must be 1, 2 or 3");
     MN_REQUIRE(batch >= 1, "fft: batch must be >= 1");
     MN_REQUIRE(data != nullptr, "fft: NULL data");
@@ -123,6 +125,7 @@ int mn_fft_exec(int dim, const int64_t n[3], int64_t batch, int isign, void *dat
     k.n2 = nn[2];
     k.batch = batch;
     k.dir = isign >= 0 ? 1 : -1;
+    k.f64 = f64 ? 1 : 0;
     std::lock_guard<std::mutex> lock(g_mu);
     if (!g_setup) {
         MN_FFT_CHECK(rocfft_setup());
@@ -140,6 +143,25 @@ int mn_fft_exec(int dim, const int64_t n[3], int64_t batch, int isign, void *dat
     void *buf[1] = {data};
     MN_FFT_CHECK(rocfft_execute(p.plan, buf, nullptr, p.info));
     return MN_OK;
+}
+
+}  // namespace
+}  // namespace mn
+
+using namespace mn;
+
+extern "C" {
+
+int mn_fft_exec(int dim, const int64_t n[3], int64_t batch, int isign, void *data,
+                mn_stream_t stream) {
+    clear_error();
+    return fft_exec(dim, n, batch, isign, data, 0, stream);
+}
+
+int mn_fft_exec_f64(int dim, const int64_t n[3], int64_t batch, int isign, void *data,
+                    mn_stream_t stream) {
+    clear_error();
+    return fft_exec(dim, n, batch, isign, data, 1, stream);
 }
 
 int mn_fft_cache_clear(void) {

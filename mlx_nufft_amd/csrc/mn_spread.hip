@@ -14,6 +14,8 @@
 // ref: nd.py:492-579 (OD spread), nd.py:683-742 (batched), gpu_t3.py:565-591.
 #include "mn_common.h"
 
+#include <type_traits>
+
 namespace mn {
 
 namespace {
@@ -28,7 +30,8 @@ struct SpreadArgs {
     CF3s frs;
     const float2 *c;    // strengths (caller order); batched: B x P
     const float2 *pre;  // optional sorted-order multiplier
-    float2 *grid;
+    void *grid;  // complex64, or complex128 when f64
+    bool f64;    // fp64 strength x weight products and a complex128 grid
     int64_t b0;  // first vector of this launch (batched)
     int bc;      // vectors in this launch
     hipStream_t s;
@@ -48,14 +51,19 @@ __device__ __forceinline__ int local_cell(int i1, int hw, int n, int b, int m) {
     return ((unsigned)loc < (unsigned)m) ? loc : -1;
 }
 
-template <int DIM, int W, bool BATCH>
+// F64: the strength times its prephase and every tap product are formed in
+// fp64 and the grid is complex128 (flushed with fp64 atomics), so the grid
+// carries no white fp32 rounding noise; the ES weights stay fp32 (their
+// error is a smooth function of the fraction).
+template <int DIM, int W, bool BATCH, bool F64>
 __global__ __launch_bounds__(256) void k_spread_tiled(Geom g, float bl2e, float inv_hw,
                                                       int64_t nsub, const int32_t *__restrict__ info,
                                                       const uint32_t *__restrict__ perm, CI3s i1s,
                                                       CF3s frs, const float2 *__restrict__ c,
                                                       const float2 *__restrict__ pre,
-                                                      float2 *__restrict__ grid, int64_t P,
+                                                      void *__restrict__ grid, int64_t P,
                                                       int64_t b0, int bc) {
+    using Real = typename std::conditional<F64, double, float>::type;
     extern __shared__ double lds[];
     const int p1 = g.p[1], p2 = g.p[2];
     const int T = g.p[0] * p1 * p2;
@@ -92,27 +100,32 @@ __global__ __launch_bounds__(256) void k_spread_tiled(Geom g, float bl2e, float 
         float2 pv = make_float2(1.0f, 0.0f);
         if (!BATCH && pre) pv = pre[j];
         for (int v = 0; v < nvec; ++v) {
-            float2 cv = BATCH ? c[(b0 + v) * P + src] : c[src];
-            if (!BATCH && pre)
-                cv = make_float2(cv.x * pv.x - cv.y * pv.y, cv.x * pv.y + cv.y * pv.x);
+            const float2 c0 = BATCH ? c[(b0 + v) * P + src] : c[src];
+            Real cvx = c0.x, cvy = c0.y;
+            if (!BATCH && pre) {
+                const Real px = pv.x, py = pv.y;
+                const Real rx = cvx * px - cvy * py;
+                cvy = cvx * py + cvy * px;
+                cvx = rx;
+            }
             double *tre = lds + (size_t)2 * T * v;
             double *tim = tre + T;
             if constexpr (DIM == 1) {
 #pragma unroll
                 for (int a0 = 0; a0 < W; ++a0) {
                     const int idx = loc[0] + a0;
-                    atomicAdd(&tre[idx], (double)(cv.x * wt[0][a0]));
-                    atomicAdd(&tim[idx], (double)(cv.y * wt[0][a0]));
+                    atomicAdd(&tre[idx], (double)(cvx * (Real)wt[0][a0]));
+                    atomicAdd(&tim[idx], (double)(cvy * (Real)wt[0][a0]));
                 }
             } else if constexpr (DIM == 2) {
 #pragma unroll
                 for (int a0 = 0; a0 < W; ++a0) {
-                    const float r = cv.x * wt[0][a0], i = cv.y * wt[0][a0];
+                    const Real r = cvx * (Real)wt[0][a0], i = cvy * (Real)wt[0][a0];
                     const int base = (loc[0] + a0) * p1 + loc[1];
 #pragma unroll
                     for (int a1 = 0; a1 < W; ++a1) {
-                        atomicAdd(&tre[base + a1], (double)(r * wt[1][a1]));
-                        atomicAdd(&tim[base + a1], (double)(i * wt[1][a1]));
+                        atomicAdd(&tre[base + a1], (double)(r * (Real)wt[1][a1]));
+                        atomicAdd(&tim[base + a1], (double)(i * (Real)wt[1][a1]));
                     }
                 }
             } else {
@@ -120,13 +133,13 @@ __global__ __launch_bounds__(256) void k_spread_tiled(Geom g, float bl2e, float 
                 for (int a0 = 0; a0 < W; ++a0) {
 #pragma unroll
                     for (int a1 = 0; a1 < W; ++a1) {
-                        const float w01 = wt[0][a0] * wt[1][a1];
-                        const float r = cv.x * w01, i = cv.y * w01;
+                        const Real w01 = (Real)wt[0][a0] * (Real)wt[1][a1];
+                        const Real r = cvx * w01, i = cvy * w01;
                         const int base = ((loc[0] + a0) * p1 + loc[1] + a1) * p2 + loc[2];
 #pragma unroll
                         for (int a2 = 0; a2 < W; ++a2) {
-                            atomicAdd(&tre[base + a2], (double)(r * wt[2][a2]));
-                            atomicAdd(&tim[base + a2], (double)(i * wt[2][a2]));
+                            atomicAdd(&tre[base + a2], (double)(r * (Real)wt[2][a2]));
+                            atomicAdd(&tim[base + a2], (double)(i * (Real)wt[2][a2]));
                         }
                     }
                 }
@@ -148,11 +161,20 @@ __global__ __launch_bounds__(256) void k_spread_tiled(Geom g, float bl2e, float 
         const int64_t cell = ((int64_t)g0 * g.n[1] + g1) * g.n[2] + g2;
         for (int v = 0; v < nvec; ++v) {
             const double *tre = lds + (size_t)2 * T * v;
-            const float re = (float)tre[q], im = (float)tre[T + q];
-            if (re == 0.0f && im == 0.0f) continue;
-            float *dst = reinterpret_cast<float *>(grid + (BATCH ? (b0 + v) * gsz : 0) + cell);
-            unsafeAtomicAdd(dst, re);
-            unsafeAtomicAdd(dst + 1, im);
+            if constexpr (F64) {
+                const double re = tre[q], im = tre[T + q];
+                if (re == 0.0 && im == 0.0) continue;
+                double *dst = reinterpret_cast<double *>(grid) + 2 * cell;
+                unsafeAtomicAdd(dst, re);
+                unsafeAtomicAdd(dst + 1, im);
+            } else {
+                const float re = (float)tre[q], im = (float)tre[T + q];
+                if (re == 0.0f && im == 0.0f) continue;
+                float *dst = reinterpret_cast<float *>(
+                    reinterpret_cast<float2 *>(grid) + (BATCH ? (b0 + v) * gsz : 0) + cell);
+                unsafeAtomicAdd(dst, re);
+                unsafeAtomicAdd(dst + 1, im);
+            }
         }
     }
 }
@@ -171,7 +193,9 @@ struct SpreadLaunch {
             return MN_EINVAL;
         }
         if (a.nsub == 0) return MN_OK;
-        auto kern = batch ? k_spread_tiled<DIM, W, true> : k_spread_tiled<DIM, W, false>;
+        auto kern = batch   ? k_spread_tiled<DIM, W, true, false>
+                    : a.f64 ? k_spread_tiled<DIM, W, false, true>
+                            : k_spread_tiled<DIM, W, false, false>;
         if (lds > 65536)
             MN_HIP_CHECK(hipFuncSetAttribute((const void *)kern,
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
@@ -192,7 +216,7 @@ using namespace mn;
 static int spread_impl(const mn_bins *g, float beta, int64_t P, int64_t nsub,
                        const int32_t *sub_info, const uint32_t *perm,
                        const int32_t *const i1s[3], const float *const frs[3], const void *c,
-                       const void *pre, void *grid, bool zero, mn_stream_t stream) {
+                       const void *pre, void *grid, bool zero, bool f64, mn_stream_t stream) {
     clear_error();
     int rc = check_bins(g);
     if (rc) return rc;
@@ -210,12 +234,13 @@ static int spread_impl(const mn_bins *g, float beta, int64_t P, int64_t nsub,
     a.perm = perm;
     a.c = static_cast<const float2 *>(c);
     a.pre = static_cast<const float2 *>(pre);
-    a.grid = static_cast<float2 *>(grid);
+    a.grid = grid;
+    a.f64 = f64;
     a.b0 = 0;
     a.bc = 1;
     a.s = as_stream(stream);
     if (zero) {
-        rc = fill_zero(grid, gsz * 8, a.s);
+        rc = fill_zero(grid, gsz * (f64 ? 16 : 8), a.s);
         if (rc) return rc;
     }
     return select_dim_w<SpreadLaunch>(g->dim, g->w, a);
@@ -226,14 +251,24 @@ extern "C" {
 int mn_spread(const mn_bins *g, float beta, int64_t P, int64_t nsub, const int32_t *sub_info,
               const uint32_t *perm, const int32_t *const i1s[3], const float *const frs[3],
               const void *c, const void *pre, void *grid, mn_stream_t stream) {
-    return spread_impl(g, beta, P, nsub, sub_info, perm, i1s, frs, c, pre, grid, true, stream);
+    return spread_impl(g, beta, P, nsub, sub_info, perm, i1s, frs, c, pre, grid, true, false,
+                       stream);
+}
+
+int mn_spread_c128(const mn_bins *g, float beta, int64_t P, int64_t nsub,
+                   const int32_t *sub_info, const uint32_t *perm, const int32_t *const i1s[3],
+                   const float *const frs[3], const void *c, const void *pre, void *grid,
+                   mn_stream_t stream) {
+    return spread_impl(g, beta, P, nsub, sub_info, perm, i1s, frs, c, pre, grid, true, true,
+                       stream);
 }
 
 int mn_spread_accumulate(const mn_bins *g, float beta, int64_t P, int64_t nsub,
                          const int32_t *sub_info, const uint32_t *perm,
                          const int32_t *const i1s[3], const float *const frs[3], const void *c,
                          const void *pre, void *grid, mn_stream_t stream) {
-    return spread_impl(g, beta, P, nsub, sub_info, perm, i1s, frs, c, pre, grid, false, stream);
+    return spread_impl(g, beta, P, nsub, sub_info, perm, i1s, frs, c, pre, grid, false, false,
+                       stream);
 }
 
 int mn_spread_batch(const mn_bins *g, float beta, int64_t P, int64_t nsub,
@@ -258,7 +293,8 @@ int mn_spread_batch(const mn_bins *g, float beta, int64_t P, int64_t nsub,
     a.perm = perm;
     a.c = static_cast<const float2 *>(cs);
     a.pre = nullptr;
-    a.grid = static_cast<float2 *>(grids);
+    a.grid = grids;
+    a.f64 = false;
     a.s = as_stream(stream);
     rc = fill_zero(grids, B * gsz * 8, a.s);
     if (rc) return rc;

@@ -33,6 +33,8 @@ def _sub(full, N, modes):
 
 def _gate(case, key=None):
     r = REF[case]
+    if "ref_err_fp64" in r:  # type 3: the all-fp64 restatement's error (stricter)
+        return max(r["eps"], 2.0 * r["ref_err_fp64"])
     ref = r["ref_err"] if key is None else r["ref_err"][key]
     return max(r["eps"], 2.0 * ref)
 

@@ -124,15 +124,14 @@ def test_type3_vs_direct(isign, eps, oracle, mn):
     f = mn.Type3Plan(tuple(x), tuple(s), eps=eps, isign=isign).execute(c)
     idx = np.arange(0, M, 7)
     fe = oracle.dft_t3(x, c, s, isign, idx)
-    # The reference's type-3 pipeline spreads in fp32; at sigma=1.25 that
-    # stage's rounding, amplified by the deconvolution, sets its error floor
-    # (ref: harness/diagnose_ref.py). Its own error is therefore at least the
-    # restatement's error with the fp32 spread stage.
-    err64 = oracle.rel_l2(oracle.nufft_t3(x, c, s, eps, isign)[idx], fe)
+    # ref_err is the all-fp64 restatement's error. (The reference's own
+    # pipeline spreads in fp32, which at sigma = 1.25 raises its error to
+    # the spread64=False figure printed alongside; this engine's type-3 path
+    # keeps the inner grid in fp64 and is held to the stricter fp64 bound.)
+    ref_err = oracle.rel_l2(oracle.nufft_t3(x, c, s, eps, isign)[idx], fe)
     err32 = oracle.rel_l2(oracle.nufft_t3(x, c, s, eps, isign, spread64=False)[idx], fe)
-    ref_err = max(err64, err32)
     err = oracle.rel_l2(f[idx], fe)
-    print(f"  err={err:.3e} ref_err={ref_err:.3e}")
+    print(f"  err={err:.3e} ref_err(fp64)={ref_err:.3e} (fp32-spread restatement {err32:.3e})")
     assert err <= max(eps, 2 * ref_err)
 
 
