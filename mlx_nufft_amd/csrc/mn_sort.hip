@@ -16,8 +16,11 @@ namespace mn {
 namespace {
 
 constexpr int RS_THREADS = 256;
-constexpr int RS_ITEMS = 16;
-constexpr int RS_TILE = RS_THREADS * RS_ITEMS;  // 4096 elements per tile
+// 8192-element tiles: twice the digit-run length of 4096-element ones, so
+// fewer partial cache lines at the run ends (measured 9 % faster per set of
+// passes at 2e7 keys; 12288 spills registers)
+constexpr int RS_ITEMS = 32;
+constexpr int RS_TILE = RS_THREADS * RS_ITEMS;  // 8192 elements per tile
 constexpr int RS_RADIX = 256;
 
 constexpr int SC_THREADS = 256;
@@ -124,11 +127,11 @@ struct SortCols {
     uint32_t *out[MN_SORT_MAX_COLS];
 };
 
-// Stable scatter of one 4096-element tile: the key, its value (the caller
+// Stable scatter of one 8192-element tile: the key, its value (the caller
 // index; implicit on the first pass) and up to MN_SORT_MAX_COLS payload
 // columns.
-//  1. Rank: wave w owns the tile's elements [1024w, 1024w + 1024) and visits
-//     them in 16 rounds of 64 consecutive elements; lanes with equal digits
+//  1. Rank: wave w owns the tile's elements [2048w, 2048w + 2048) and visits
+//     them in 32 rounds of 64 consecutive elements; lanes with equal digits
 //     find each other with a ballot match and a wave-private LDS counter per
 //     digit gives the count of the wave's earlier elements with that digit.
 //     No barrier is needed inside a wave (its LDS accesses stay in order).
