@@ -2,8 +2,9 @@
 // written exactly once with a plain store.
 //
 // Layout. The grid is cut into 8x8 (x, y) column blocks. Each wavefront owns
-// one block over a z-segment; lane (lx, ly) owns column (8 bx + lx, 8 by + ly)
-// and keeps a W-cell complex window [z, z + W) of its column in VGPRs. The
+// one block over a z-segment; each lane owns one column of the block (lanes
+// grouped by 4x4 quadrant, below) and keeps a W-cell complex window
+// [z, z + W) of its column in VGPRs. The
 // wave sweeps z upwards: at each z it adds every point whose first tap is at
 // z and whose footprint touches the block, then cell z is complete and is
 // stored (staged in LDS so stores run along z), and the window shifts by one
@@ -25,6 +26,9 @@
 // W z-weights. Per z-step and 4x4 column quadrant, a list holds the byte
 // offsets of the rows of the points that touch the quadrant; the 16 lanes
 // of the quadrant walk it, each point costing 2 MULs and 2*W FMAs per lane.
+// Loads are pipelined two batches deep: while batch k is built and swept,
+// the strengths of batch k+1 and the words / fractions / perm of batch k+2
+// are in flight.
 //
 // ref: nd.py:492-579 (the reference's output-driven spread this replaces),
 // nd.py:298-372 (its bin sort and subproblem tables).
