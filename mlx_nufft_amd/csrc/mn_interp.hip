@@ -62,22 +62,48 @@ __global__ __launch_bounds__(256) void k_interp_tiled(Geom g, float bl2e, float 
     const int o2 = DIM >= 3 ? b[2] * g.m[2] - W / 2 : 0;
     {
         // Tile cell q = (q0*p1 + q1)*p2 + q2, walked with a stride of nt as a
-        // mixed-radix counter (no division per cell).
+        // mixed-radix counter (no division per cell). Loads go out in batches
+        // of LB cells per thread before any LDS write, so their latencies
+        // overlap; bins whose padded tile lies inside the grid (uniform per
+        // workgroup) skip the periodic wrap.
+        constexpr int LB = 8;
         const int nt = blockDim.x;
         const int s2 = nt % p2, s12 = nt / p2, s1 = s12 % p1, s0 = s12 / p1;
         int q2 = threadIdx.x % p2, q1 = (threadIdx.x / p2) % p1, q0 = threadIdx.x / (p2 * p1);
-        for (int q = threadIdx.x; q < T; q += nt) {
-            const int g0 = wrap_tile_i(o0 + q0, g.n[0]);
-            const int g1 = DIM >= 2 ? wrap_tile_i(o1 + q1, g.n[1]) : 0;
-            const int g2 = DIM >= 3 ? wrap_tile_i(o2 + q2, g.n[2]) : 0;
-            tile[q] = grid[((int64_t)g0 * g.n[1] + g1) * g.n[2] + g2];
-            q2 += s2;
-            int c = q2 >= p2;
-            q2 -= c ? p2 : 0;
-            q1 += s1 + c;
-            c = q1 >= p1;
-            q1 -= c ? p1 : 0;
-            q0 += s0 + c;
+        const bool inside = o0 >= 0 && o0 + g.p[0] <= g.n[0] && o1 >= 0 && o1 + p1 <= g.n[1] &&
+                            o2 >= 0 && o2 + p2 <= g.n[2];
+        const int64_t n12 = (int64_t)g.n[1] * g.n[2];
+        for (int qb = threadIdx.x; qb < T; qb += nt * LB) {
+            float2 v[LB];
+#pragma unroll
+            for (int b = 0; b < LB; ++b) {
+                const int q = qb + b * nt;
+                v[b] = make_float2(0.f, 0.f);
+                if (q < T) {
+                    int64_t idx;
+                    if (inside) {
+                        idx = (int64_t)(o0 + q0) * n12 + (int64_t)(o1 + q1) * g.n[2] + (o2 + q2);
+                    } else {
+                        const int g0 = wrap_tile_i(o0 + q0, g.n[0]);
+                        const int g1 = DIM >= 2 ? wrap_tile_i(o1 + q1, g.n[1]) : 0;
+                        const int g2 = DIM >= 3 ? wrap_tile_i(o2 + q2, g.n[2]) : 0;
+                        idx = ((int64_t)g0 * g.n[1] + g1) * g.n[2] + g2;
+                    }
+                    v[b] = grid[idx];
+                }
+                q2 += s2;
+                int c = q2 >= p2;
+                q2 -= c ? p2 : 0;
+                q1 += s1 + c;
+                c = q1 >= p1;
+                q1 -= c ? p1 : 0;
+                q0 += s0 + c;
+            }
+#pragma unroll
+            for (int b = 0; b < LB; ++b) {
+                const int q = qb + b * nt;
+                if (q < T) tile[q] = v[b];
+            }
         }
     }
     __syncthreads();
