@@ -207,6 +207,37 @@ int mn_spread_zsweep(const mn_bins *g, float beta, int64_t P, int zseg, const in
                      mn_stream_t stream);
 
 /*
+ * Owner-computes 2D spread ("y-sweep"), the fast path for 2D type-1 grids
+ * with n0 a multiple of 64 (>= 128), w <= 8 and (n0/64)*n1*2 <= 2^26 keys.
+ * Each wavefront owns 64 consecutive x-columns over a y-segment of yseg
+ * cells, walks y with a w-cell window per column in registers and stores
+ * every grid cell once (no atomics; the grids are fully overwritten).
+ * B strength vectors (c: B x P, caller order; grid: B x n0 x n1) run as
+ * independent rows of one launch. g: dim 2, w, n (m and nb are not used).
+ *
+ * Point word (one uint32 per point, from mn_ysweep_setpts):
+ *   bits 0-25  key = (bx*n1 + y)*2 + reach, where bx is the 64-column block
+ *              of the first tap, y its cell, and reach whether the
+ *              footprint crosses into the next block;
+ *   bits 26-31 x cell of the first tap within its block.
+ * mn_ysweep_setpts computes the words and fr exactly as mn_setpts_t12 does
+ * the cells; sort them with mn_sort_pairs (key_bits = bits of
+ * mn_ysweep_nkeys() - 1, fr as payload) and build ystart
+ * (mn_ysweep_nkeys() + 1 int32) with mn_ysweep_starts. Strengths are
+ * c[perm[j]], or c[j] when perm is NULL.
+ * ref: nd.py:152-165 (cells), nd.py:492-579 and nd.py:683-742 (output-driven
+ * and batched spread), nd.py:298-372 (bin sort).
+ */
+int64_t mn_ysweep_nkeys(const mn_bins *g);
+int mn_ysweep_setpts(const mn_bins *g, int64_t P, const double *const x[2], int prec64,
+                     uint32_t *word, float *const fr[2], mn_stream_t stream);
+int mn_ysweep_starts(const mn_bins *g, int64_t P, const uint32_t *sorted_word, int32_t *ystart,
+                     mn_stream_t stream);
+int mn_spread_ysweep(const mn_bins *g, float beta, int64_t P, int64_t B, int yseg,
+                     const int32_t *ystart, const uint32_t *perm, const uint32_t *sorted_word,
+                     const float *const frs[2], const void *c, void *grid, mn_stream_t stream);
+
+/*
  * out[j] = in[perm[j]] for P complex64 values (a strength vector into
  * sorted order). ref: nd.py:603 (mx.take of c by perm, GM spread).
  */

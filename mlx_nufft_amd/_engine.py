@@ -262,6 +262,85 @@ class ZSweepPoints:
         return _rows(self.frs, 3)
 
 
+def ysweep_eligible(dim, w, n_up):
+    """True when the owner-computes y-sweep spread applies: 2D, w <= 8, the x
+    fine-grid size a multiple of 64 (>= 128) and at most 2^26 sort keys
+    ((n0/64)*n1*2). MN_SPREAD=tiles forces the LDS-tile spread instead."""
+    if os.environ.get("MN_SPREAD", "") == "tiles":
+        return False
+    return (dim == 2 and 2 <= w <= 8 and n_up[0] % 64 == 0 and n_up[0] >= 128
+            and n_up[1] >= w and (n_up[0] // 64) * n_up[1] * 2 <= 1 << 26)
+
+
+class YSweepPoints:
+    """Point state for the 2D y-sweep spread: packed point words and
+    fractions, stably sorted together by the y-sweep key, and the key start
+    table. Buffers of the previous point set of the same plan (prev, same P
+    and geometry) are reused, as in ZSweepPoints."""
+
+    kind = "ysweep"
+
+    def __init__(self, bins, x64, prec64, prev=None):
+        lib = L.lib()
+        dev = x64[0].device
+        self.bins = bins
+        self.P = P = x64[0].numel()
+        self.K = K = int(lib.mn_ysweep_nkeys(ctypes.byref(bins)))
+        same = (prev is not None and prev.P == P and prev.K == K and prev.dev == dev)
+        self.dev = dev
+        self._bufs = bufs = prev._bufs if same else {}
+
+        def buf(name, shape, dtype):
+            if name not in bufs:
+                bufs[name] = torch.empty(shape, dtype=dtype, device=dev)
+            return bufs[name]
+
+        V2 = ctypes.c_void_p * 2
+        word = buf("word_in", P, torch.int32)
+        fr = buf("fr_in", (2, P), torch.float32)
+        L.check(lib.mn_ysweep_setpts(ctypes.byref(bins), P, V2(x64[0].data_ptr(), x64[1].data_ptr()),
+                                     int(bool(prec64)), L.ptr(word),
+                                     V2(fr[0].data_ptr(), fr[1].data_ptr()), L.stream()),
+                "ysweep setpts")
+        self.frs = buf("frs", (2, P), torch.float32)
+        ws_bytes = int(lib.mn_sort_pairs_workspace_bytes(P, 2))
+        self.word, self.perm, _ = sort_pairs(
+            word, max(1, (K - 1).bit_length()), _rows(fr, 2), _rows(self.frs, 2),
+            skey=buf("word", P, torch.int32), perm=buf("perm", P, torch.int32),
+            ws=buf("ws", ws_bytes, torch.uint8))
+        self.ystart = buf("ystart", K + 1, torch.int32)
+        L.check(lib.mn_ysweep_starts(ctypes.byref(bins), P, L.ptr(self.word), L.ptr(self.ystart),
+                                     L.stream()), "ysweep starts")
+
+    def fr_rows(self):
+        return _rows(self.frs, 2)
+
+
+def ysweep_segment(n_up, B):
+    """y-segment per wavefront: the longest power of two (<= 256) that still
+    gives at least 8192 wavefronts over the B vectors, but at least 32 (each
+    segment re-reads the w - 1 rows below it to warm its window). Measured
+    at 2048^2, 1e7 points, w = 7: 64 for B = 8 (3.58 ms; 3.70 at 32), 32 for
+    B = 1 (0.49 ms; 0.58 at 16, 0.84 at 64)."""
+    nbx = n_up[0] // 64
+    yseg = 256
+    while yseg > 32 and nbx * (-(-n_up[1] // yseg)) * B < 8192:
+        yseg //= 2
+    return yseg
+
+
+def spread_ysweep(pts, beta, cs, grids):
+    """grids[b] = spread(cs[b]) for B vectors (cs: (B, P) or (P,), caller
+    order) with the 2D y-sweep; grids are fully overwritten."""
+    B = 1 if cs.dim() == 1 else int(cs.shape[0])
+    n_up = [int(pts.bins.n[0]), int(pts.bins.n[1])]
+    V2 = ctypes.c_void_p * 2
+    L.check(L.lib().mn_spread_ysweep(ctypes.byref(pts.bins), float(beta), pts.P, B,
+                                     ysweep_segment(n_up, B), L.ptr(pts.ystart), L.ptr(pts.perm),
+                                     L.ptr(pts.word), V2(pts.frs[0].data_ptr(), pts.frs[1].data_ptr()),
+                                     L.ptr(cs), L.ptr(grids), L.stream()), "spread_ysweep")
+
+
 def permute_c64(perm, c, out):
     """out[j] = c[perm[j]] (complex64 strengths into sorted order)."""
     L.check(L.lib().mn_permute_c64(perm.numel(), L.ptr(perm), L.ptr(c), L.ptr(out), L.stream()),

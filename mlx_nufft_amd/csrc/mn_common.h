@@ -180,6 +180,28 @@ __device__ __forceinline__ uint32_t zs_word(int x, int y, int z, int n1, int n2,
 int zsweep_check(const mn_bins *g);
 int64_t zsweep_nkeys(const mn_bins *g);
 
+// ---- y-sweep point word (2D) ---------------------------------------------
+// The 2D owner-computes spread sorts one 32-bit word per point:
+//   bits  0-25  key = (bx*n1 + y)*2 + reach (sorted on)
+//   bits 26-31  x cell of the first tap within its 64-column block
+// where bx is the 64-column block of the first tap x, y its cell, and reach
+// says whether the footprint crosses into the next block.
+constexpr int kYsBlock = 64;
+constexpr int kYsKeyBits = 26;
+constexpr uint32_t kYsKeyMask = (1u << kYsKeyBits) - 1u;
+
+__device__ __forceinline__ uint32_t ys_word(int x, int y, int n1, int w) {
+    const int lx = x & (kYsBlock - 1);
+    const uint32_t reach = (lx + w - 1 >= kYsBlock) ? 1u : 0u;
+    const uint32_t key = ((uint32_t)(x / kYsBlock) * (uint32_t)n1 + (uint32_t)y) * 2u + reach;
+    return key | ((uint32_t)lx << kYsKeyBits);
+}
+
+// Validate a y-sweep geometry (2D, 2 <= w <= 8, n0 a multiple of 64 and
+// >= 128, key space within kYsKeyBits); number of keys K = (n0/64)*n1*2.
+int ysweep_check(const mn_bins *g);
+int64_t ysweep_nkeys(const mn_bins *g);
+
 // Validate the point/subproblem arguments shared by spread and interp.
 int check_points(const mn_bins *g, int64_t P, int64_t nsub, const int32_t *info,
                  const uint32_t *perm, const int32_t *const i1s[3], const float *const frs[3],

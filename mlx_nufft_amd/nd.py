@@ -76,6 +76,9 @@ class _PointsND:
         self._zsweep = self._use_zsweep and E.zsweep_eligible(self.dim, self.w, self.n_up)
         if self._zsweep:
             self._zbins = E.make_bins(3, self.w, self.n_up, m=(8, 8, 1))
+        self._ysweep = self._use_zsweep and E.ysweep_eligible(self.dim, self.w, self.n_up)
+        if self._ysweep:
+            self._ybins = E.make_bins(2, self.w, self.n_up, m=(64, 1))
         self._set_points(x64)
 
         # Mode deconvolution 1/phihat(2 pi k / n_up) on the uncentred fine grid
@@ -123,6 +126,12 @@ class _PointsND:
                 prev = getattr(self, "pts", None)
                 self.pts = E.ZSweepPoints(self._zbins, x64, self.prec == "crit64",
                                           prev=prev if isinstance(prev, E.ZSweepPoints) else None)
+                del prev
+        elif self._ysweep:
+            with tm("setpts+sort+tables"):
+                prev = getattr(self, "pts", None)
+                self.pts = E.YSweepPoints(self._ybins, x64, self.prec == "crit64",
+                                          prev=prev if isinstance(prev, E.YSweepPoints) else None)
                 del prev
         else:
             with tm("setpts"):
@@ -218,6 +227,9 @@ class Type1PlanND(_PointsND):
         if self.pts.kind == "zsweep":
             with tm("spread"):
                 E.spread_zsweep(self.pts, self.beta, cd, grid)
+        elif self.pts.kind == "ysweep":
+            with tm("spread"):
+                E.spread_ysweep(self.pts, self.beta, cd, grid)
         else:
             with tm("zero"):
                 E.fill_zero(grid)
@@ -258,6 +270,8 @@ class Type1PlanND(_PointsND):
             if self.pts.kind == "zsweep":
                 for b in range(B):
                     E.spread_zsweep(self.pts, self.beta, cd[b], grids[b])
+            elif self.pts.kind == "ysweep":
+                E.spread_ysweep(self.pts, self.beta, cd, grids)
             else:
                 E.spread_batch(self.pts, self.beta, cd, grids)
         self._fft_crop(grids, fk, tm, B)
@@ -279,7 +293,7 @@ class Type1PlanND(_PointsND):
         if P < 1 or not all(v.numel() == P for v in x64):
             raise ValueError("coordinate arrays must be non-empty, equal length")
         self.P = P
-        if not (isinstance(self.pts, E.ZSweepPoints) and self.pts.P == P):
+        if not (isinstance(self.pts, (E.ZSweepPoints, E.YSweepPoints)) and self.pts.P == P):
             self.pts = None  # nothing to reuse: free the old point state first
         self._set_points(x64)
         return self
