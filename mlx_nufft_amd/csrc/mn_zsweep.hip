@@ -32,6 +32,9 @@
 //
 // ref: nd.py:492-579 (the reference's output-driven spread this replaces),
 // nd.py:298-372 (its bin sort and subproblem tables).
+#include <cstdlib>
+#include <cstring>
+
 #include "mn_common.h"
 
 namespace mn {
@@ -106,14 +109,15 @@ struct ZCursor {
     int zc, bat, tot;
 };
 
-// The ranges themselves, in LDS (the wave reads them back with broadcast
-// loads): element e of range q, with pf[q] <= e < pf[q + 1], is sorted
-// point e + dj[q]; pf is the running sum of the range sizes.
+// The ranges of a group of ZC z-steps, in LDS (the wave reads them back
+// with broadcast loads): element e of range q, with pf[q] <= e < pf[q + 1],
+// is sorted point e + dj[q]; pf is the running sum of the range sizes.
+template <int ZC>
 struct __align__(16) ZRanges {
-    int pf[ZCH * NR];
-    int dj[ZCH * NR];
+    static_assert(ZC >= 1 && ZC <= 8, "at most 32 ranges");
+    int pf[ZC * NR];
+    int dj[ZC * NR];
 };
-static_assert(ZCH * NR == 8, "ranges are read as two int4");
 
 // The four source blocks of a block (itself, -x, -y, -xy) and the segment end.
 struct ZBlocks {
@@ -121,15 +125,16 @@ struct ZBlocks {
     int n2, zend;
 };
 
-// Load the ranges of the pair starting at zc: lane i < 8 takes range
+// Load the ranges of the group starting at zc: lane i < ZC * NR takes range
 // q = i (z-step i / NR, source i % NR), then a shuffle scan forms pf.
+template <int ZC>
 __device__ __forceinline__ void zc_load(ZCursor &k, int zc, const ZBlocks b,
-                                        const int32_t *__restrict__ zstart, ZRanges &rg,
+                                        const int32_t *__restrict__ zstart, ZRanges<ZC> &rg,
                                         int lane) {
     k.zc = zc;
     k.bat = 0;
     int st = 0, cnt = 0;
-    if (lane < ZCH * NR) {
+    if (lane < ZC * NR) {
         const int r = lane % NR, z = zc + lane / NR;
         if (z < b.zend) {
             const int zz = z < 0 ? z + b.n2 : z;
@@ -144,22 +149,23 @@ __device__ __forceinline__ void zc_load(ZCursor &k, int zc, const ZBlocks b,
     }
     int incl = cnt;
 #pragma unroll
-    for (int d = 1; d < ZCH * NR; d <<= 1) {
+    for (int d = 1; d < ZC * NR; d <<= 1) {
         const int v = __shfl_up(incl, d, 64);
         incl += (lane >= d) ? v : 0;
     }
-    if (lane < ZCH * NR) {
+    if (lane < ZC * NR) {
         rg.pf[lane] = incl - cnt;
         rg.dj[lane] = st - (incl - cnt);
     }
-    k.tot = __shfl(incl, ZCH * NR - 1, 64);
+    k.tot = __shfl(incl, ZC * NR - 1, 64);
 }
 
-// Advance past exhausted (or empty) pairs; stops at the segment end.
+// Advance past exhausted (or empty) groups; stops at the segment end.
+template <int ZC>
 __device__ __forceinline__ void zc_settle(ZCursor &k, const ZBlocks b,
-                                          const int32_t *__restrict__ zstart, ZRanges &rg,
+                                          const int32_t *__restrict__ zstart, ZRanges<ZC> &rg,
                                           int lane) {
-    while (k.bat >= k.tot && k.zc < b.zend) zc_load(k, k.zc + ZCH, b, zstart, rg, lane);
+    while (k.bat >= k.tot && k.zc < b.zend) zc_load<ZC>(k, k.zc + ZC, b, zstart, rg, lane);
 }
 
 // One lane's point of a batch, its loads issued (the strength, which needs
@@ -167,14 +173,15 @@ __device__ __forceinline__ void zc_settle(ZCursor &k, const ZBlocks b,
 struct ZPoint {
     int zc, nb;          // the batch's pair and size (uniform; nb = 0: done)
     bool valid;
-    int tsel, r;         // z-step within the pair and source range
+    int tsel, r;         // z-step within the group and source range
     uint32_t wd, src;    // sorted word; index of the strength in c
     float fx, fy, fz;
     float2 pv;           // prephase (1 if none)
 };
 
+template <int ZC>
 __device__ __forceinline__ ZPoint zp_issue(ZCursor &k, const ZBlocks b, int lane,
-                                           const int32_t *__restrict__ zstart, ZRanges &rg,
+                                           const int32_t *__restrict__ zstart, ZRanges<ZC> &rg,
                                            const uint32_t *__restrict__ perm,
                                            const uint32_t *__restrict__ word, const CF3s &frs,
                                            const float2 *__restrict__ pre) {
@@ -191,16 +198,18 @@ __device__ __forceinline__ ZPoint zp_issue(ZCursor &k, const ZBlocks b, int lane
     if (q.valid) {
         // the element's range: the last q with pf[q] <= e (empty ranges
         // repeat pf and are passed over)
-        const int4 pa = *reinterpret_cast<const int4 *>(rg.pf);
-        const int4 pb = *reinterpret_cast<const int4 *>(rg.pf + 4);
-        const int4 da = *reinterpret_cast<const int4 *>(rg.dj);
-        const int4 db = *reinterpret_cast<const int4 *>(rg.dj + 4);
-        const int pf[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
-        const int djs[8] = {da.x, da.y, da.z, da.w, db.x, db.y, db.z, db.w};
+        int pf[ZC * NR], djs[ZC * NR];
+#pragma unroll
+        for (int s = 0; s < ZC * NR; s += 4) {
+            const int4 pa = *reinterpret_cast<const int4 *>(rg.pf + s);
+            const int4 da = *reinterpret_cast<const int4 *>(rg.dj + s);
+            pf[s] = pa.x, pf[s + 1] = pa.y, pf[s + 2] = pa.z, pf[s + 3] = pa.w;
+            djs[s] = da.x, djs[s + 1] = da.y, djs[s + 2] = da.z, djs[s + 3] = da.w;
+        }
         const int e = k.bat + lane;
         int i = 0, dj = djs[0];
 #pragma unroll
-        for (int s = 1; s < ZCH * NR; ++s) {
+        for (int s = 1; s < ZC * NR; ++s) {
             const bool ge = e >= pf[s];
             i += ge ? 1 : 0;
             dj = ge ? djs[s] : dj;
@@ -217,7 +226,71 @@ __device__ __forceinline__ ZPoint zp_issue(ZCursor &k, const ZBlocks b, int lane
     }
     if (k.zc < b.zend) {
         k.bat += 64;
-        zc_settle(k, b, zstart, rg, lane);
+        zc_settle<ZC>(k, b, zstart, rg, lane);
+    }
+    return q;
+}
+
+// zp_issue with the range of each element found from ballots of the range
+// starts instead of one compare per range, so its cost and registers do not
+// grow with the number of ranges: lane j takes the last non-empty range that
+// starts at a batch element in (0, j] (marked in qidx by element, so that a
+// ballot of the marks is a mask over elements), else the one holding bat.
+template <int ZC>
+__device__ __forceinline__ ZPoint zp_issue_mask(ZCursor &k, const ZBlocks b, int lane,
+                                                const int32_t *__restrict__ zstart,
+                                                ZRanges<ZC> &rg, uint8_t *qidx,
+                                                const uint32_t *__restrict__ perm,
+                                                const uint32_t *__restrict__ word, const CF3s &frs,
+                                                const float2 *__restrict__ pre) {
+    constexpr int NQ = ZC * NR;
+    ZPoint q;
+    q.zc = k.zc;
+    q.nb = k.zc < b.zend ? min(64, k.tot - k.bat) : 0;
+    q.valid = lane < q.nb;
+    q.tsel = -1;
+    q.r = 0;
+    q.wd = 0;
+    q.src = 0;
+    q.fx = q.fy = q.fz = 0.f;
+    q.pv = make_float2(1.f, 0.f);
+    if (q.nb > 0) {
+        __syncthreads();  // the ranges written by zc_load are visible
+        int d = 0;
+        bool ne = false;
+        if (lane < NQ) {
+            const int st = rg.pf[lane];
+            ne = (lane + 1 < NQ ? rg.pf[lane + 1] : k.tot) > st;
+            d = st - k.bat;
+        }
+        // non-empty ranges starting at or before bat (ballot bit = range
+        // index); the last holds bat (bat < tot, so there is one)
+        const uint64_t mbefore = __ballot(ne && d <= 0);
+        const int q0 = 63 - __clzll(mbefore);
+        // qidx[d] = the range starting at batch element d (0xff: none), and
+        // mpos bit d set where one starts (ballot bit = element)
+        qidx[lane] = 0xff;
+        __syncthreads();
+        if (ne && d > 0 && d < 64) qidx[d] = (uint8_t)lane;
+        __syncthreads();
+        const uint64_t mpos = __ballot(qidx[lane] != 0xff);
+        if (q.valid) {
+            const uint64_t m = mpos & (lane == 63 ? ~0ull : ((2ull << lane) - 1));
+            const int i = m ? (int)qidx[63 - __clzll(m)] : q0;
+            q.tsel = i / NR;
+            q.r = i % NR;
+            const uint32_t j = (uint32_t)(k.bat + lane + rg.dj[i]);
+            q.wd = word[j];
+            q.fx = frs.p[0][j];
+            q.fy = frs.p[1][j];
+            q.fz = frs.p[2][j];
+            q.src = perm ? perm[j] : j;
+            if (pre) q.pv = pre[j];
+        }
+    }
+    if (k.zc < b.zend) {
+        k.bat += 64;
+        zc_settle<ZC>(k, b, zstart, rg, lane);
     }
     return q;
 }
@@ -241,7 +314,7 @@ __global__ __launch_bounds__(64) void k_spread_zsweep(int n0, int n1, int n2, in
     __shared__ __align__(16) uint16_t lists[ZCH][4][64];
     constexpr uint32_t kPad = 64u * REC * 4u;  // byte offset of the zero row
     __shared__ float2 stage[ZST][64];
-    __shared__ ZRanges rg;
+    __shared__ ZRanges<ZCH> rg;
     const int64_t nw = (int64_t)nbx * nby * nseg;
     int64_t wid = xcd_remap(blockIdx.x, nw);
     const int seg = (int)(wid % nseg);
@@ -269,14 +342,14 @@ __global__ __launch_bounds__(64) void k_spread_zsweep(int n0, int n1, int n2, in
     // Software pipeline over batches: while batch p1 is built and swept,
     // the strengths of p2 and the words / fractions / perm of p3 load.
     ZCursor cur;
-    zc_load(cur, z0 - (W - 1), bk, zstart, rg, lane);
-    zc_settle(cur, bk, zstart, rg, lane);
-    ZPoint p1 = zp_issue(cur, bk, lane, zstart, rg, perm, word, frs, pre);
+    zc_load<ZCH>(cur, z0 - (W - 1), bk, zstart, rg, lane);
+    zc_settle<ZCH>(cur, bk, zstart, rg, lane);
+    ZPoint p1 = zp_issue<ZCH>(cur, bk, lane, zstart, rg, perm, word, frs, pre);
     float2 c1 = p1.valid ? c[p1.src] : make_float2(0.f, 0.f);
-    ZPoint p2 = zp_issue(cur, bk, lane, zstart, rg, perm, word, frs, pre);
+    ZPoint p2 = zp_issue<ZCH>(cur, bk, lane, zstart, rg, perm, word, frs, pre);
     while (p1.nb > 0) {
         const float2 c2 = p2.valid ? c[p2.src] : make_float2(0.f, 0.f);
-        const ZPoint p3 = zp_issue(cur, bk, lane, zstart, rg, perm, word, frs, pre);
+        const ZPoint p3 = zp_issue<ZCH>(cur, bk, lane, zstart, rg, perm, word, frs, pre);
         const int zc = p1.zc;
         __syncthreads();
 #pragma unroll
@@ -390,6 +463,240 @@ __global__ __launch_bounds__(64) void k_spread_zsweep(int n0, int n1, int n2, in
     }
 }
 
+// ---------------------------------------------------------------------------
+// MFMA z-sweep: the same blocks, segments, point order and cursor as above,
+// with the z-window held in matrix-core accumulators instead of per-lane
+// registers.
+//
+// Each 4x4 column quadrant q = (qx, qy) of the block has one 16x16 f32
+// accumulator: rows i are its cells (4qx + i/4, 4qy + i%4), columns
+// j = 2s + ri are 8 z-slots (z = zb + s) times (re, im). A chunk is ZC
+// consecutive z-steps [zb, zb + ZC) with ZC + W - 1 <= 8, so the footprint
+// of every point whose first tap lies in the chunk fits the 8 slots. The
+// cursor walks groups of G chunks and a batch holds up to 64 points of one
+// group, in z-major order, so each chunk's points are consecutive lanes.
+//
+// A lane-per-point prologue writes each point's table row: the block's 8
+// x-weights and 8 y-weights (zero outside the footprint), stored as pairs
+// (w[a], w[a + 4]) so that one 8-byte read gives a lane its factor for both
+// quadrant columns (rows), and B = strength x z-weight at the point's slot
+// offset in its chunk (16 floats, j = 2s + ri). The sweep then takes the
+// chunk's rows 4 at a time; per K-step every quadrant runs
+// v_mfma_f32_16x16x4f32 with A[i][k] = wx[x_i] wy[y_i] (zero off the
+// footprint) and the shared B[k][j]. Lane l supplies A[l % 16][l / 16] and
+// B[l / 16][l % 16] and holds D[4 (l / 16) + r][l % 16] in element r. Every
+// point costs 4 MFMAs / 4 and the lane 3 LDS reads and 4 MULs per K-step.
+//
+// When the sweep passes a chunk, its slots 0 .. ZC-1 are complete: they go
+// to an LDS ring of RING z-cells per column (flushed as runs along z) and
+// every accumulator register shifts down by ZC slots (2 ZC lanes) with one
+// DPP row_shl, which fills the freed slots with zeros.
+#ifndef ZM_REC
+#define ZM_REC 36
+#endif
+#ifndef ZM_UNR
+#define ZM_UNR 2
+#endif
+constexpr int MREC = ZM_REC;  // floats per table row: wx pairs[8], wy pairs[8], B[16], pad
+constexpr int RING = 8;       // z-cells per column in the store ring
+constexpr int KUNR = ZM_UNR;  // K-steps per unrolled sweep iteration
+
+template <int W>
+constexpr int mfma_chunk() {
+    return (9 - W) < 4 ? (9 - W) : 4;
+}
+// chunks per cursor group: groups of 6 - 8 z-steps (at most 32 key ranges)
+template <int W>
+constexpr int mfma_group() {
+    return 8 / mfma_chunk<W>();
+}
+
+template <int SH>
+__device__ __forceinline__ float row_shl_zero(float v) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + SH, 0xf, 0xf, true));
+}
+
+// Write the ring's cells [fz, cz) of the owned segment (starting at z0) to
+// the grid: 8 lanes per column, 8 columns per pass.
+__device__ __forceinline__ void ring_flush(const float2 *ring, float2 *__restrict__ grid, int lane,
+                                           int fz, int cz, int z0, int n1, int n2, int bx,
+                                           int by) {
+    __syncthreads();
+    const int nz = cz - fz, zo = lane & 7;
+#pragma unroll
+    for (int pass = 0; pass < 8; ++pass) {
+        const int col = pass * 8 + (lane >> 3);
+        if (zo < nz) {
+            const int gx = ZB * bx + (col >> 3), gy = ZB * by + (col & 7);
+            grid[((int64_t)gx * n1 + gy) * n2 + fz + zo] =
+                ring[col * RING + ((fz - z0 + zo) & (RING - 1))];
+        }
+    }
+    __syncthreads();
+}
+
+typedef float mf4 __attribute__((ext_vector_type(4)));
+
+#ifdef ZM_OCC
+#define ZM_WPE __attribute__((amdgpu_waves_per_eu(ZM_OCC)))
+#else
+#define ZM_WPE
+#endif
+template <int W>
+__global__ __launch_bounds__(64) ZM_WPE void k_spread_zsweep_mfma(
+    int n0, int n1, int n2, int nbx, int nby, int zseg, int nseg, float bl2e, float inv_hw,
+    const int32_t *__restrict__ zstart, const uint32_t *__restrict__ perm,
+    const uint32_t *__restrict__ word, CF3s frs, const float2 *__restrict__ c,
+    const float2 *__restrict__ pre, float2 *__restrict__ grid) {
+    constexpr int ZC = mfma_chunk<W>(), G = mfma_group<W>(), ZG = ZC * G;
+    static_assert(ZC + W - 1 <= 8 && ZC <= RING, "chunk footprint exceeds the 8 slots");
+    __shared__ __align__(16) float table[(64 + 1) * MREC];
+    __shared__ __align__(16) float2 ring[64 * RING];
+    __shared__ ZRanges<ZG> rg;
+    __shared__ uint8_t qidx[64];
+    constexpr uint32_t kPad = 64u * MREC * 4u;  // byte offset of the zero row
+    const int64_t nw = (int64_t)nbx * nby * nseg;
+    int64_t wid = xcd_remap(blockIdx.x, nw);
+    const int seg = (int)(wid % nseg);
+    wid /= nseg;
+    const int by = (int)(wid % nby), bx = (int)(wid / nby);
+    const int z0 = seg * zseg, zend = min(z0 + zseg, n2);
+    const int lane = threadIdx.x, li = lane & 15, lk = lane >> 4;
+    if (lane < MREC) table[64 * MREC + lane] = 0.f;
+    // byte offsets, within a table row, of this lane's wx pair, wy pair and B
+    const int xo = 8 * (li >> 2), yo = 4 * ZB + 8 * (li & 3), bo = 4 * 2 * ZB + 4 * li;
+    ZBlocks bk;
+    bk.bx = bx;
+    bk.by = by;
+    bk.bxm = bx == 0 ? nbx - 1 : bx - 1;
+    bk.bym = by == 0 ? nby - 1 : by - 1;
+    bk.nby = nby;
+    bk.n2 = n2;
+    bk.zend = zend;
+    mf4 acc[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) acc[q] = mf4{0.f, 0.f, 0.f, 0.f};
+    int zb = z0 - (W - 1);  // z of slot 0
+    int fz = z0, cz = z0;   // owned cells [z0, fz) are stored, [fz, cz) sit in the ring
+
+    // Slots 0 .. ZC-1 are complete: stage the owned ones in the ring, then
+    // shift every accumulator down by ZC slots.
+    auto advance = [&]() {
+        const int lo = max(zb, z0), hi = min(zb + ZC, zend);
+        if (lo < hi) {
+            if (hi - fz > RING) {
+                ring_flush(ring, grid, lane, fz, cz, z0, n1, n2, bx, by);
+                fz = cz;
+            }
+            const int s = li >> 1, z = zb + s;
+            if (s < ZC && z >= lo && z < hi) {
+                float *rf = reinterpret_cast<float *>(ring) + ((z - z0) & (RING - 1)) * 2 + (li & 1);
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int col = (4 * (q >> 1) + lk) * ZB + 4 * (q & 1) + r;
+                        rf[col * RING * 2] = acc[q][r];
+                    }
+            }
+            cz = hi;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[q][r] = row_shl_zero<2 * ZC>(acc[q][r]);
+        zb += ZC;
+    };
+
+    ZCursor cur;
+    zc_load<ZG>(cur, z0 - (W - 1), bk, zstart, rg, lane);
+    zc_settle<ZG>(cur, bk, zstart, rg, lane);
+    ZPoint p1 = zp_issue_mask<ZG>(cur, bk, lane, zstart, rg, qidx, perm, word, frs, pre);
+    float2 c1 = p1.valid ? c[p1.src] : make_float2(0.f, 0.f);
+    ZPoint p2 = zp_issue_mask<ZG>(cur, bk, lane, zstart, rg, qidx, perm, word, frs, pre);
+    while (p1.nb > 0) {
+        const float2 c2 = p2.valid ? c[p2.src] : make_float2(0.f, 0.f);
+        const ZPoint p3 = zp_issue_mask<ZG>(cur, bk, lane, zstart, rg, qidx, perm, word, frs, pre);
+        const int pch = p1.tsel / ZC;  // the point's chunk in the group
+        __syncthreads();
+        if (p1.valid) {
+            // first tap relative to this block (minus 8 for points of the -x
+            // / -y neighbour blocks) and its slot in the chunk
+            const int ox = (int)((p1.wd >> kZsKeyBits) & 7u) - ((p1.r & 1) ? ZB : 0);
+            const int oy = (int)((p1.wd >> (kZsKeyBits + 3)) & 7u) - ((p1.r & 2) ? ZB : 0);
+            const int dz = p1.tsel - pch * ZC;
+            const float2 cv = make_float2(c1.x * p1.pv.x - c1.y * p1.pv.y,
+                                          c1.x * p1.pv.y + c1.y * p1.pv.x);
+            float4 *rec = reinterpret_cast<float4 *>(table + lane * MREC);
+            constexpr float ih = 2.0f / W;
+            const float sx = ((float)ox + p1.fx) * ih, sy = ((float)oy + p1.fy) * ih;
+            const float sz = p1.fz * ih;
+            float wx[ZB], wy[ZB], bz[ZB];
+#pragma unroll
+            for (int q = 0; q < ZB; ++q) {
+                const float ex = es_weight_z((float)q * ih - sx, bl2e);
+                const float ey = es_weight_z((float)q * ih - sy, bl2e);
+                const float ez = es_weight_z((float)(q - dz) * ih - sz, bl2e);
+                wx[q] = ((unsigned)(q - ox) < (unsigned)W) ? ex : 0.f;
+                wy[q] = ((unsigned)(q - oy) < (unsigned)W) ? ey : 0.f;
+                bz[q] = ((unsigned)(q - dz) < (unsigned)W) ? ez : 0.f;
+            }
+            rec[0] = make_float4(wx[0], wx[4], wx[1], wx[5]);
+            rec[1] = make_float4(wx[2], wx[6], wx[3], wx[7]);
+            rec[2] = make_float4(wy[0], wy[4], wy[1], wy[5]);
+            rec[3] = make_float4(wy[2], wy[6], wy[3], wy[7]);
+#pragma unroll
+            for (int q = 0; q < ZB; q += 2)
+                rec[4 + q / 2] = make_float4(cv.x * bz[q], cv.y * bz[q], cv.x * bz[q + 1],
+                                             cv.y * bz[q + 1]);
+        }
+        // each chunk's points: lanes [lo, lo + n) of the batch
+        int nn[G], lo[G];
+#pragma unroll
+        for (int ch = 0; ch < G; ++ch) {
+            nn[ch] = __popcll(__ballot(p1.valid && pch == ch));
+            lo[ch] = ch == 0 ? 0 : lo[ch - 1] + nn[ch - 1];
+        }
+        __syncthreads();
+        const char *tb = reinterpret_cast<const char *>(table);
+#pragma unroll
+        for (int ch = 0; ch < G; ++ch) {
+            // a chunk with points in this batch: every earlier chunk is
+            // complete (the cursor is z-major), so the window moves up to it
+            const int n = nn[ch];
+            if (n == 0) continue;
+            while (zb < p1.zc + ch * ZC) advance();
+            for (int e0 = 0; e0 < n; e0 += 4 * KUNR) {
+                float av[KUNR][4], bv[KUNR];
+#pragma unroll
+                for (int u = 0; u < KUNR; ++u) {
+                    const int e = e0 + 4 * u + lk;
+                    const uint32_t rb = e < n ? (uint32_t)(lo[ch] + e) * (MREC * 4u) : kPad;
+                    const float2 px = *reinterpret_cast<const float2 *>(tb + rb + xo);
+                    const float2 py = *reinterpret_cast<const float2 *>(tb + rb + yo);
+                    bv[u] = *reinterpret_cast<const float *>(tb + rb + bo);
+                    av[u][0] = px.x * py.x;  // q = 0: (qx, qy) = (0, 0)
+                    av[u][1] = px.x * py.y;  // q = 1: (0, 1)
+                    av[u][2] = px.y * py.x;  // q = 2: (1, 0)
+                    av[u][3] = px.y * py.y;  // q = 3: (1, 1)
+                }
+#pragma unroll
+                for (int u = 0; u < KUNR; ++u)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u][q], bv[u], acc[q],
+                                                                      0, 0, 0);
+            }
+        }
+        p1 = p2;
+        c1 = c2;
+        p2 = p3;
+    }
+    while (zb < zend) advance();
+    if (cz > fz) ring_flush(ring, grid, lane, fz, cz, z0, n1, n2, bx, by);
+}
+
 }  // namespace
 
 int zsweep_check(const mn_bins *g) {
@@ -420,6 +727,7 @@ struct ZArgs {
     const float2 *c, *pre;
     float2 *grid;
     hipStream_t s;
+    bool valu;  // per-lane register windows instead of MFMA accumulators
 };
 
 template <int DIM, int W>
@@ -434,9 +742,14 @@ struct ZLaunch {
             const int64_t nw = (int64_t)nbx * nby * nseg;
             const float bl2e = (float)(a.beta * 1.4426950408889634);
             const float inv_hw = (float)(2.0 / W);
-            k_spread_zsweep<W><<<(unsigned)nw, 64, 0, a.s>>>(n0, n1, n2, nbx, nby, a.zseg, nseg,
-                                                             bl2e, inv_hw, a.zstart, a.perm,
-                                                             a.word, a.frs, a.c, a.pre, a.grid);
+            if (a.valu)
+                k_spread_zsweep<W><<<(unsigned)nw, 64, 0, a.s>>>(
+                    n0, n1, n2, nbx, nby, a.zseg, nseg, bl2e, inv_hw, a.zstart, a.perm, a.word,
+                    a.frs, a.c, a.pre, a.grid);
+            else
+                k_spread_zsweep_mfma<W><<<(unsigned)nw, 64, 0, a.s>>>(
+                    n0, n1, n2, nbx, nby, a.zseg, nseg, bl2e, inv_hw, a.zstart, a.perm, a.word,
+                    a.frs, a.c, a.pre, a.grid);
             MN_LAUNCH_CHECK("spread_zsweep");
             return MN_OK;
         }
@@ -490,6 +803,8 @@ int mn_spread_zsweep(const mn_bins *g, float beta, int64_t P, int zseg, const in
     a.pre = static_cast<const float2 *>(pre);
     a.grid = static_cast<float2 *>(grid);
     a.s = as_stream(stream);
+    const char *kv = getenv("MN_ZSWEEP_KERNEL");
+    a.valu = kv && strcmp(kv, "valu") == 0;
     return select_dim_w<ZLaunch>(3, g->w, a);
 }
 

@@ -79,10 +79,15 @@ def _grid_check(oracle, mn, x, c, N, eps, tol=1e-5):
     return p
 
 
+KERNELS = ["mfma", "valu"]
+
+
+@pytest.mark.parametrize("kernel", KERNELS)
 @pytest.mark.parametrize("eps", [1e-1, 1e-2, 1e-3, 1e-4, 1e-5, 1e-6, 1e-7])
-def test_zsweep_widths(eps, oracle, mn):
-    """w = 2 .. 8 through eps (sigma = 2)."""
-    print(f"case zsweep width eps={eps}", flush=True)
+def test_zsweep_widths(eps, kernel, oracle, mn, monkeypatch):
+    """w = 2 .. 8 through eps (sigma = 2), both sweep kernels."""
+    print(f"case zsweep width eps={eps} kernel={kernel}", flush=True)
+    monkeypatch.setenv("MN_ZSWEEP_KERNEL", kernel)
     rng = np.random.default_rng(22)
     M = 20_000
     x = [rng.uniform(-np.pi, np.pi, M) for _ in range(3)]
@@ -90,10 +95,12 @@ def test_zsweep_widths(eps, oracle, mn):
     _grid_check(oracle, mn, x, c, (24, 20, 18), eps)
 
 
-def test_zsweep_clustered_and_wrapping(oracle, mn):
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_zsweep_clustered_and_wrapping(kernel, oracle, mn, monkeypatch):
     """Points clustered at the periodic corner (many per block and z, and
     footprints wrapping in x, y, z) on a 16x16 grid."""
-    print("case zsweep clustered", flush=True)
+    print(f"case zsweep clustered kernel={kernel}", flush=True)
+    monkeypatch.setenv("MN_ZSWEEP_KERNEL", kernel)
     rng = np.random.default_rng(23)
     M = 40_000
     h = 2 * np.pi / 16
@@ -103,9 +110,11 @@ def test_zsweep_clustered_and_wrapping(oracle, mn):
     _grid_check(oracle, mn, x, c, (8, 8, 8), 1e-5)
 
 
-def test_zsweep_partial_segment(oracle, mn):
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_zsweep_partial_segment(kernel, oracle, mn, monkeypatch):
     """A z extent (n2 = 300) that is not a multiple of the 128-cell segment."""
-    print("case zsweep partial segment", flush=True)
+    print(f"case zsweep partial segment kernel={kernel}", flush=True)
+    monkeypatch.setenv("MN_ZSWEEP_KERNEL", kernel)
     rng = np.random.default_rng(24)
     M = 60_000
     x = [rng.uniform(-np.pi, np.pi, M) for _ in range(3)]
@@ -138,3 +147,33 @@ def test_zsweep_matches_tiles(mn, monkeypatch):
     gp = torch.empty_like(gz)
     E.spread_zsweep(pz.pts, pz.beta, cs, gp, presorted=True)
     assert torch.equal(gp, gz)
+
+
+@pytest.mark.parametrize("N,eps", [((64, 64, 48), 1e-5), ((32, 48, 40), 1e-7), ((48, 32, 64), 1e-2)])
+def test_zsweep_mfma_equals_valu(N, eps, mn, monkeypatch):
+    """The MFMA accumulator sweep and the per-lane register sweep spread the
+    same points to the same grid (fp32 rounding apart), with segments
+    shorter than the grid so segment edges are exercised."""
+    from mlx_nufft_amd import _engine as E
+
+    print(f"case zsweep mfma vs valu N={N} eps={eps}", flush=True)
+    rng = np.random.default_rng(27)
+    M = 150_000
+    x = [rng.uniform(-np.pi, np.pi, M) for _ in range(3)]
+    c = torch.from_numpy((rng.standard_normal(M) + 1j * rng.standard_normal(M))
+                         .astype(np.complex64)).cuda()
+    p = mn.Type1PlanND(tuple(x), N, eps=eps)
+    assert p.pts.kind == "zsweep"
+    grids = {}
+    for kernel in KERNELS:
+        monkeypatch.setenv("MN_ZSWEEP_KERNEL", kernel)
+        for zseg in (16, 128):
+            g = torch.full(p.n_up, float("nan"), dtype=torch.complex64, device="cuda")
+            E.spread_zsweep(p.pts, p.beta, c, g, zseg=zseg)
+            assert bool(torch.isfinite(torch.view_as_real(g)).all()), (kernel, zseg)
+            grids[kernel, zseg] = g
+    ref = grids["valu", 128]
+    for key, g in grids.items():
+        rel = float((g - ref).abs().norm() / ref.abs().norm())
+        print(f"  {key}: rel diff {rel:.2e}")
+        assert rel < 1e-6, key
