@@ -231,31 +231,98 @@ __device__ __forceinline__ ZPoint zp_issue(ZCursor &k, const ZBlocks b, int lane
     return q;
 }
 
+// A cursor that prefetches: while the wave works through group zc, the raw
+// zstart bounds of group pzc = zc + ZC are already loading into nst / nen
+// (lane i < ZC * NR: range i of that group), so moving to the next group does
+// not wait for memory.
+struct ZCursorP {
+    int zc, bat, tot;  // as ZCursor
+    int pzc;           // group whose bounds are in nst / nen
+    int nst, nen;      // this lane's range of group pzc: sorted [nst, nen)
+};
+
+template <int ZC>
+__device__ __forceinline__ void zcp_fetch(ZCursorP &k, int zc, const ZBlocks b,
+                                          const int32_t *__restrict__ zstart, int lane) {
+    k.pzc = zc;
+    const int r = lane % NR, z = zc + lane / NR;
+    const bool ok = lane < ZC * NR && z < b.zend;
+    const int zz = z < 0 ? z + b.n2 : z;
+    // source r: bit 0 = -x neighbour, bit 1 = -y neighbour; its key classes
+    // [lo, hi] are those that reach this block
+    const int blk = ((r & 1) ? b.bxm : b.bx) * b.nby + ((r & 2) ? b.bym : b.by);
+    const int lo = r == 0 ? 0 : (r == 2 ? 1 : 2), hi = (r & 2) ? 2 : 3;
+    const int64_t kb = ok ? ((int64_t)blk * b.n2 + zz) * 4 : 0;
+    // loads by every lane (key 0 for the others), outside any branch
+    const int st = zstart[kb + (ok ? lo : 0)], en = zstart[kb + (ok ? hi + 1 : 0)];
+    k.nst = ok ? st : 0;
+    k.nen = ok ? en : 0;
+}
+
+// Make group zc current (its ranges into rg, as zc_load) and start loading
+// the bounds of the group after it.
+template <int ZC>
+__device__ __forceinline__ void zcp_load(ZCursorP &k, int zc, const ZBlocks b,
+                                         const int32_t *__restrict__ zstart, ZRanges<ZC> &rg,
+                                         int lane) {
+    if (k.pzc != zc) zcp_fetch<ZC>(k, zc, b, zstart, lane);
+    const int st = k.nst, cnt = k.nen - k.nst;
+    k.zc = zc;
+    k.bat = 0;
+    int incl = cnt;
+#pragma unroll
+    for (int d = 1; d < ZC * NR; d <<= 1) {
+        const int v = __shfl_up(incl, d, 64);
+        incl += (lane >= d) ? v : 0;
+    }
+    __syncthreads();  // earlier reads of rg are done
+    if (lane < ZC * NR) {
+        rg.pf[lane] = incl - cnt;
+        rg.dj[lane] = st - (incl - cnt);
+    }
+    k.tot = __shfl(incl, ZC * NR - 1, 64);
+    // the next group's bounds load only now, after this group's were used,
+    // so using them never waits on the new loads
+    zcp_fetch<ZC>(k, zc + ZC, b, zstart, lane);
+}
+
+template <int ZC>
+__device__ __forceinline__ void zcp_settle(ZCursorP &k, const ZBlocks b,
+                                           const int32_t *__restrict__ zstart, ZRanges<ZC> &rg,
+                                           int lane) {
+    // the usual single step is straight-line code; only a run of empty
+    // groups loops (a loop makes the compiler wait for every load first)
+    if (k.bat >= k.tot && k.zc < b.zend) {
+        zcp_load<ZC>(k, k.zc + ZC, b, zstart, rg, lane);
+        while (k.bat >= k.tot && k.zc < b.zend) zcp_load<ZC>(k, k.zc + ZC, b, zstart, rg, lane);
+    }
+}
+
 // zp_issue with the range of each element found from ballots of the range
 // starts instead of one compare per range, so its cost and registers do not
 // grow with the number of ranges: lane j takes the last non-empty range that
 // starts at a batch element in (0, j] (marked in qidx by element, so that a
 // ballot of the marks is a mask over elements), else the one holding bat.
-template <int ZC>
-__device__ __forceinline__ ZPoint zp_issue_mask(ZCursor &k, const ZBlocks b, int lane,
+template <int ZC, bool PRE>
+__device__ __forceinline__ ZPoint zp_issue_mask(ZCursorP &k, const ZBlocks b, int lane,
                                                 const int32_t *__restrict__ zstart,
                                                 ZRanges<ZC> &rg, uint8_t *qidx,
                                                 const uint32_t *__restrict__ perm,
                                                 const uint32_t *__restrict__ word, const CF3s &frs,
                                                 const float2 *__restrict__ pre) {
     constexpr int NQ = ZC * NR;
+    // settle here rather than after the previous batch's loads were issued,
+    // so a group change never waits on loads that are not needed yet
+    zcp_settle<ZC>(k, b, zstart, rg, lane);
     ZPoint q;
     q.zc = k.zc;
     q.nb = k.zc < b.zend ? min(64, k.tot - k.bat) : 0;
     q.valid = lane < q.nb;
     q.tsel = -1;
     q.r = 0;
-    q.wd = 0;
-    q.src = 0;
-    q.fx = q.fy = q.fz = 0.f;
-    q.pv = make_float2(1.f, 0.f);
+    uint32_t j = 0;  // sorted index of this lane's point (0 for an idle lane)
     if (q.nb > 0) {
-        __syncthreads();  // the ranges written by zc_load are visible
+        __syncthreads();  // the ranges written by zcp_load are visible
         int d = 0;
         bool ne = false;
         if (lane < NQ) {
@@ -274,24 +341,27 @@ __device__ __forceinline__ ZPoint zp_issue_mask(ZCursor &k, const ZBlocks b, int
         if (ne && d > 0 && d < 64) qidx[d] = (uint8_t)lane;
         __syncthreads();
         const uint64_t mpos = __ballot(qidx[lane] != 0xff);
-        if (q.valid) {
-            const uint64_t m = mpos & (lane == 63 ? ~0ull : ((2ull << lane) - 1));
-            const int i = m ? (int)qidx[63 - __clzll(m)] : q0;
-            q.tsel = i / NR;
-            q.r = i % NR;
-            const uint32_t j = (uint32_t)(k.bat + lane + rg.dj[i]);
-            q.wd = word[j];
-            q.fx = frs.p[0][j];
-            q.fy = frs.p[1][j];
-            q.fz = frs.p[2][j];
-            q.src = perm ? perm[j] : j;
-            if (pre) q.pv = pre[j];
-        }
+        const uint64_t m = mpos & (lane == 63 ? ~0ull : ((2ull << lane) - 1));
+        const int i = m ? (int)qidx[63 - __clzll(m)] : q0;
+        const uint32_t jv = (uint32_t)(k.bat + lane + rg.dj[i]);
+        q.tsel = q.valid ? i / NR : -1;
+        q.r = i % NR;
+        j = q.valid ? jv : 0u;
     }
-    if (k.zc < b.zend) {
-        k.bat += 64;
-        zc_settle<ZC>(k, b, zstart, rg, lane);
-    }
+    // The loads are issued by every lane (an idle lane reads element 0,
+    // P >= 1), outside any branch, so the compiler can wait for exactly the
+    // loads a later use needs and the batches overlap.
+    q.wd = word[j];
+    q.fx = frs.p[0][j];
+    q.fy = frs.p[1][j];
+    q.fz = frs.p[2][j];
+    const uint32_t pj = (perm ? perm : word)[j];
+    q.src = perm ? pj : j;
+    if constexpr (PRE)
+        q.pv = pre[j];
+    else
+        q.pv = make_float2(1.f, 0.f);
+    if (k.zc < b.zend) k.bat += 64;
     return q;
 }
 
@@ -538,12 +608,11 @@ __device__ __forceinline__ void ring_flush(const float2 *ring, float2 *__restric
 
 typedef float mf4 __attribute__((ext_vector_type(4)));
 
-#ifdef ZM_OCC
-#define ZM_WPE __attribute__((amdgpu_waves_per_eu(ZM_OCC)))
-#else
-#define ZM_WPE
+#ifndef ZM_OCC
+#define ZM_OCC 3
 #endif
-template <int W>
+#define ZM_WPE __attribute__((amdgpu_waves_per_eu(ZM_OCC)))
+template <int W, bool PRE>
 __global__ __launch_bounds__(64) ZM_WPE void k_spread_zsweep_mfma(
     int n0, int n1, int n2, int nbx, int nby, int zseg, int nseg, float bl2e, float inv_hw,
     const int32_t *__restrict__ zstart, const uint32_t *__restrict__ perm,
@@ -609,29 +678,22 @@ __global__ __launch_bounds__(64) ZM_WPE void k_spread_zsweep_mfma(
         zb += ZC;
     };
 
-    ZCursor cur;
-    zc_load<ZG>(cur, z0 - (W - 1), bk, zstart, rg, lane);
-    zc_settle<ZG>(cur, bk, zstart, rg, lane);
-    ZPoint p1 = zp_issue_mask<ZG>(cur, bk, lane, zstart, rg, qidx, perm, word, frs, pre);
-    float2 c1 = p1.valid ? c[p1.src] : make_float2(0.f, 0.f);
-    ZPoint p2 = zp_issue_mask<ZG>(cur, bk, lane, zstart, rg, qidx, perm, word, frs, pre);
-    while (p1.nb > 0) {
-        const float2 c2 = p2.valid ? c[p2.src] : make_float2(0.f, 0.f);
-        const ZPoint p3 = zp_issue_mask<ZG>(cur, bk, lane, zstart, rg, qidx, perm, word, frs, pre);
-        const int pch = p1.tsel / ZC;  // the point's chunk in the group
+    // Build and sweep one batch p whose strengths are cp.
+    auto process = [&](const ZPoint &p, const float2 cp) __attribute__((always_inline)) {
+        const int pch = p.tsel / ZC;  // the point's chunk in the group
         __syncthreads();
-        if (p1.valid) {
+        if (p.valid) {
             // first tap relative to this block (minus 8 for points of the -x
             // / -y neighbour blocks) and its slot in the chunk
-            const int ox = (int)((p1.wd >> kZsKeyBits) & 7u) - ((p1.r & 1) ? ZB : 0);
-            const int oy = (int)((p1.wd >> (kZsKeyBits + 3)) & 7u) - ((p1.r & 2) ? ZB : 0);
-            const int dz = p1.tsel - pch * ZC;
-            const float2 cv = make_float2(c1.x * p1.pv.x - c1.y * p1.pv.y,
-                                          c1.x * p1.pv.y + c1.y * p1.pv.x);
+            const int ox = (int)((p.wd >> kZsKeyBits) & 7u) - ((p.r & 1) ? ZB : 0);
+            const int oy = (int)((p.wd >> (kZsKeyBits + 3)) & 7u) - ((p.r & 2) ? ZB : 0);
+            const int dz = p.tsel - pch * ZC;
+            const float2 cv = make_float2(cp.x * p.pv.x - cp.y * p.pv.y,
+                                          cp.x * p.pv.y + cp.y * p.pv.x);
             float4 *rec = reinterpret_cast<float4 *>(table + lane * MREC);
             constexpr float ih = 2.0f / W;
-            const float sx = ((float)ox + p1.fx) * ih, sy = ((float)oy + p1.fy) * ih;
-            const float sz = p1.fz * ih;
+            const float sx = ((float)ox + p.fx) * ih, sy = ((float)oy + p.fy) * ih;
+            const float sz = p.fz * ih;
             float wx[ZB], wy[ZB], bz[ZB];
 #pragma unroll
             for (int q = 0; q < ZB; ++q) {
@@ -655,7 +717,7 @@ __global__ __launch_bounds__(64) ZM_WPE void k_spread_zsweep_mfma(
         int nn[G], lo[G];
 #pragma unroll
         for (int ch = 0; ch < G; ++ch) {
-            nn[ch] = __popcll(__ballot(p1.valid && pch == ch));
+            nn[ch] = __popcll(__ballot(p.valid && pch == ch));
             lo[ch] = ch == 0 ? 0 : lo[ch - 1] + nn[ch - 1];
         }
         __syncthreads();
@@ -666,7 +728,17 @@ __global__ __launch_bounds__(64) ZM_WPE void k_spread_zsweep_mfma(
             // complete (the cursor is z-major), so the window moves up to it
             const int n = nn[ch];
             if (n == 0) continue;
-            while (zb < p1.zc + ch * ZC) advance();
+            // usually one chunk: the first two steps are straight-line code,
+            // so only a longer jump enters a loop (a loop that stores makes the
+            // compiler wait for every outstanding load before it)
+            const int zt = p.zc + ch * ZC;
+            if (zb < zt) {
+                advance();
+                if (zb < zt) {
+                    advance();
+                    while (zb < zt) advance();
+                }
+            }
             for (int e0 = 0; e0 < n; e0 += 4 * KUNR) {
                 float av[KUNR][4], bv[KUNR];
 #pragma unroll
@@ -689,9 +761,33 @@ __global__ __launch_bounds__(64) ZM_WPE void k_spread_zsweep_mfma(
                                                                       0, 0, 0);
             }
         }
-        p1 = p2;
-        c1 = c2;
-        p2 = p3;
+    };
+
+    // The batch loop, unrolled three ways with rotating names (A, B, C) so
+    // that no register still being loaded is copied (a copy would wait for
+    // it): each stage issues the loads of the batch two ahead, gathers the
+    // strengths of the next one, then builds and sweeps the current one.
+    ZCursorP cur;
+    cur.pzc = INT32_MIN;
+    zcp_load<ZG>(cur, z0 - (W - 1), bk, zstart, rg, lane);
+    ZPoint pa = zp_issue_mask<ZG, PRE>(cur, bk, lane, zstart, rg, qidx, perm, word, frs, pre);
+    float2 ca = c[pa.src];  // idle lanes read c[perm[0]]: their rows are never used
+    ZPoint pb = zp_issue_mask<ZG, PRE>(cur, bk, lane, zstart, rg, qidx, perm, word, frs, pre);
+    ZPoint pc;
+    float2 cb, cc;
+    for (;;) {
+        if (pa.nb == 0) break;
+        pc = zp_issue_mask<ZG, PRE>(cur, bk, lane, zstart, rg, qidx, perm, word, frs, pre);
+        cb = c[pb.src];
+        process(pa, ca);
+        if (pb.nb == 0) break;
+        pa = zp_issue_mask<ZG, PRE>(cur, bk, lane, zstart, rg, qidx, perm, word, frs, pre);
+        cc = c[pc.src];
+        process(pb, cb);
+        if (pc.nb == 0) break;
+        pb = zp_issue_mask<ZG, PRE>(cur, bk, lane, zstart, rg, qidx, perm, word, frs, pre);
+        ca = c[pa.src];
+        process(pc, cc);
     }
     while (zb < zend) advance();
     if (cz > fz) ring_flush(ring, grid, lane, fz, cz, z0, n1, n2, bx, by);
@@ -746,8 +842,12 @@ struct ZLaunch {
                 k_spread_zsweep<W><<<(unsigned)nw, 64, 0, a.s>>>(
                     n0, n1, n2, nbx, nby, a.zseg, nseg, bl2e, inv_hw, a.zstart, a.perm, a.word,
                     a.frs, a.c, a.pre, a.grid);
+            else if (a.pre)
+                k_spread_zsweep_mfma<W, true><<<(unsigned)nw, 64, 0, a.s>>>(
+                    n0, n1, n2, nbx, nby, a.zseg, nseg, bl2e, inv_hw, a.zstart, a.perm, a.word,
+                    a.frs, a.c, a.pre, a.grid);
             else
-                k_spread_zsweep_mfma<W><<<(unsigned)nw, 64, 0, a.s>>>(
+                k_spread_zsweep_mfma<W, false><<<(unsigned)nw, 64, 0, a.s>>>(
                     n0, n1, n2, nbx, nby, a.zseg, nseg, bl2e, inv_hw, a.zstart, a.perm, a.word,
                     a.frs, a.c, a.pre, a.grid);
             MN_LAUNCH_CHECK("spread_zsweep");
