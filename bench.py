@@ -185,7 +185,10 @@ def main():
     fk = plan.execute(cd, return_np=False)
     plan_w, plan_bins = plan.w, [plan.bins.m[d] for d in range(3)]
     zsweep = plan.pts.kind == "zsweep"
-    spread_kernel = f"k_spread_zsweep<{plan_w}>" if zsweep else f"k_spread_tiled<3,{plan_w},false>"
+    valu_sweep = os.environ.get("MN_ZSWEEP_KERNEL") == "valu"
+    spread_kernel = ((f"k_spread_zsweep<{plan_w}>" if valu_sweep
+                      else f"k_spread_zsweep_mfma<{plan_w}, false>") if zsweep
+                     else f"k_spread_tiled<3,{plan_w},false>")
     del plan
     p2 = mn.Type2PlanND(tuple(xd), N, eps=eps, isign=-1)
     for _ in range(max(1, args.warmup)):
@@ -216,7 +219,10 @@ def main():
         "config": {"workload": "3D type-1 M=2e7 N=256^3 eps=1e-5 (BASELINE.json configs[3])",
                    "M": M, "N": list(N), "eps": eps, "isign": 1, "w": plan_w,
                    "n_up": list(n_up),
-                   "spread": ("z-sweep, 8x8 column blocks" if zsweep else f"LDS tiles {plan_bins}"),
+                   "spread": ((("z-sweep, 8x8 column blocks, "
+                                + ("per-lane register windows" if valu_sweep
+                                   else "MFMA accumulator windows")) if zsweep
+                               else f"LDS tiles {plan_bins}")),
                    "step": ("execute only" if args.exec_only else
                             "set_sources + execute, device-resident")},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,

@@ -1,6 +1,12 @@
 // Owner-computes 3D spread ("z-sweep"): no atomics, every fine-grid cell is
 // written exactly once with a plain store.
 //
+// Two kernels share the blocks, segments, point order and key ranges below:
+// k_spread_zsweep_mfma (the default, described further down) keeps the
+// z-window of each 4x4 column quadrant in a matrix-core accumulator, and
+// k_spread_zsweep (MN_ZSWEEP_KERNEL=valu) keeps it in per-lane registers, as
+// this first part describes.
+//
 // Layout. The grid is cut into 8x8 (x, y) column blocks. Each wavefront owns
 // one block over a z-segment; each lane owns one column of the block (lanes
 // grouped by 4x4 quadrant, below) and keeps a W-cell complex window
@@ -561,6 +567,15 @@ __global__ __launch_bounds__(64) void k_spread_zsweep(int n0, int n1, int n2, in
 // to an LDS ring of RING z-cells per column (flushed as runs along z) and
 // every accumulator register shifts down by ZC slots (2 ZC lanes) with one
 // DPP row_shl, which fills the freed slots with zeros.
+//
+// Loads. Memory waits on this target count outstanding loads in issue order,
+// and the compiler can only wait for "all but the newest n" when every load
+// is certain to have been issued. So each batch's loads are issued by every
+// lane outside any branch, the batch loop is unrolled three ways (a register
+// copy of a value still loading would wait for it), and the key-range
+// bounds of the next cursor group are fetched one group ahead. The words,
+// fractions and perm of batch k + 2 and the strengths of batch k + 1 are in
+// flight while batch k is built and swept.
 #ifndef ZM_REC
 #define ZM_REC 36
 #endif
@@ -690,7 +705,7 @@ __global__ __launch_bounds__(64) ZM_WPE void k_spread_zsweep_mfma(
             const int dz = p.tsel - pch * ZC;
             const float2 cv = make_float2(cp.x * p.pv.x - cp.y * p.pv.y,
                                           cp.x * p.pv.y + cp.y * p.pv.x);
-            float4 *rec = reinterpret_cast<float4 *>(table + lane * MREC);
+            static_assert(MREC % 2 == 0, "table rows hold float2 pairs");
             constexpr float ih = 2.0f / W;
             const float sx = ((float)ox + p.fx) * ih, sy = ((float)oy + p.fy) * ih;
             const float sz = p.fz * ih;
@@ -704,14 +719,15 @@ __global__ __launch_bounds__(64) ZM_WPE void k_spread_zsweep_mfma(
                 wy[q] = ((unsigned)(q - oy) < (unsigned)W) ? ey : 0.f;
                 bz[q] = ((unsigned)(q - dz) < (unsigned)W) ? ez : 0.f;
             }
-            rec[0] = make_float4(wx[0], wx[4], wx[1], wx[5]);
-            rec[1] = make_float4(wx[2], wx[6], wx[3], wx[7]);
-            rec[2] = make_float4(wy[0], wy[4], wy[1], wy[5]);
-            rec[3] = make_float4(wy[2], wy[6], wy[3], wy[7]);
+            // row: wx pairs (wx[a], wx[a + 4]), wy pairs, then B[2s + ri]
+            float2 *rec2 = reinterpret_cast<float2 *>(table + lane * MREC);
 #pragma unroll
-            for (int q = 0; q < ZB; q += 2)
-                rec[4 + q / 2] = make_float4(cv.x * bz[q], cv.y * bz[q], cv.x * bz[q + 1],
-                                             cv.y * bz[q + 1]);
+            for (int a = 0; a < 4; ++a) {
+                rec2[a] = make_float2(wx[a], wx[a + 4]);
+                rec2[4 + a] = make_float2(wy[a], wy[a + 4]);
+            }
+#pragma unroll
+            for (int q = 0; q < ZB; ++q) rec2[8 + q] = make_float2(cv.x * bz[q], cv.y * bz[q]);
         }
         // each chunk's points: lanes [lo, lo + n) of the batch
         int nn[G], lo[G];
