@@ -666,13 +666,14 @@ __global__ __launch_bounds__(64) ZM_WPE void k_spread_zsweep_mfma(
 
     // Slots 0 .. ZC-1 are complete: stage the owned ones in the ring, then
     // shift every accumulator down by ZC slots.
+    // Cells leave the ring in whole groups of 4 z-cells from z0 (32-byte
+    // aligned runs of a column when z0 is a multiple of 4), so no sector is
+    // written twice; at most 3 cells wait, and with ZC <= 4 new ones the
+    // ring never holds more than 7.
+    static_assert(RING >= 3 + ZC, "store ring too small");
     auto advance = [&]() {
         const int lo = max(zb, z0), hi = min(zb + ZC, zend);
         if (lo < hi) {
-            if (hi - fz > RING) {
-                ring_flush(ring, grid, lane, fz, cz, z0, n1, n2, bx, by);
-                fz = cz;
-            }
             const int s = li >> 1, z = zb + s;
             if (s < ZC && z >= lo && z < hi) {
                 float *rf = reinterpret_cast<float *>(ring) + ((z - z0) & (RING - 1)) * 2 + (li & 1);
@@ -685,6 +686,11 @@ __global__ __launch_bounds__(64) ZM_WPE void k_spread_zsweep_mfma(
                     }
             }
             cz = hi;
+            const int f4 = z0 + ((cz - z0) & ~3);
+            if (f4 > fz) {
+                ring_flush(ring, grid, lane, fz, f4, z0, n1, n2, bx, by);
+                fz = f4;
+            }
         }
 #pragma unroll
         for (int q = 0; q < 4; ++q)
