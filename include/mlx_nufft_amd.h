@@ -193,6 +193,10 @@ int mn_spread_c128(const mn_bins *g, float beta, int64_t P, int64_t nsub,
  * >= k) with mn_zsweep_starts. The spread reads the sorted words and
  * fractions; strengths are c[perm[j]] (caller order), or c[j] when perm is
  * NULL (c already in sorted order); pre: optional sorted-order multiplier.
+ * mn_spread_zsweep runs the matrix-core kernel (one 16x16x4 f32 MFMA
+ * accumulator per 4x4 column quadrant holds the z-window); with the
+ * environment variable MN_ZSWEEP_KERNEL=valu it runs the per-lane register
+ * kernel, which gives the same grid within fp32 rounding.
  * ref: nd.py:152-165 (cells), nd.py:492-579 (output-driven spread),
  * nd.py:298-372 (bin sort).
  */
