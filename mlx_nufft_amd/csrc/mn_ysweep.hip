@@ -24,9 +24,16 @@
 // walk the list, each point costing 2*W FMAs per lane. Vectors of a batch
 // are independent rows of the launch grid.
 //
+// The cursor (mn_cursor.h) walks groups of two y-steps; batches take up to
+// 64 consecutive points of a group, with lists per y-step. Loads are issued
+// by every lane outside any branch and the batch loop is unrolled three
+// ways, so the words / fractions / perm of batch k + 2 and the strengths of
+// batch k + 1 are in flight while batch k is built and swept.
+//
 // ref: nd.py:492-579 (the reference's output-driven spread this replaces),
 // nd.py:683-742 (its batched spread), nd.py:298-372 (bin sort).
 #include "mn_common.h"
+#include "mn_cursor.h"
 
 namespace mn {
 namespace {
@@ -56,6 +63,63 @@ __device__ __forceinline__ void ys_store_stage(float2 (*stage)[64], float2 *__re
     }
 }
 
+constexpr int NRY = 2;  // key ranges per y: own block (both classes), -x neighbour (reaching)
+constexpr int YZ = 2;   // y-steps per cursor group
+constexpr int NQY = YZ * NRY;
+
+// The bounds of the key ranges (SweepCursor fetch): range i = (y-step i / 2,
+// source i % 2) of the group starting at yc. Source 0 is the block's own
+// points, keys (bx n1 + y) * 2 + {0, 1}; source 1 is the -x neighbour's
+// reaching points, key (bxm n1 + y) * 2 + 1. Every lane loads (key 0 for
+// lanes without a range), outside any branch.
+struct YFetch {
+    int bx, dbx, n1, yend, nq;  // dbx = bxm - bx (the source is chosen by arithmetic)
+    const int32_t *ystart;
+    __device__ __forceinline__ int2 operator()(int yc, int lane) const {
+        const int r = lane % NRY, y = yc + lane / NRY;
+        const bool ok = lane < nq && y < yend;
+        const int yy = y < 0 ? y + n1 : y;
+        const int64_t kb = ok ? ((int64_t)(bx + r * dbx) * n1 + yy) * 2 : 0;
+        const int st = ystart[kb + (ok ? r : 0)], en = ystart[kb + (ok ? 2 : 0)];
+        return make_int2(ok ? st : 0, ok ? en : 0);
+    }
+};
+
+// One lane's point of a batch, its loads issued (the strength, which needs
+// src, is gathered one batch later).
+struct YPoint {
+    int yc, nb;        // the batch's group and size (uniform; nb = 0: done)
+    bool valid;
+    int tsel, r;       // y-step within the group and source
+    uint32_t wd, src;  // sorted word; index of the strength in c
+    float fx, fy;
+};
+
+// The next batch, its loads issued by every lane (an idle lane reads element
+// 0) outside any branch, so the compiler can wait for exactly the loads a
+// later use needs.
+__device__ __forceinline__ YPoint yp_next(SweepCursor &k, const YFetch yf, int lane,
+                                          SweepRanges<NQY> &rg, uint8_t *qidx,
+                                          const uint32_t *__restrict__ perm,
+                                          const uint32_t *__restrict__ word,
+                                          const float *__restrict__ fx,
+                                          const float *__restrict__ fy) {
+    const SweepBatch sb = sweep_next<NQY, YZ>(k, yf.yend, rg, qidx, lane, yf);
+    YPoint q;
+    q.yc = sb.zc;
+    q.nb = sb.nb;
+    q.valid = sb.valid;
+    q.tsel = sb.valid ? sb.range / NRY : -1;
+    q.r = sb.range % NRY;
+    const uint32_t j = sb.j;
+    q.wd = word[j];
+    q.fx = fx[j];
+    q.fy = fy[j];
+    const uint32_t pj = (perm ? perm : word)[j];
+    q.src = perm ? pj : j;
+    return q;
+}
+
 template <int W>
 __global__ __launch_bounds__(64) void k_spread_ysweep(int n1, int nbx, int yseg, int nseg,
                                                       float bl2e, int64_t P,
@@ -67,8 +131,10 @@ __global__ __launch_bounds__(64) void k_spread_ysweep(int n1, int nbx, int yseg,
                                                       const float2 *__restrict__ c,
                                                       float2 *__restrict__ grid, int64_t gsz) {
     __shared__ __align__(16) float table[(64 + 1) * YREC];
-    __shared__ __align__(16) uint16_t lists[NG][64];
+    __shared__ __align__(16) uint16_t lists[YZ][NG][64];
     __shared__ float2 stage[YST][64];
+    __shared__ SweepRanges<NQY> rg;
+    __shared__ uint8_t qidx[64];
     constexpr uint32_t kPad = 64u * YREC * 4u;  // byte offset of the zero row
     const int vec = blockIdx.y;
     c += (int64_t)vec * P;
@@ -84,83 +150,89 @@ __global__ __launch_bounds__(64) void k_spread_ysweep(int n1, int nbx, int yseg,
 #pragma unroll
     for (int a = 0; a < W; ++a) wre[a] = wim[a] = 0.f;
     int yw = y0 - (W - 1);  // y of window cell 0
-    for (int y = y0 - (W - 1); y < yend; ++y) {
-        // window cell 0 moves to y (cell y - 1 is complete)
-        while (yw < y) {
-            if (yw >= y0)
-                ys_store_stage(stage, grid, lane, (yw - y0) % YST, yw, n1, bx, wre[0], wim[0],
-                               yw == yend - 1);
+
+    // Window cell 0 moves up by one: cell yw is complete (staged and stored
+    // if this segment owns it).
+    auto step = [&]() {
+        if (yw >= y0)
+            ys_store_stage(stage, grid, lane, (yw - y0) % YST, yw, n1, bx, wre[0], wim[0],
+                           yw == yend - 1);
 #pragma unroll
-            for (int a = 0; a < W - 1; ++a) {
-                wre[a] = wre[a + 1];
-                wim[a] = wim[a + 1];
-            }
-            wre[W - 1] = wim[W - 1] = 0.f;
-            ++yw;
+        for (int a = 0; a < W - 1; ++a) {
+            wre[a] = wre[a + 1];
+            wim[a] = wim[a + 1];
         }
-        const int yy = y < 0 ? y + n1 : y;
-        const int64_t k0 = ((int64_t)bx * n1 + yy) * 2, kn = ((int64_t)bxm * n1 + yy) * 2;
-        const int st0 = ystart[k0], cnt0 = ystart[k0 + 2] - st0;
-        const int st1 = ystart[kn + 1], cnt1 = ystart[kn + 2] - st1;
-        const int tot = cnt0 + cnt1;
-        for (int bat = 0; bat < tot; bat += 64) {
-            __syncthreads();
+        wre[W - 1] = wim[W - 1] = 0.f;
+        ++yw;
+    };
+
+    // Build and sweep one batch p whose strengths are cp.
+    auto process = [&](const YPoint &p, const float2 cp) __attribute__((always_inline)) {
+        __syncthreads();
 #pragma unroll
-            for (int k = 0; k < NG * 32; k += 64)
-                reinterpret_cast<uint32_t *>(lists)[k + lane] = kPad | (kPad << 16);
-            const int e = bat + lane;
-            const bool valid = e < tot;
-            int g0 = -1, touch2 = 0;
-            if (valid) {
-                const bool nb = e >= cnt0;
-                const uint32_t j = (uint32_t)(nb ? st1 + (e - cnt0) : st0 + e);
-                // first tap relative to this block (-64 for the -x neighbour's points)
-                const int ox = (int)(word[j] >> kYsKeyBits) - (nb ? YB : 0);
-                const float f0 = fx[j], f1 = fy[j];
-                const float2 cv = c[perm ? perm[j] : j];
-                g0 = max(ox, 0) / YG;
-                touch2 = (g0 + 1 < NG && YG * (g0 + 1) < ox + W) ? 1 : 0;
-                float *rec = table + lane * YREC;
-                constexpr float ih = 2.0f / W;
-                const float sx = ((float)(YG * g0 - ox) - f0) * ih, sy = f1 * ih;
-                float wy[8];
+        for (int k = 0; k < YZ * NG * 32; k += 64)
+            reinterpret_cast<uint32_t *>(lists)[k + lane] = kPad | (kPad << 16);
+        int g0 = -1, touch2 = 0;
+        if (p.valid) {
+            // first tap relative to this block (-64 for the -x neighbour's points)
+            const int ox = (int)(p.wd >> kYsKeyBits) - (p.r == 1 ? YB : 0);
+            g0 = max(ox, 0) / YG;
+            touch2 = (g0 + 1 < NG && YG * (g0 + 1) < ox + W) ? 1 : 0;
+            float *rec = table + lane * YREC;
+            constexpr float ih = 2.0f / W;
+            const float sx = ((float)(YG * g0 - ox) - p.fx) * ih, sy = p.fy * ih;
+            float wy[8];
 #pragma unroll
-                for (int a = 0; a < 8; ++a) wy[a] = a < W ? es_weight_z((float)a * ih - sy, bl2e) : 0.f;
+            for (int a = 0; a < 8; ++a) wy[a] = a < W ? es_weight_z((float)a * ih - sy, bl2e) : 0.f;
 #pragma unroll
-                for (int r = 0; r < 2; ++r) {
-                    float4 *run = reinterpret_cast<float4 *>(rec + r * YRUN);
+            for (int r = 0; r < 2; ++r) {
+                float4 *run = reinterpret_cast<float4 *>(rec + r * YRUN);
 #pragma unroll
-                    for (int q = 0; q < YG; q += 2) {
-                        // columns YG*g0 + s, s = YG*r + q (+1): tap s + YG*g0 - ox
-                        const int s = YG * r + q, a0 = YG * g0 + s - ox;
-                        const float e0 = es_weight_z((float)s * ih + sx, bl2e);
-                        const float e1 = es_weight_z((float)(s + 1) * ih + sx, bl2e);
-                        const float w0 = (unsigned)a0 < (unsigned)W ? e0 : 0.f;
-                        const float w1 = (unsigned)(a0 + 1) < (unsigned)W ? e1 : 0.f;
-                        run[q / 2] = make_float4(cv.x * w0, cv.y * w0, cv.x * w1, cv.y * w1);
-                    }
-                    run[4] = make_float4(wy[0], wy[1], wy[2], wy[3]);
-                    run[5] = make_float4(wy[4], wy[5], wy[6], wy[7]);
+                for (int q = 0; q < YG; q += 2) {
+                    // columns YG*g0 + s, s = YG*r + q (+1): tap s + YG*g0 - ox
+                    const int s = YG * r + q, a0 = YG * g0 + s - ox;
+                    const float e0 = es_weight_z((float)s * ih + sx, bl2e);
+                    const float e1 = es_weight_z((float)(s + 1) * ih + sx, bl2e);
+                    const float w0 = (unsigned)a0 < (unsigned)W ? e0 : 0.f;
+                    const float w1 = (unsigned)(a0 + 1) < (unsigned)W ? e1 : 0.f;
+                    run[q / 2] = make_float4(cp.x * w0, cp.y * w0, cp.x * w1, cp.y * w1);
                 }
+                run[4] = make_float4(wy[0], wy[1], wy[2], wy[3]);
+                run[5] = make_float4(wy[4], wy[5], wy[6], wy[7]);
             }
-            // per group: the batch runs that touch it, in order
-            int cnt[NG];
+        }
+        // per y-step and group: the batch runs that touch it, in order
+        int cnt[YZ][NG];
+#pragma unroll
+        for (int t = 0; t < YZ; ++t)
 #pragma unroll
             for (int q = 0; q < NG; ++q) {
-                const bool first = valid && q == g0;
-                const bool second = valid && touch2 && q == g0 + 1;
+                const bool mine = p.tsel == t;
+                const bool first = mine && q == g0;
+                const bool second = mine && touch2 && q == g0 + 1;
                 const uint64_t bq = __ballot(first || second);
-                cnt[q] = __popcll(bq);
+                cnt[t][q] = __popcll(bq);
                 if (first || second)
-                    lists[q][__popcll(bq & lt_mask)] =
+                    lists[t][q][__popcll(bq & lt_mask)] =
                         (uint16_t)(lane * YREC * 4 + (second ? YRUN * 4 : 0));
             }
-            __syncthreads();
-            int nit = cnt[0];
+        __syncthreads();
+        const char *tb = reinterpret_cast<const char *>(table);
 #pragma unroll
-            for (int q = 1; q < NG; ++q) nit = max(nit, cnt[q]);
-            const uint16_t *lq = lists[grp];
-            const char *tb = reinterpret_cast<const char *>(table);
+        for (int t = 0; t < YZ; ++t) {
+            int nit = cnt[t][0];
+#pragma unroll
+            for (int q = 1; q < NG; ++q) nit = max(nit, cnt[t][q]);
+            if (nit == 0) continue;
+            // the window moves to this step's y: usually one cell, as
+            // straight-line code (a loop that stores makes the compiler wait
+            // for every outstanding load before it)
+            const int yt = p.yc + t;
+            if (yw < yt) {
+                step();
+                while (yw < yt) step();
+            }
+            const uint16_t *lq = lists[t][grp];
             for (int it = 0; it < nit; ++it) {
                 const char *run = tb + lq[it];
                 const float2 v = *reinterpret_cast<const float2 *>(run + 8 * slot);
@@ -177,19 +249,36 @@ __global__ __launch_bounds__(64) void k_spread_ysweep(int n1, int nbx, int yseg,
                 }
             }
         }
+    };
+
+    // The batch loop, unrolled three ways with rotating names (A, B, C) so
+    // that no register still being loaded is copied (a copy would wait for
+    // it): each stage issues the loads of the batch two ahead, gathers the
+    // strengths of the next one, then builds and sweeps the current one.
+    const YFetch yf{bx, bxm - bx, n1, yend, NQY, ystart};
+    SweepCursor cur;
+    cur.pzc = INT32_MIN;
+    sweep_load<NQY, YZ>(cur, y0 - (W - 1), rg, lane, yf);
+    YPoint pa = yp_next(cur, yf, lane, rg, qidx, perm, word, fx, fy);
+    float2 ca = c[pa.src];  // idle lanes read c[perm[0]]: their rows are never used
+    YPoint pb = yp_next(cur, yf, lane, rg, qidx, perm, word, fx, fy);
+    YPoint pc;
+    float2 cb, cc;
+    for (;;) {
+        if (pa.nb == 0) break;
+        pc = yp_next(cur, yf, lane, rg, qidx, perm, word, fx, fy);
+        cb = c[pb.src];
+        process(pa, ca);
+        if (pb.nb == 0) break;
+        pa = yp_next(cur, yf, lane, rg, qidx, perm, word, fx, fy);
+        cc = c[pc.src];
+        process(pb, cb);
+        if (pc.nb == 0) break;
+        pb = yp_next(cur, yf, lane, rg, qidx, perm, word, fx, fy);
+        ca = c[pa.src];
+        process(pc, cc);
     }
-    while (yw < yend) {  // drain the window up to the segment end
-        if (yw >= y0)
-            ys_store_stage(stage, grid, lane, (yw - y0) % YST, yw, n1, bx, wre[0], wim[0],
-                           yw == yend - 1);
-#pragma unroll
-        for (int a = 0; a < W - 1; ++a) {
-            wre[a] = wre[a + 1];
-            wim[a] = wim[a + 1];
-        }
-        wre[W - 1] = wim[W - 1] = 0.f;
-        ++yw;
-    }
+    while (yw < yend) step();  // drain the window up to the segment end
 }
 
 struct YsArgs {

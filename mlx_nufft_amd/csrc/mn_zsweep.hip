@@ -42,6 +42,7 @@
 #include <cstring>
 
 #include "mn_common.h"
+#include "mn_cursor.h"
 
 namespace mn {
 namespace {
@@ -237,126 +238,45 @@ __device__ __forceinline__ ZPoint zp_issue(ZCursor &k, const ZBlocks b, int lane
     return q;
 }
 
-// A cursor that prefetches: while the wave works through group zc, the raw
-// zstart bounds of group pzc = zc + ZC are already loading into nst / nen
-// (lane i < ZC * NR: range i of that group), so moving to the next group does
-// not wait for memory.
-struct ZCursorP {
-    int zc, bat, tot;  // as ZCursor
-    int pzc;           // group whose bounds are in nst / nen
-    int nst, nen;      // this lane's range of group pzc: sorted [nst, nen)
+// The bounds of the MFMA kernel's key ranges (SweepCursor fetch): range
+// i = (z-step i / NR, source i % NR) of the group starting at zc. Every lane
+// loads (key 0 for lanes without a range), outside any branch.
+struct ZFetch {
+    int bx, by, dbx, dby, nby, n2, zend, nq;  // dbx = bxm - bx, dby = bym - by
+    const int32_t *zstart;
+    __device__ __forceinline__ int2 operator()(int zc, int lane) const {
+        const int r = lane % NR, z = zc + lane / NR;
+        const bool ok = lane < nq && z < zend;
+        const int zz = z < 0 ? z + n2 : z;
+        // source r: bit 0 = -x neighbour, bit 1 = -y neighbour (chosen by
+        // arithmetic: a lane-dependent choice between two fields would put
+        // the object in scratch); its key classes [lo, hi] are those that
+        // reach this block
+        const int blk = (bx + (r & 1) * dbx) * nby + (by + ((r >> 1) & 1) * dby);
+        const int lo = r == 0 ? 0 : (r == 2 ? 1 : 2), hi = (r & 2) ? 2 : 3;
+        const int64_t kb = ok ? ((int64_t)blk * n2 + zz) * 4 : 0;
+        const int st = zstart[kb + (ok ? lo : 0)], en = zstart[kb + (ok ? hi + 1 : 0)];
+        return make_int2(ok ? st : 0, ok ? en : 0);
+    }
 };
 
-template <int ZC>
-__device__ __forceinline__ void zcp_fetch(ZCursorP &k, int zc, const ZBlocks b,
-                                          const int32_t *__restrict__ zstart, int lane) {
-    k.pzc = zc;
-    const int r = lane % NR, z = zc + lane / NR;
-    const bool ok = lane < ZC * NR && z < b.zend;
-    const int zz = z < 0 ? z + b.n2 : z;
-    // source r: bit 0 = -x neighbour, bit 1 = -y neighbour; its key classes
-    // [lo, hi] are those that reach this block
-    const int blk = ((r & 1) ? b.bxm : b.bx) * b.nby + ((r & 2) ? b.bym : b.by);
-    const int lo = r == 0 ? 0 : (r == 2 ? 1 : 2), hi = (r & 2) ? 2 : 3;
-    const int64_t kb = ok ? ((int64_t)blk * b.n2 + zz) * 4 : 0;
-    // loads by every lane (key 0 for the others), outside any branch
-    const int st = zstart[kb + (ok ? lo : 0)], en = zstart[kb + (ok ? hi + 1 : 0)];
-    k.nst = ok ? st : 0;
-    k.nen = ok ? en : 0;
-}
-
-// Make group zc current (its ranges into rg, as zc_load) and start loading
-// the bounds of the group after it.
-template <int ZC>
-__device__ __forceinline__ void zcp_load(ZCursorP &k, int zc, const ZBlocks b,
-                                         const int32_t *__restrict__ zstart, ZRanges<ZC> &rg,
-                                         int lane) {
-    if (k.pzc != zc) zcp_fetch<ZC>(k, zc, b, zstart, lane);
-    const int st = k.nst, cnt = k.nen - k.nst;
-    k.zc = zc;
-    k.bat = 0;
-    int incl = cnt;
-#pragma unroll
-    for (int d = 1; d < ZC * NR; d <<= 1) {
-        const int v = __shfl_up(incl, d, 64);
-        incl += (lane >= d) ? v : 0;
-    }
-    __syncthreads();  // earlier reads of rg are done
-    if (lane < ZC * NR) {
-        rg.pf[lane] = incl - cnt;
-        rg.dj[lane] = st - (incl - cnt);
-    }
-    k.tot = __shfl(incl, ZC * NR - 1, 64);
-    // the next group's bounds load only now, after this group's were used,
-    // so using them never waits on the new loads
-    zcp_fetch<ZC>(k, zc + ZC, b, zstart, lane);
-}
-
-template <int ZC>
-__device__ __forceinline__ void zcp_settle(ZCursorP &k, const ZBlocks b,
-                                           const int32_t *__restrict__ zstart, ZRanges<ZC> &rg,
-                                           int lane) {
-    // the usual single step is straight-line code; only a run of empty
-    // groups loops (a loop makes the compiler wait for every load first)
-    if (k.bat >= k.tot && k.zc < b.zend) {
-        zcp_load<ZC>(k, k.zc + ZC, b, zstart, rg, lane);
-        while (k.bat >= k.tot && k.zc < b.zend) zcp_load<ZC>(k, k.zc + ZC, b, zstart, rg, lane);
-    }
-}
-
-// zp_issue with the range of each element found from ballots of the range
-// starts instead of one compare per range, so its cost and registers do not
-// grow with the number of ranges: lane j takes the last non-empty range that
-// starts at a batch element in (0, j] (marked in qidx by element, so that a
-// ballot of the marks is a mask over elements), else the one holding bat.
-template <int ZC, bool PRE>
-__device__ __forceinline__ ZPoint zp_issue_mask(ZCursorP &k, const ZBlocks b, int lane,
-                                                const int32_t *__restrict__ zstart,
-                                                ZRanges<ZC> &rg, uint8_t *qidx,
-                                                const uint32_t *__restrict__ perm,
-                                                const uint32_t *__restrict__ word, const CF3s &frs,
-                                                const float2 *__restrict__ pre) {
-    constexpr int NQ = ZC * NR;
-    // settle here rather than after the previous batch's loads were issued,
-    // so a group change never waits on loads that are not needed yet
-    zcp_settle<ZC>(k, b, zstart, rg, lane);
+// The next batch of the MFMA kernel, its point loads issued by every lane
+// (an idle lane reads element 0) outside any branch, so the compiler can
+// wait for exactly the loads a later use needs.
+template <int ZG, bool PRE>
+__device__ __forceinline__ ZPoint zp_next(SweepCursor &k, const ZFetch zf, int lane,
+                                          SweepRanges<ZG * NR> &rg, uint8_t *qidx,
+                                          const uint32_t *__restrict__ perm,
+                                          const uint32_t *__restrict__ word, const CF3s &frs,
+                                          const float2 *__restrict__ pre) {
+    const SweepBatch sb = sweep_next<ZG * NR, ZG>(k, zf.zend, rg, qidx, lane, zf);
     ZPoint q;
-    q.zc = k.zc;
-    q.nb = k.zc < b.zend ? min(64, k.tot - k.bat) : 0;
-    q.valid = lane < q.nb;
-    q.tsel = -1;
-    q.r = 0;
-    uint32_t j = 0;  // sorted index of this lane's point (0 for an idle lane)
-    if (q.nb > 0) {
-        __syncthreads();  // the ranges written by zcp_load are visible
-        int d = 0;
-        bool ne = false;
-        if (lane < NQ) {
-            const int st = rg.pf[lane];
-            ne = (lane + 1 < NQ ? rg.pf[lane + 1] : k.tot) > st;
-            d = st - k.bat;
-        }
-        // non-empty ranges starting at or before bat (ballot bit = range
-        // index); the last holds bat (bat < tot, so there is one)
-        const uint64_t mbefore = __ballot(ne && d <= 0);
-        const int q0 = 63 - __clzll(mbefore);
-        // qidx[d] = the range starting at batch element d (0xff: none), and
-        // mpos bit d set where one starts (ballot bit = element)
-        qidx[lane] = 0xff;
-        __syncthreads();
-        if (ne && d > 0 && d < 64) qidx[d] = (uint8_t)lane;
-        __syncthreads();
-        const uint64_t mpos = __ballot(qidx[lane] != 0xff);
-        const uint64_t m = mpos & (lane == 63 ? ~0ull : ((2ull << lane) - 1));
-        const int i = m ? (int)qidx[63 - __clzll(m)] : q0;
-        const uint32_t jv = (uint32_t)(k.bat + lane + rg.dj[i]);
-        q.tsel = q.valid ? i / NR : -1;
-        q.r = i % NR;
-        j = q.valid ? jv : 0u;
-    }
-    // The loads are issued by every lane (an idle lane reads element 0,
-    // P >= 1), outside any branch, so the compiler can wait for exactly the
-    // loads a later use needs and the batches overlap.
+    q.zc = sb.zc;
+    q.nb = sb.nb;
+    q.valid = sb.valid;
+    q.tsel = sb.valid ? sb.range / NR : -1;
+    q.r = sb.range % NR;
+    const uint32_t j = sb.j;
     q.wd = word[j];
     q.fx = frs.p[0][j];
     q.fy = frs.p[1][j];
@@ -367,7 +287,6 @@ __device__ __forceinline__ ZPoint zp_issue_mask(ZCursorP &k, const ZBlocks b, in
         q.pv = pre[j];
     else
         q.pv = make_float2(1.f, 0.f);
-    if (k.zc < b.zend) k.bat += 64;
     return q;
 }
 
@@ -637,7 +556,7 @@ __global__ __launch_bounds__(64) ZM_WPE void k_spread_zsweep_mfma(
     static_assert(ZC + W - 1 <= 8 && ZC <= RING, "chunk footprint exceeds the 8 slots");
     __shared__ __align__(16) float table[(64 + 1) * MREC];
     __shared__ __align__(16) float2 ring[64 * RING];
-    __shared__ ZRanges<ZG> rg;
+    __shared__ SweepRanges<ZG * NR> rg;
     __shared__ uint8_t qidx[64];
     constexpr uint32_t kPad = 64u * MREC * 4u;  // byte offset of the zero row
     const int64_t nw = (int64_t)nbx * nby * nseg;
@@ -789,25 +708,26 @@ __global__ __launch_bounds__(64) ZM_WPE void k_spread_zsweep_mfma(
     // that no register still being loaded is copied (a copy would wait for
     // it): each stage issues the loads of the batch two ahead, gathers the
     // strengths of the next one, then builds and sweeps the current one.
-    ZCursorP cur;
+    const ZFetch zf{bk.bx, bk.by, bk.bxm - bk.bx, bk.bym - bk.by, nby, n2, zend, ZG * NR, zstart};
+    SweepCursor cur;
     cur.pzc = INT32_MIN;
-    zcp_load<ZG>(cur, z0 - (W - 1), bk, zstart, rg, lane);
-    ZPoint pa = zp_issue_mask<ZG, PRE>(cur, bk, lane, zstart, rg, qidx, perm, word, frs, pre);
+    sweep_load<ZG * NR, ZG>(cur, z0 - (W - 1), rg, lane, zf);
+    ZPoint pa = zp_next<ZG, PRE>(cur, zf, lane, rg, qidx, perm, word, frs, pre);
     float2 ca = c[pa.src];  // idle lanes read c[perm[0]]: their rows are never used
-    ZPoint pb = zp_issue_mask<ZG, PRE>(cur, bk, lane, zstart, rg, qidx, perm, word, frs, pre);
+    ZPoint pb = zp_next<ZG, PRE>(cur, zf, lane, rg, qidx, perm, word, frs, pre);
     ZPoint pc;
     float2 cb, cc;
     for (;;) {
         if (pa.nb == 0) break;
-        pc = zp_issue_mask<ZG, PRE>(cur, bk, lane, zstart, rg, qidx, perm, word, frs, pre);
+        pc = zp_next<ZG, PRE>(cur, zf, lane, rg, qidx, perm, word, frs, pre);
         cb = c[pb.src];
         process(pa, ca);
         if (pb.nb == 0) break;
-        pa = zp_issue_mask<ZG, PRE>(cur, bk, lane, zstart, rg, qidx, perm, word, frs, pre);
+        pa = zp_next<ZG, PRE>(cur, zf, lane, rg, qidx, perm, word, frs, pre);
         cc = c[pc.src];
         process(pb, cb);
         if (pc.nb == 0) break;
-        pb = zp_issue_mask<ZG, PRE>(cur, bk, lane, zstart, rg, qidx, perm, word, frs, pre);
+        pb = zp_next<ZG, PRE>(cur, zf, lane, rg, qidx, perm, word, frs, pre);
         ca = c[pa.src];
         process(pc, cc);
     }
