@@ -482,6 +482,13 @@ __global__ __launch_bounds__(64) void k_spread_zsweep(int n0, int n1, int n2, in
 // B[l / 16][l % 16] and holds D[4 (l / 16) + r][l % 16] in element r. Every
 // point costs 4 MFMAs / 4 and the lane 3 LDS reads and 4 MULs per K-step.
 //
+// For W <= ZM_F16_MAXW (6) the products run on the fp16 matrix path
+// instead: K-steps of 16 points with v_mfma_f32_16x16x16f16, each f32
+// operand split into fp16 hi + lo and the product taken as hi*hi' + hi*lo'
+// + lo*hi' (about 2^-20 relative). On gfx950 f32 MFMAs and VALU
+// instructions from waves sharing a SIMD do not overlap, but fp16 MFMAs
+// mostly do, and they retire about 17x the MACs per cycle.
+//
 // When the sweep passes a chunk, its slots 0 .. ZC-1 are complete: they go
 // to an LDS ring of RING z-cells per column (flushed as runs along z) and
 // every accumulator register shifts down by ZC slots (2 ZC lanes) with one
@@ -541,6 +548,24 @@ __device__ __forceinline__ void ring_flush(const float2 *ring, float2 *__restric
 }
 
 typedef float mf4 __attribute__((ext_vector_type(4)));
+typedef _Float16 mh4 __attribute__((ext_vector_type(4)));
+
+// Widths up to ZM_F16_MAXW sweep with fp16 matrix products (below).
+#ifndef ZM_F16_MAXW
+#define ZM_F16_MAXW 6
+#endif
+
+// x = hi + lo with hi = x cut to fp16's 10 stored mantissa bits (exact in
+// fp16 for |x| in its normal range, so every conversion path gives the same
+// hi) and lo = fp16(x - hi), where x - hi is exact in fp32: about 21
+// significant bits, so hi*hi' + hi*lo' + lo*hi' carries a product to about
+// 2^-20. (Rounding hi instead lets the compiler derive the hi in lo and the hi
+// fed to the MFMA by different roundings, which can differ by a whole ulp.)
+__device__ __forceinline__ void split_f16(float x, _Float16 &hi, _Float16 &lo) {
+    const float h = __int_as_float(__float_as_int(x) & 0xffffe000);
+    hi = (_Float16)h;
+    lo = (_Float16)(x - h);
+}
 
 #ifndef ZM_OCC
 #define ZM_OCC 3
@@ -554,6 +579,16 @@ __global__ __launch_bounds__(64) ZM_WPE void k_spread_zsweep_mfma(
     const float2 *__restrict__ pre, float2 *__restrict__ grid) {
     constexpr int ZC = mfma_chunk<W>(), G = mfma_group<W>(), ZG = ZC * G;
     static_assert(ZC + W - 1 <= 8 && ZC <= RING, "chunk footprint exceeds the 8 slots");
+    // fp16 products: A = wx wy is stored scaled by 2^14 (2^7 per axis) and
+    // B = strength x wz by 2^sexp, a power of two per wave chosen so that
+    // |B| < 2^14, which keeps both inside fp16's normal range; the
+    // accumulators hold the grid times 2^(14 + sexp) and cells are scaled
+    // back when they leave the window.
+    constexpr bool F16 = W <= ZM_F16_MAXW;
+    constexpr float kAxisScale = F16 ? 128.0f : 1.0f;
+    int sexp = INT32_MIN;  // unset until the first batch with a nonzero strength
+    float unscale = 1.0f;  // 2^-(14 + sexp)
+    float bscale = 1.0f;   // 2^sexp
     __shared__ __align__(16) float table[(64 + 1) * MREC];
     __shared__ __align__(16) float2 ring[64 * RING];
     __shared__ SweepRanges<ZG * NR> rg;
@@ -601,7 +636,7 @@ __global__ __launch_bounds__(64) ZM_WPE void k_spread_zsweep_mfma(
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const int col = (4 * (q >> 1) + lk) * ZB + 4 * (q & 1) + r;
-                        rf[col * RING * 2] = acc[q][r];
+                        rf[col * RING * 2] = acc[q][r] * unscale;
                     }
             }
             cz = hi;
@@ -622,14 +657,36 @@ __global__ __launch_bounds__(64) ZM_WPE void k_spread_zsweep_mfma(
     auto process = [&](const ZPoint &p, const float2 cp) __attribute__((always_inline)) {
         const int pch = p.tsel / ZC;  // the point's chunk in the group
         __syncthreads();
+        const float2 cv = p.valid ? make_float2(cp.x * p.pv.x - cp.y * p.pv.y,
+                                                cp.x * p.pv.y + cp.y * p.pv.x)
+                                  : make_float2(0.f, 0.f);
+        if constexpr (F16) {
+            // the batch's largest strength is below 2^e
+            const float mx = fmaxf(fabsf(cv.x), fabsf(cv.y));
+            int e = ((__float_as_int(mx) >> 23) & 0xff) - 126;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) e = max(e, __shfl_xor(e, off, 64));
+            const int want = min(max(14 - e, -100), 100);
+            if (sexp == INT32_MIN || want < sexp) {
+                if (sexp != INT32_MIN) {
+                    // a larger strength than before: rescale what is held
+                    const float f = __builtin_amdgcn_ldexpf(1.0f, want - sexp);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) acc[q][r] *= f;
+                }
+                sexp = want;
+                bscale = __builtin_amdgcn_ldexpf(1.0f, sexp);
+                unscale = __builtin_amdgcn_ldexpf(1.0f, -14 - sexp);
+            }
+        }
         if (p.valid) {
             // first tap relative to this block (minus 8 for points of the -x
             // / -y neighbour blocks) and its slot in the chunk
             const int ox = (int)((p.wd >> kZsKeyBits) & 7u) - ((p.r & 1) ? ZB : 0);
             const int oy = (int)((p.wd >> (kZsKeyBits + 3)) & 7u) - ((p.r & 2) ? ZB : 0);
             const int dz = p.tsel - pch * ZC;
-            const float2 cv = make_float2(cp.x * p.pv.x - cp.y * p.pv.y,
-                                          cp.x * p.pv.y + cp.y * p.pv.x);
             static_assert(MREC % 2 == 0, "table rows hold float2 pairs");
             constexpr float ih = 2.0f / W;
             const float sx = ((float)ox + p.fx) * ih, sy = ((float)oy + p.fy) * ih;
@@ -648,11 +705,12 @@ __global__ __launch_bounds__(64) ZM_WPE void k_spread_zsweep_mfma(
             float2 *rec2 = reinterpret_cast<float2 *>(table + lane * MREC);
 #pragma unroll
             for (int a = 0; a < 4; ++a) {
-                rec2[a] = make_float2(wx[a], wx[a + 4]);
-                rec2[4 + a] = make_float2(wy[a], wy[a + 4]);
+                rec2[a] = make_float2(wx[a] * kAxisScale, wx[a + 4] * kAxisScale);
+                rec2[4 + a] = make_float2(wy[a] * kAxisScale, wy[a + 4] * kAxisScale);
             }
+            const float2 cb = make_float2(cv.x * bscale, cv.y * bscale);
 #pragma unroll
-            for (int q = 0; q < ZB; ++q) rec2[8 + q] = make_float2(cv.x * bz[q], cv.y * bz[q]);
+            for (int q = 0; q < ZB; ++q) rec2[8 + q] = make_float2(cb.x * bz[q], cb.y * bz[q]);
         }
         // each chunk's points: lanes [lo, lo + n) of the batch
         int nn[G], lo[G];
@@ -680,26 +738,61 @@ __global__ __launch_bounds__(64) ZM_WPE void k_spread_zsweep_mfma(
                     while (zb < zt) advance();
                 }
             }
-            for (int e0 = 0; e0 < n; e0 += 4 * KUNR) {
-                float av[KUNR][4], bv[KUNR];
+            if constexpr (F16) {
+                // K-steps of 16 points: lane group lk supplies points
+                // 4 lk .. 4 lk + 3 of the step (A[i][k], B[k][j] for
+                // k = 4 lk + t), each product as hi*hi + hi*lo + lo*hi
+                for (int e0 = 0; e0 < n; e0 += 16) {
+                    mh4 ah[4], al[4], bh, bl;
 #pragma unroll
-                for (int u = 0; u < KUNR; ++u) {
-                    const int e = e0 + 4 * u + lk;
-                    const uint32_t rb = e < n ? (uint32_t)(lo[ch] + e) * (MREC * 4u) : kPad;
-                    const float2 px = *reinterpret_cast<const float2 *>(tb + rb + xo);
-                    const float2 py = *reinterpret_cast<const float2 *>(tb + rb + yo);
-                    bv[u] = *reinterpret_cast<const float *>(tb + rb + bo);
-                    av[u][0] = px.x * py.x;  // q = 0: (qx, qy) = (0, 0)
-                    av[u][1] = px.x * py.y;  // q = 1: (0, 1)
-                    av[u][2] = px.y * py.x;  // q = 2: (1, 0)
-                    av[u][3] = px.y * py.y;  // q = 3: (1, 1)
+                    for (int t = 0; t < 4; ++t) {
+                        const int e = e0 + 4 * lk + t;
+                        const uint32_t rb = e < n ? (uint32_t)(lo[ch] + e) * (MREC * 4u) : kPad;
+                        const float2 px = *reinterpret_cast<const float2 *>(tb + rb + xo);
+                        const float2 py = *reinterpret_cast<const float2 *>(tb + rb + yo);
+                        const float bv = *reinterpret_cast<const float *>(tb + rb + bo);
+                        const float a4[4] = {px.x * py.x, px.x * py.y, px.y * py.x, px.y * py.y};
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            _Float16 h, l;
+                            split_f16(a4[q], h, l);
+                            ah[q][t] = h;
+                            al[q][t] = l;
+                        }
+                        _Float16 h, l;
+                        split_f16(bv, h, l);
+                        bh[t] = h;
+                        bl[t] = l;
+                    }
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        acc[q] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah[q], bh, acc[q], 0, 0, 0);
+                        acc[q] = __builtin_amdgcn_mfma_f32_16x16x16f16(ah[q], bl, acc[q], 0, 0, 0);
+                        acc[q] = __builtin_amdgcn_mfma_f32_16x16x16f16(al[q], bh, acc[q], 0, 0, 0);
+                    }
                 }
-#pragma unroll
-                for (int u = 0; u < KUNR; ++u)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u][q], bv[u], acc[q],
-                                                                      0, 0, 0);
+            } else {
+                for (int e0 = 0; e0 < n; e0 += 4 * KUNR) {
+                    float av[KUNR][4], bv[KUNR];
+    #pragma unroll
+                    for (int u = 0; u < KUNR; ++u) {
+                        const int e = e0 + 4 * u + lk;
+                        const uint32_t rb = e < n ? (uint32_t)(lo[ch] + e) * (MREC * 4u) : kPad;
+                        const float2 px = *reinterpret_cast<const float2 *>(tb + rb + xo);
+                        const float2 py = *reinterpret_cast<const float2 *>(tb + rb + yo);
+                        bv[u] = *reinterpret_cast<const float *>(tb + rb + bo);
+                        av[u][0] = px.x * py.x;  // q = 0: (qx, qy) = (0, 0)
+                        av[u][1] = px.x * py.y;  // q = 1: (0, 1)
+                        av[u][2] = px.y * py.x;  // q = 2: (1, 0)
+                        av[u][3] = px.y * py.y;  // q = 3: (1, 1)
+                    }
+    #pragma unroll
+                    for (int u = 0; u < KUNR; ++u)
+    #pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u][q], bv[u], acc[q],
+                                                                          0, 0, 0);
+                }
             }
         }
     };
