@@ -177,3 +177,40 @@ def test_zsweep_mfma_equals_valu(N, eps, mn, monkeypatch):
         rel = float((g - ref).abs().norm() / ref.abs().norm())
         print(f"  {key}: rel diff {rel:.2e}")
         assert rel < 1e-6, key
+
+
+@pytest.mark.parametrize("case", ["tiny", "huge", "mixed", "sparse"])
+def test_zsweep_mfma_strength_range(case, mn, monkeypatch):
+    """The fp16 product path scales strengths per wave by a power of two
+    (rescaling what it holds when a batch brings a larger one): strengths
+    at 1e-30 and 1e30, a mix where 1 % of the points are 1e8 times larger,
+    and mostly-zero strengths (whole batches of zeros) all give the
+    register kernel's grid, finite, within 1e-6."""
+    from mlx_nufft_amd import _engine as E
+
+    print(f"case zsweep strength range {case}", flush=True)
+    rng = np.random.default_rng(28)
+    M = 120_000
+    x = [rng.uniform(-np.pi, np.pi, M) for _ in range(3)]
+    c = rng.standard_normal(M) + 1j * rng.standard_normal(M)
+    if case == "tiny":
+        c *= 1e-30
+    elif case == "huge":
+        c *= 1e30
+    elif case == "mixed":
+        c[rng.random(M) < 0.01] *= 1e8
+    else:
+        c[rng.random(M) < 0.98] = 0
+    cd = torch.from_numpy(c.astype(np.complex64)).cuda()
+    p = mn.Type1PlanND(tuple(x), (64, 64, 48), eps=1e-5)
+    assert p.pts.kind == "zsweep" and p.w == 6
+    grids = {}
+    for kernel in KERNELS:
+        monkeypatch.setenv("MN_ZSWEEP_KERNEL", kernel)
+        g = torch.empty(p.n_up, dtype=torch.complex64, device="cuda")
+        E.spread_zsweep(p.pts, p.beta, cd, g)
+        assert bool(torch.isfinite(torch.view_as_real(g)).all()), kernel
+        grids[kernel] = g.to(torch.complex128)
+    rel = float((grids["mfma"] - grids["valu"]).abs().norm() / grids["valu"].abs().norm())
+    print(f"  rel diff {rel:.2e}")
+    assert rel < 1e-6
