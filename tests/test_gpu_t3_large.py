@@ -1,0 +1,108 @@
+"""GPU checks of type-3 on large anisotropic grids and of type-3 execute_batch.
+
+The geometry is the reference's anisotropic type-3 generator
+(ref: harness/gen.py:15-51): two wide source axes reaching ~1e7, a thin third
+axis, and an N x N target lattice whose third coordinate is a quadratic form
+of the first two. It makes type-3 fine grids that are thousands of cells wide
+on two axes and tens on the third. The cases and the 1e-4 gate follow
+ref: harness/test_large_t3_batch.py:68-140:
+
+* single execute at n_up = (7200, 7200, 24), about 1.24e9 cells;
+* single execute at n_up = (10800, 10800, 24), 2.8e9 cells: every grid index
+  on the path is past 2^31;
+* execute_batch with three channels at n_up = (2700, 2700, 24) and at
+  (7200, 7200, 24), each channel against its own direct sum.
+
+Every result is checked against the oracle's exact fp64 direct sum on a
+random target subset. The plan's grid sizes are checked against the sizes
+the reference's test quotes for the same geometry.
+"""
+
+import gc
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+GATE = 1e-4
+
+
+def gen_anisotropic(N, P, lat, seed=0):
+    """ref: harness/gen.py:15-51 (same constants and draws, same order)."""
+    rng = np.random.default_rng(seed)
+    s0 = 520e-9
+    k0 = 2.0 * np.pi / s0
+    A = 7.17e-4
+    u = rng.uniform(-lat, lat, P)
+    v = rng.uniform(-lat, lat, P)
+    d = rng.uniform(1.2, 6.0, P)
+    tau = 1.0 / d
+    amp = rng.uniform(0.2, 1.0, P)
+    th = rng.uniform(0, 2 * np.pi, P)
+    c = (amp * np.exp(1j * th) / (1j * s0 * d)
+         * np.exp(1j * 0.5 * k0 * tau * (u * u + v * v))).astype(np.complex128)
+    x = (-k0 * tau * v, -k0 * tau * u, 0.5 * k0 * tau)
+    r = (np.arange(N) - N / 2) * (A / N)
+    GY, GX = np.meshgrid(r, r, indexing="ij")
+    s = (GY.ravel(), GX.ravel(), (GX * GX + GY * GY).ravel())
+    return x, c, s
+
+
+def _release(mn):
+    from mlx_nufft_amd import _lib as L
+
+    gc.collect()
+    torch.cuda.synchronize()
+    L.check(L.lib().mn_fft_cache_clear(), "fft cache clear")
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("lat,n_up", [(2.0, [7200, 7200, 24]), (3.0, [10800, 10800, 24])])
+def test_t3_large_grid_execute(lat, n_up, oracle, mn):
+    print(f"case t3 large grid lat={lat}", flush=True)
+    x, c, s = gen_anisotropic(1024, 40_000, lat)
+    plan = mn.Type3Plan(x, s, eps=1e-5, isign=+1, prec="crit64")
+    try:
+        assert list(plan.n_up) == n_up
+        cells = int(np.prod(plan.n_up))
+        print(f"  n_up={plan.n_up} cells={cells:.3e} ({cells / 2**31:.2f} x 2^31)", flush=True)
+        f, times = plan.execute_profiled(c)
+        print("  stages ms: " + ", ".join(f"{k}={v * 1e3:.2f}" for k, v in times.items()),
+              flush=True)
+        idx = np.random.default_rng(5).choice(s[0].size, 4000, replace=False)
+        fd = oracle.dft_t3(x, c, s, +1, idx=idx)
+        err = oracle.rel_l2(np.asarray(f)[idx], fd)
+        print(f"  rel_l2={err:.3e} (gate {GATE:.0e})", flush=True)
+        assert err <= GATE
+    finally:
+        del plan
+        _release(mn)
+
+
+@pytest.mark.parametrize("lat,P,n_up", [(0.75, 100_000, [2700, 2700, 24]),
+                                        (2.0, 40_000, [7200, 7200, 24])])
+def test_t3_large_execute_batch(lat, P, n_up, oracle, mn):
+    print(f"case t3 execute_batch lat={lat} P={P}", flush=True)
+    x, c, s = gen_anisotropic(1024, P, lat)
+    rng = np.random.default_rng(6)
+    cs = np.stack([c, c * (0.5 + 0.5j),
+                   rng.standard_normal(c.size) + 1j * rng.standard_normal(c.size)])
+    plan = mn.Type3Plan(x, s, eps=1e-5, isign=+1, prec="crit64")
+    try:
+        assert list(plan.n_up) == n_up
+        fb = np.asarray(plan.execute_batch(cs.astype(np.complex64)))
+        assert fb.shape == (3, s[0].size)
+        idx = rng.choice(s[0].size, 3000, replace=False)
+        for ch in range(3):
+            fd = oracle.dft_t3(x, cs[ch], s, +1, idx=idx)
+            err = oracle.rel_l2(fb[ch][idx], fd)
+            print(f"  ch{ch} rel_l2={err:.3e}", flush=True)
+            assert err <= GATE
+        # channel 1 is channel 0 times a constant: the transform is linear
+        lin = oracle.rel_l2(fb[1], fb[0] * (0.5 + 0.5j))
+        assert lin < 1e-6, lin
+    finally:
+        del plan
+        _release(mn)
