@@ -410,7 +410,29 @@ int mn_pad_deconv_c128(int dim, const int64_t n_up[3], const int64_t N[3], int64
                        mn_stream_t stream);
 int mn_round_c64(int64_t n, const void *in, void *out, mn_stream_t stream);
 
-/* Destroy all cached FFT plans (call with no transform in flight). */
+/*
+ * Batched zero-padding line FFTs in double precision: one axis pass of the
+ * type-3 inner-grid transform, with that axis's pad and deconvolution fused.
+ * `in` is complex128 of shape (A, nin, B), C order; `out` has shape
+ * (A, n, B), complex128, or complex64 when out_c64 != 0. Line (a, b) is
+ * in[a, :, b]: element m, times dec[m] (fp64, length nin; NULL for none),
+ * sits at FFT index (m - nin/2) mod n with zeros elsewhere, and
+ *   out[a, r, b] = sum_p x[p] exp(isign 2 pi i p r / n)   (unnormalised).
+ * Three passes (z, y, x) of bf (nf0 nf1 nf2) give
+ * FFT(pad(bf * dec0 x dec1 x dec2)) on n_up without a padded fp64 grid.
+ * n must be 2^a 3^b 5^c in [2, 8192] (mn_fft64_lines_supported), 1 <= nin <=
+ * n, A*B < 2^31, and in and out must not overlap. The twiddle tables are
+ * cached per (device, n, sign) and released by mn_fft_cache_clear.
+ * ref: gpu_t3.py:630-651 (t3pad), gpu_t3.py:94-148 (fft_axis),
+ * gpu_t3.py:697-741 (t3padz: the slab path's fused pad, deconvolution and
+ * z-DFT).
+ */
+int mn_fft64_lines_supported(int64_t n);
+int mn_fft64_lines(int64_t A, int64_t nin, int64_t B, int64_t n, int isign, const void *in,
+                   const double *dec, void *out, int out_c64, mn_stream_t stream);
+
+/* Destroy all cached FFT plans and line-FFT twiddle tables (call with no
+ * transform in flight). */
 int mn_fft_cache_clear(void);
 
 /* Zero `bytes` bytes of device memory with a fill kernel (no memset node). */

@@ -451,6 +451,22 @@ def round_c64(src128, out64):
             "round_c64")
 
 
+def fft64_lines_supported(n):
+    return bool(L.lib().mn_fft64_lines_supported(int(n)))
+
+
+def fft64_lines(A, nin, B, n, isign, src128, dec64, out):
+    """One axis pass of the zero-padding fp64 line FFT: src128 (A, nin, B)
+    complex128 -> out (A, n, B), complex128 or complex64 (by out's dtype)."""
+    c64 = out.dtype == torch.complex64
+    assert src128.dtype == torch.complex128 and src128.numel() >= A * nin * B
+    assert out.numel() >= A * n * B and (c64 or out.dtype == torch.complex128)
+    assert dec64 is None or (dec64.dtype == torch.float64 and dec64.numel() >= nin)
+    L.check(L.lib().mn_fft64_lines(int(A), int(nin), int(B), int(n), int(isign), L.ptr(src128),
+                                   None if dec64 is None else L.ptr(dec64), L.ptr(out), int(c64),
+                                   L.stream()), "fft64_lines")
+
+
 def fft(grid, n_up, isign, batch=1):
     L.check(L.lib().mn_fft_exec(len(n_up), L.i64x3(n_up), int(batch), int(isign), L.ptr(grid),
                                 L.stream()), "fft")

@@ -62,6 +62,9 @@ inline int64_t tile_cells(const mn_bins *g) {
 // LDS bytes available to one workgroup on the current device.
 int max_lds_per_block();
 
+// Releases the cached twiddle tables of the fp64 line FFTs (mn_fftl.hip).
+void fftl_cache_clear();
+
 // Zero device memory with a fill kernel (usable under graph capture).
 int fill_zero(void *ptr, int64_t bytes, hipStream_t s);
 

@@ -169,6 +169,7 @@ int mn_fft_cache_clear(void) {
     std::lock_guard<std::mutex> lock(g_mu);
     for (auto &kv : g_plans) destroy_plan(kv.second);
     g_plans.clear();
+    fftl_cache_clear();
     return MN_OK;
 }
 

@@ -11,11 +11,18 @@ mode deconvolution vectors) is host fp64; per-point setup (source and target
 rescale, phases, phihat at every target) is native fp64 on the GPU. The
 prephase is fused into the spread and the post factor into the gather.
 
-MI355X holds the n_up^3 grid in HBM at every size the reference handles, so
-there is no slab mode: grids past the reference's 3 GB slab threshold run
-the same single-grid pipeline.
+The deconvolve + pad + FFT stage runs as three fp64 line-FFT passes (z, y,
+x) that each transform only the lines that can be non-zero, with that
+axis's zero padding and deconvolution fused into the line load and the last
+pass rounding to complex64 (csrc/mn_fftl.hip). It never materialises a
+padded fp64 grid; this is the role of the reference's slab mode
+(gpu_t3.py:697-1041: fused pad, deconv and z-DFT, then per-slab lateral
+FFTs), generalised to every axis. Axes longer than 8192 or not 5-smooth
+fall back to pad + rocFFT. MI355X holds every grid the reference handles in
+HBM, so there is no slab switch.
 """
 
+import os
 import warnings
 
 import numpy as np
@@ -137,6 +144,14 @@ class GpuT3Plan:
         self._hd = hd
         self._bf = None
         self._H = None
+        # inner-grid transform: three fused pad + deconvolve + line-FFT passes
+        # when every axis length is 2^a 3^b 5^c <= 8192 and the line counts
+        # fit, else pad + rocFFT (MN_T3_FFT=rocfft forces the latter)
+        nf, nu = self.nf, self.n_up
+        self.fft_lines = (os.environ.get("MN_T3_FFT", "lines") != "rocfft"
+                          and all(E.fft64_lines_supported(n) for n in nu)
+                          and nf[0] * nf[1] < 2**31 and nf[0] * nu[2] < 2**31
+                          and nu[1] * nu[2] < 2**31)
         self.low_mem = bool(low_mem) if low_mem is not None else False
         self.set_sources(x64)
 
@@ -182,10 +197,35 @@ class GpuT3Plan:
 
     def _buffers(self):
         if self._bf is None:
-            self._bf = torch.empty(self.nf, dtype=torch.complex128, device=self.device)
-            self._H = torch.empty(self.n_up, dtype=torch.complex64, device=self.device)
-            self._H64 = torch.empty(self.n_up, dtype=torch.complex128, device=self.device)
+            nf, nu = self.nf, self.n_up
+            self._bf = torch.empty(nf, dtype=torch.complex128, device=self.device)
+            self._H = torch.empty(nu, dtype=torch.complex64, device=self.device)
+            if self.fft_lines:
+                self._T = (torch.empty((nf[0], nf[1], nu[2]), dtype=torch.complex128,
+                                       device=self.device),
+                           torch.empty((nf[0], nu[1], nu[2]), dtype=torch.complex128,
+                                       device=self.device))
+                self._H64 = None
+            else:
+                self._T = None
+                self._H64 = torch.empty(nu, dtype=torch.complex128, device=self.device)
         return self._bf, self._H, self._H64
+
+    def _inner_fft(self, bf, H, H64, tm):
+        """H = (complex64) FFT(pad(bf * dec0 x dec1 x dec2)) on the n_up grid."""
+        nf, nu, d = self.nf, self.n_up, self.dev_dec64
+        if self.fft_lines:
+            T1, T2 = self._T
+            with tm("fft"):
+                E.fft64_lines(nf[0] * nf[1], nf[2], 1, nu[2], self.isign, bf, d[2], T1)
+                E.fft64_lines(nf[0], nf[1], nu[2], nu[1], self.isign, T1, d[1], T2)
+                E.fft64_lines(1, nf[0], nu[1] * nu[2], nu[0], self.isign, T2, d[0], H)
+            return
+        with tm("pad+deconv"):
+            E.pad_deconv_c128(self.n_up, self.nf, bf, d, H64)
+        with tm("fft"):
+            E.fft_f64(H64, self.n_up, self.isign)
+            E.round_c64(H64, H)
 
     def _run(self, cd, tm):
         """Spread (fp64 products and accumulation into a complex128 grid),
@@ -199,15 +239,11 @@ class GpuT3Plan:
         out = torch.empty(self.M, dtype=torch.complex64, device=self.device)
         with tm("spread"):
             E.spread_c128(self.src, self.beta, cd, bf, pre=self.src.extra)
-        with tm("pad+deconv"):
-            E.pad_deconv_c128(self.n_up, self.nf, bf, self.dev_dec64, H64)
-        with tm("fft"):
-            E.fft_f64(H64, self.n_up, self.isign)
-            E.round_c64(H64, H)
+        self._inner_fft(bf, H, H64, tm)
         with tm("gather"):
             E.interp(self.trg, self.beta2, H, out, post=self.trg.extra)
         if self.low_mem:
-            self._bf = self._H = self._H64 = None
+            self._bf = self._H = self._H64 = self._T = None
         return out
 
     def _strengths(self, c):
@@ -238,10 +274,11 @@ class GpuT3Plan:
 
     def execute_profiled(self, c):
         """(result, {stage: seconds}) with HIP-event stage times; the prephase
-        is fused into the spread (ref: gpu_t3.py:1351-1364)."""
+        is fused into the spread and, on the line-FFT path, pad+deconv into
+        the fft (ref: gpu_t3.py:1351-1364)."""
         tm = E.StageTimer(True)
         out = self._run(self._strengths(c), tm)
         ms = tm.times_ms()
-        times = {"prephase": 0.0}
+        times = {"prephase": 0.0, "spread": 0.0, "pad+deconv": 0.0}
         times.update({k: v / 1e3 for k, v in ms.items()})
         return L.to_host(out), times

@@ -1,0 +1,138 @@
+"""GPU checks of the fp64 zero-padding line FFT (mn_fft64_lines) and of the
+type-3 pipeline built on it.
+
+* one pass against numpy's FFT of the explicitly padded, deconvolved lines,
+  for every radix (2, 3, 4, 5, 8 and mixes), odd and even nin, nin = 1 and
+  nin = n, contiguous (B = 1) and strided (B > 1) lines, partial last tiles,
+  both signs and both output precisions;
+* three passes (z, y, x) against numpy's ifftn / fftn of the padded grid;
+* invalid lengths and shapes raise;
+* type-3 through the line passes equals type-3 through pad + rocFFT, and
+  matches the direct sum.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _padded(x, dec, n):
+    """(A, nin, B) -> (A, n, B): element m times dec[m] at (m - nin//2) mod n."""
+    A, nin, B = x.shape
+    pos = (np.arange(nin) - nin // 2) % n
+    out = np.zeros((A, n, B), np.complex128)
+    out[:, pos, :] = x * (dec[None, :, None] if dec is not None else 1.0)
+    return out
+
+
+def _ref(x, dec, n, isign):
+    p = _padded(x, dec, n)
+    return np.fft.ifft(p, axis=1) * n if isign > 0 else np.fft.fft(p, axis=1)
+
+
+CASES = [  # (A, nin, B, n)
+    (7, 18, 1, 24), (3, 5, 7, 8), (1, 1, 33, 2), (2, 3, 5, 3), (4, 5, 3, 5),
+    (5, 13, 1, 16), (3, 40, 9, 64), (2, 25, 6, 30), (1, 180, 17, 240), (9, 486, 1, 640),
+    (1, 639, 8, 640), (3, 625, 2, 625), (2, 729, 3, 729), (1, 5760, 3, 7200),
+    (2, 8192, 1, 8192), (1, 4001, 2, 4096), (300, 7, 1, 12), (1, 90, 1000, 120),
+]
+
+
+@pytest.mark.parametrize("A,nin,B,n", CASES)
+@pytest.mark.parametrize("isign", [+1, -1])
+def test_fft64_lines_vs_numpy(A, nin, B, n, isign, mn):
+    from mlx_nufft_amd import _engine as E
+
+    print(f"case fft64_lines A={A} nin={nin} B={B} n={n} isign={isign}", flush=True)
+    rng = np.random.default_rng(n * 7 + nin)
+    x = rng.standard_normal((A, nin, B)) + 1j * rng.standard_normal((A, nin, B))
+    dec = rng.uniform(0.5, 2.0, nin)
+    ref = _ref(x, dec, n, isign)
+    xd = torch.from_numpy(x).cuda()
+    dd = torch.from_numpy(dec).cuda()
+    out = torch.full((A, n, B), complex(np.nan, np.nan), dtype=torch.complex128, device="cuda")
+    E.fft64_lines(A, nin, B, n, isign, xd, dd, out)
+    got = out.cpu().numpy()
+    err = np.abs(got - ref).max() / np.abs(ref).max()
+    assert err < 1e-13, err
+    out32 = torch.empty((A, n, B), dtype=torch.complex64, device="cuda")
+    E.fft64_lines(A, nin, B, n, isign, xd, None, out32)
+    ref32 = _ref(x, None, n, isign)
+    err32 = np.abs(out32.cpu().numpy() - ref32).max() / np.abs(ref32).max()
+    assert err32 < 1e-6, err32
+
+
+@pytest.mark.parametrize("nf,nu", [((18, 20, 10), (24, 30, 16)), ((45, 36, 18), (60, 48, 24)),
+                                   ((7, 9, 11), (8, 10, 12))])
+@pytest.mark.parametrize("isign", [+1, -1])
+def test_fft64_lines_three_passes_vs_fftn(nf, nu, isign, mn):
+    from mlx_nufft_amd import _engine as E
+
+    print(f"case fft64_lines 3D nf={nf} nu={nu} isign={isign}", flush=True)
+    rng = np.random.default_rng(sum(nf))
+    bf = rng.standard_normal(nf) + 1j * rng.standard_normal(nf)
+    decs = [rng.uniform(0.5, 2.0, k) for k in nf]
+    pad = np.zeros(nu, np.complex128)
+    idx = np.ix_(*[(np.arange(k) - k // 2) % n for k, n in zip(nf, nu)])
+    pad[idx] = bf * decs[0][:, None, None] * decs[1][None, :, None] * decs[2][None, None, :]
+    ref = np.fft.ifftn(pad) * np.prod(nu) if isign > 0 else np.fft.fftn(pad)
+    bd = torch.from_numpy(bf).cuda()
+    dd = [torch.from_numpy(d).cuda() for d in decs]
+    T1 = torch.empty((nf[0], nf[1], nu[2]), dtype=torch.complex128, device="cuda")
+    T2 = torch.empty((nf[0], nu[1], nu[2]), dtype=torch.complex128, device="cuda")
+    H = torch.empty(nu, dtype=torch.complex128, device="cuda")
+    E.fft64_lines(nf[0] * nf[1], nf[2], 1, nu[2], isign, bd, dd[2], T1)
+    E.fft64_lines(nf[0], nf[1], nu[2], nu[1], isign, T1, dd[1], T2)
+    E.fft64_lines(1, nf[0], nu[1] * nu[2], nu[0], isign, T2, dd[0], H)
+    err = np.abs(H.cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err < 1e-13, err
+
+
+def test_fft64_lines_rejects_bad_shapes(mn):
+    from mlx_nufft_amd import _engine as E
+    from mlx_nufft_amd import _lib as L
+
+    print("case fft64_lines errors", flush=True)
+    for n, ok in [(7, False), (14, False), (8194, False), (10800, False), (8192, True),
+                  (7200, True), (1, False), (2, True)]:
+        assert E.fft64_lines_supported(n) == ok, n
+    x = torch.zeros((2, 8, 1), dtype=torch.complex128, device="cuda")
+    out = torch.zeros((2, 16, 1), dtype=torch.complex128, device="cuda")
+    with pytest.raises(ValueError):
+        E.fft64_lines(2, 8, 1, 14, +1, x, None, out)     # 14 = 2 * 7
+    with pytest.raises(ValueError):
+        L.check(L.lib().mn_fft64_lines(2, 17, 1, 16, 1, L.ptr(x), None, L.ptr(out), 0,
+                                       L.stream()), "nin > n")
+    with pytest.raises(ValueError):
+        L.check(L.lib().mn_fft64_lines(2, 8, 1, 16, 1, L.ptr(x), None, L.ptr(x), 0,
+                                       L.stream()), "aliasing")
+
+
+def _gen_generic(P, M, X, S, seed):
+    rng = np.random.default_rng(seed)
+    x = tuple(rng.uniform(-X, X, P) for _ in range(3))
+    s = tuple(rng.uniform(-S, S, M) for _ in range(3))
+    c = rng.standard_normal(P) + 1j * rng.standard_normal(P)
+    return x, c, s
+
+
+@pytest.mark.parametrize("X,S", [(1.0, 200.0), (30.0, 20.0), (5.0, 9.0)])
+@pytest.mark.parametrize("isign", [+1, -1])
+def test_type3_lines_equals_rocfft_path(X, S, isign, oracle, mn, monkeypatch):
+    print(f"case t3 lines vs rocfft X={X} S={S} isign={isign}", flush=True)
+    x, c, s = _gen_generic(60_000, 40_000, X, S, seed=int(X * S))
+    pl = mn.Type3Plan(x, s, eps=1e-5, isign=isign)
+    assert pl.fft_lines
+    fl = pl.execute(c.astype(np.complex64))
+    monkeypatch.setenv("MN_T3_FFT", "rocfft")
+    pr = mn.Type3Plan(x, s, eps=1e-5, isign=isign)
+    assert not pr.fft_lines
+    fr = pr.execute(c.astype(np.complex64))
+    assert oracle.rel_l2(fl, fr) < 1e-6
+    idx = np.random.default_rng(1).choice(s[0].size, 500, replace=False)
+    fd = oracle.dft_t3(x, c, s, isign, idx=idx)
+    err = oracle.rel_l2(fl[idx], fd)
+    print(f"  n_up={pl.n_up} rel_l2={err:.3e}", flush=True)
+    assert err < 1e-4
