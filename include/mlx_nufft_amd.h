@@ -173,6 +173,24 @@ int mn_spread_c128(const mn_bins *g, float beta, int64_t P, int64_t nsub,
                    const void *pre, void *grid, mn_stream_t stream);
 
 /*
+ * The same fp64 spread into a complex128 3D grid, owner-computes: one
+ * workgroup per bin sums the taps that land in its bin from the points of
+ * every bin whose footprints reach it, in an fp64 LDS tile of just the bin,
+ * and stores the bin with plain writes. Every cell of the grid is written
+ * once: no zero fill, no global atomics. Points are sorted by bin (the key
+ * of mn_t3_setpts_src on the same geometry), bin_start[b] is the first
+ * sorted point of bin b (mn_bin_starts, nbins + 1 entries), pre is in
+ * sorted order (may be NULL). Bins need 16 * m0*m1*m2 bytes of LDS and,
+ * along a dim with more than one bin, m >= w - 1.
+ * ref: gpu_t3.py:565-591 (t3spread), nd.py:492-579 (the output-driven spread
+ * idea).
+ */
+int mn_spread_owner_c128(const mn_bins *g, float beta, int64_t P, const int32_t *bin_start,
+                         const uint32_t *perm, const int32_t *const i1s[3],
+                         const float *const frs[3], const void *c, const void *pre, void *grid,
+                         mn_stream_t stream);
+
+/*
  * Owner-computes 3D spread ("z-sweep"), the fast path for 3D type-1 grids
  * with n0, n1 multiples of 8 (>= 16), w <= 8 and n0*n1*n2/16 <= 2^26 keys.
  * Each wavefront owns an 8x8 (x, y) column block over a z-segment of zseg

@@ -191,6 +191,7 @@ class SortedPoints:
                                           L.ptr(self.bstart), L.stream()), "bin starts")
             self.info, self.nsub = None, 0
         else:
+            self.bstart = None
             self.info, self.nsub = build_subproblems(bins, skey, msub)
         self.skey = skey
 
@@ -370,6 +371,31 @@ def spread_c128(pts, beta, c, grid128, pre=None):
                                    L.ptr(pts.info), L.ptr(pts.perm), L.ptr3(pts.i1_rows()),
                                    L.ptr3(pts.fr_rows()), L.ptr(c), L.ptr(pre), L.ptr(grid128),
                                    L.stream()), "spread_c128")
+
+
+OWNER_M = 16   # owner-computes spread bins: 16^3 fp64 complex cells = 64 KB of LDS
+
+
+def owner_bins(w, n):
+    """Owner-computes spread bins: 16 cells per dim, except a last dim of at
+    most 18 cells, which stays whole (one bin along it: no split columns and
+    no second z-owner per point; 16*16*18 cells still fit two workgroups per
+    CU)."""
+    m = [min(OWNER_M, k) for k in n]
+    if n[2] <= 18:
+        m[2] = n[2]
+    return make_bins(3, w, n, m=m)
+
+
+def spread_owner_c128(pts, beta, c, grid128, pre=None):
+    """Owner-computes 3D spread into a complex128 grid that it fully
+    overwrites (no zero fill); pts must carry bin starts (kind "zstream")."""
+    assert pts.bstart is not None and grid128.dtype == torch.complex128
+    L.check(L.lib().mn_spread_owner_c128(ctypes.byref(pts.bins), float(beta), pts.P,
+                                         L.ptr(pts.bstart), L.ptr(pts.perm), L.ptr3(pts.i1_rows()),
+                                         L.ptr3(pts.fr_rows()), L.ptr(c),
+                                         None if pre is None else L.ptr(pre), L.ptr(grid128),
+                                         L.stream()), "spread_owner_c128")
 
 
 def spread_batch(pts, beta, cs, grids):

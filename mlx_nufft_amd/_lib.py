@@ -69,6 +69,8 @@ _SIGS = [
                                      VP3, VP3, c_vp, c_vp, c_vp, c_vp]),
     ("mn_spread_c128", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int64, c_vp, c_vp, VP3,
                                VP3, c_vp, c_vp, c_vp, c_vp]),
+    ("mn_spread_owner_c128", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_vp, c_vp, VP3, VP3,
+                                     c_vp, c_vp, c_vp, c_vp]),
     ("mn_zsweep_nkeys", c_int64, [ctypes.POINTER(Bins)]),
     ("mn_zsweep_setpts", c_int, [ctypes.POINTER(Bins), c_int64, VP3, c_int, c_vp, VP3, c_vp]),
     ("mn_zsweep_starts", c_int, [ctypes.POINTER(Bins), c_int64, c_vp, c_vp, c_vp]),

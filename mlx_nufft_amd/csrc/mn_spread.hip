@@ -179,6 +179,226 @@ __global__ __launch_bounds__(256) void k_spread_tiled(Geom g, float bl2e, float 
     }
 }
 
+// Owner-computes spread into a complex128 grid (3D): one workgroup per bin
+// sums, in an fp64 LDS tile of just that bin's cells, every tap that lands
+// in the bin from the points of the bins whose footprints can reach it, then
+// stores the tile with plain writes. Each grid cell is written by exactly
+// one workgroup, so there is no zero fill and there are no global atomics;
+// a point is read by every owner its footprint may reach (about
+// (1 + (w-1)/m)^3 of them), which costs little when points are sparse
+// relative to the grid (type-3 grids). The reaching bins per dim are those
+// whose cells meet the cyclic interval [lo - (w-1-w/2), lo + cnt - 1 + w/2]
+// of point centres (centre = first tap + w/2, the sort key's cell); at most
+// four per dim, found by walking that interval. Per point and dim, the taps
+// inside the owner's cells come from (first tap + a - lo) mod n < cnt.
+constexpr int OWN_THREADS = 256;
+constexpr int OWN_MAXQ = 4;  // reaching bins per dim
+
+template <int W>
+__global__ __launch_bounds__(OWN_THREADS) void k_spread_owner(
+    Geom g, float bl2e, float inv_hw, int64_t nbins, const int32_t *__restrict__ bstart,
+    const uint32_t *__restrict__ perm, CI3s i1s, CF3s frs, const float2 *__restrict__ c,
+    const float2 *__restrict__ pre, double2 *__restrict__ grid) {
+    extern __shared__ double own[];
+    __shared__ int pf[OWN_MAXQ * OWN_MAXQ * OWN_MAXQ + 1];
+    __shared__ int st[OWN_MAXQ * OWN_MAXQ * OWN_MAXQ];
+    const int tid = threadIdx.x;
+    const int64_t bin = xcd_remap(blockIdx.x, nbins);
+    int b[3], lo[3], cnt[3];
+    {
+        int64_t rem = bin;
+#pragma unroll
+        for (int d = 2; d >= 0; --d) {
+            b[d] = (int)(rem % g.nb[d]);
+            rem /= g.nb[d];
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < 3; ++d) {
+        lo[d] = b[d] * g.m[d];
+        cnt[d] = min(g.m[d], g.n[d] - lo[d]);
+    }
+    const int T = cnt[0] * cnt[1] * cnt[2];
+    double *tre = own, *tim = own + T;
+    if (tid < 64) {
+        // every lane of wave 0 finds the reaching bins of each dim (a little
+        // arithmetic), then lane r takes combination r: its point range, and
+        // a wave scan of the range sizes
+        int qs[3][OWN_MAXQ], nq[3];
+#pragma unroll
+        for (int d = 0; d < 3; ++d) {
+            const int n = g.n[d], m = g.m[d];
+            const int len = cnt[d] + W - 1;
+            nq[d] = 0;
+            if (len >= n) {
+                for (int q = 0; q < g.nb[d] && q < OWN_MAXQ; ++q) qs[d][nq[d]++] = q;
+            } else {
+                int cell = pmod(lo[d] - (W - 1 - W / 2), n), left = len;
+                while (left > 0 && nq[d] < OWN_MAXQ) {
+                    const int q = cell / m;
+                    bool dup = false;
+                    for (int k = 0; k < nq[d]; ++k) dup = dup || qs[d][k] == q;
+                    if (!dup) qs[d][nq[d]++] = q;
+                    const int end = min(q * m + m, n);
+                    left -= end - cell;
+                    cell = end == n ? 0 : end;
+                }
+            }
+        }
+        const int ncomb = nq[0] * nq[1] * nq[2];
+        int s0 = 0, len = 0;
+        if (tid < ncomb) {
+            const int i2 = tid % nq[2], i01 = tid / nq[2];
+            const int i1 = i01 % nq[1], i0 = i01 / nq[1];
+            const int64_t nbr = ((int64_t)qs[0][i0] * g.nb[1] + qs[1][i1]) * g.nb[2] + qs[2][i2];
+            s0 = bstart[nbr];
+            len = bstart[nbr + 1] - s0;
+        }
+        int incl = len;
+#pragma unroll
+        for (int k = 1; k < 64; k <<= 1) {
+            const int v = __shfl_up(incl, k, 64);
+            incl += tid >= k ? v : 0;
+        }
+        pf[tid] = incl - len;
+        st[tid] = s0;
+        if (tid == 63) pf[64] = incl;
+    }
+    __syncthreads();
+    const int tot = pf[OWN_MAXQ * OWN_MAXQ * OWN_MAXQ];
+    if (tot == 0) {  // no point reaches the bin: zeros straight to the grid
+        const int PL = cnt[1] * cnt[2];
+        const int64_t n12 = (int64_t)g.n[1] * g.n[2];
+        for (int t = tid; t < PL; t += OWN_THREADS) {
+            const int e1 = t / cnt[2], e2 = t - e1 * cnt[2];
+            double2 *dst =
+                grid + (int64_t)lo[0] * n12 + (int64_t)(lo[1] + e1) * g.n[2] + lo[2] + e2;
+            for (int e0 = 0; e0 < cnt[0]; ++e0) dst[(int64_t)e0 * n12] = make_double2(0.0, 0.0);
+        }
+        return;
+    }
+    for (int i = tid; i < 2 * T; i += OWN_THREADS) own[i] = 0.0;
+    __syncthreads();
+    int q = 0;
+    for (int t = tid; t < tot; t += OWN_THREADS) {
+        while (t >= pf[q + 1]) ++q;
+        const int64_t j = (int64_t)st[q] + (t - pf[q]);
+        // owner-local cell of each tap per dim (>= cnt: outside the bin);
+        // dims 1 and 2 as register arrays, dim 0 inline in the outer loop
+        int a00 = pmod(lo[0] - i1s.p[0][j], g.n[0]);
+        bool any = a00 < W || a00 > g.n[0] - cnt[0];
+        int loc[2][W];
+#pragma unroll
+        for (int d = 1; d < 3; ++d) {
+            const int n = g.n[d];
+            const int a0 = pmod(lo[d] - i1s.p[d][j], n);
+            bool hit = false;
+#pragma unroll
+            for (int a = 0; a < W; ++a) {
+                int v = a - a0;
+                v += v < 0 ? n : 0;
+                loc[d - 1][a] = v;
+                hit = hit || v < cnt[d];
+            }
+            any = any && hit;
+        }
+        if (!any) continue;
+        float wt[2][W];
+#pragma unroll
+        for (int d = 1; d < 3; ++d) {
+            const float f = frs.p[d][j];
+#pragma unroll
+            for (int a = 0; a < W; ++a)
+                wt[d - 1][a] = loc[d - 1][a] < cnt[d] ? es_weight((float)a - f, bl2e, inv_hw) : 0.0f;
+        }
+        const float f0 = frs.p[0][j];
+        const float2 c0 = c[perm[j]];
+        double cvx = c0.x, cvy = c0.y;
+        if (pre) {
+            const float2 pv = pre[j];
+            const double px = pv.x, py = pv.y;
+            const double rx = cvx * px - cvy * py;
+            cvy = cvx * py + cvy * px;
+            cvx = rx;
+        }
+        for (int a0 = 0; a0 < W; ++a0) {
+            int v0 = a0 - a00;
+            v0 += v0 < 0 ? g.n[0] : 0;
+            if (v0 >= cnt[0]) continue;
+            const double w0 = (double)es_weight((float)a0 - f0, bl2e, inv_hw);
+            const double r0 = cvx * w0, i0 = cvy * w0;
+#pragma unroll
+            for (int a1 = 0; a1 < W; ++a1) {
+                if (loc[0][a1] >= cnt[1]) continue;
+                const double r = r0 * (double)wt[0][a1], im = i0 * (double)wt[0][a1];
+                const int base = (v0 * cnt[1] + loc[0][a1]) * cnt[2];
+#pragma unroll
+                for (int a2 = 0; a2 < W; ++a2) {
+                    if (loc[1][a2] >= cnt[2]) continue;
+                    atomicAdd(&tre[base + loc[1][a2]], r * (double)wt[1][a2]);
+                    atomicAdd(&tim[base + loc[1][a2]], im * (double)wt[1][a2]);
+                }
+            }
+        }
+    }
+    __syncthreads();
+    // store: thread t owns cell (e1, e2) of every x-plane of the bin, so the
+    // index arithmetic is done once and each plane is written row by row
+    const int PL = cnt[1] * cnt[2];
+    const int64_t n12 = (int64_t)g.n[1] * g.n[2];
+    for (int t = tid; t < PL; t += OWN_THREADS) {
+        const int e1 = t / cnt[2], e2 = t - e1 * cnt[2];
+        double2 *dst = grid + (int64_t)lo[0] * n12 + (int64_t)(lo[1] + e1) * g.n[2] + lo[2] + e2;
+        for (int e0 = 0; e0 < cnt[0]; ++e0)
+            dst[(int64_t)e0 * n12] = make_double2(tre[e0 * PL + t], tim[e0 * PL + t]);
+    }
+}
+
+struct OwnerArgs {
+    const mn_bins *g;
+    float beta;
+    const int32_t *bstart;
+    const uint32_t *perm;
+    CI3s i1s;
+    CF3s frs;
+    const float2 *c, *pre;
+    double2 *grid;
+    hipStream_t s;
+};
+
+template <int DIM, int W>
+struct OwnerLaunch {
+    static int run(const OwnerArgs &a) {
+        if constexpr (DIM != 3) {
+            set_error("spread_owner: 3D only");
+            return MN_EINVAL;
+        } else {
+            Geom g = make_geom(a.g);
+            const size_t lds = (size_t)16 * g.m[0] * g.m[1] * g.m[2];
+            if (lds > (size_t)max_lds_per_block()) {
+                set_error("spread_owner: bin does not fit in LDS; use smaller bins");
+                return MN_EINVAL;
+            }
+            const int64_t nb = nbins_total(a.g);
+            const float bl2e = (float)(a.beta * 1.4426950408889634);
+            const float inv_hw = (float)(2.0 / W);
+            for (int d = 0; d < 3; ++d)
+                if (g.nb[d] > 1 && g.m[d] < W - 1) {
+                    set_error("spread_owner: bins must be at least w - 1 cells wide");
+                    return MN_EINVAL;
+                }
+            auto kern = k_spread_owner<W>;
+            if (lds > 60000)  // with the static range tables, past the 64 KB default
+                MN_HIP_CHECK(hipFuncSetAttribute(
+                    (const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+            kern<<<(unsigned)nb, OWN_THREADS, lds, a.s>>>(g, bl2e, inv_hw, nb, a.bstart, a.perm,
+                                                          a.i1s, a.frs, a.c, a.pre, a.grid);
+            MN_LAUNCH_CHECK("spread_owner");
+            return MN_OK;
+        }
+    }
+};
+
 template <int DIM, int W>
 struct SpreadLaunch {
     static int run(const SpreadArgs &a) {
@@ -261,6 +481,33 @@ int mn_spread_c128(const mn_bins *g, float beta, int64_t P, int64_t nsub,
                    mn_stream_t stream) {
     return spread_impl(g, beta, P, nsub, sub_info, perm, i1s, frs, c, pre, grid, true, true,
                        stream);
+}
+
+int mn_spread_owner_c128(const mn_bins *g, float beta, int64_t P, const int32_t *bin_start,
+                         const uint32_t *perm, const int32_t *const i1s[3],
+                         const float *const frs[3], const void *c, const void *pre, void *grid,
+                         mn_stream_t stream) {
+    clear_error();
+    int rc = check_bins(g);
+    if (rc) return rc;
+    MN_REQUIRE(g->dim == 3, "spread_owner: 3D only");
+    MN_REQUIRE(P >= 1 && P < (int64_t(1) << 31), "P must be in [1, 2^31)");
+    MN_REQUIRE(bin_start && perm && c && grid, "spread_owner: NULL pointer");
+    OwnerArgs a{};
+    for (int d = 0; d < 3; ++d) {
+        MN_REQUIRE(i1s[d] && frs[d], "NULL sorted cell/fraction pointer");
+        a.i1s.p[d] = i1s[d];
+        a.frs.p[d] = frs[d];
+    }
+    a.g = g;
+    a.beta = beta;
+    a.bstart = bin_start;
+    a.perm = perm;
+    a.c = static_cast<const float2 *>(c);
+    a.pre = static_cast<const float2 *>(pre);
+    a.grid = static_cast<double2 *>(grid);
+    a.s = as_stream(stream);
+    return select_dim_w<OwnerLaunch>(3, g->w, a);
 }
 
 int mn_spread_accumulate(const mn_bins *g, float beta, int64_t P, int64_t nsub,

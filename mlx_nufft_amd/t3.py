@@ -140,7 +140,24 @@ class GpuT3Plan:
                         for v in self.decs]
         self.dev_dec64 = [torch.from_numpy(np.ascontiguousarray(v, dtype=np.float64))
                           .to(self.device) for v in self.decs]
-        self.bins_src = E.make_bins(3, self.w, self.nf, cell_bytes=E.SPREAD_CELL_BYTES)
+        # spread: the LDS-tile spread (zero fill, atomic halo flushes) or the
+        # owner-computes spread (bins of about 16^3 cells, each cell written
+        # once). Measured on MI355X, the owner spread wins when taps per fine
+        # cell (P w^3 / prod nf) lie in about [0.3, 20] on grids without a
+        # thin axis: the tiles' halo flushes dominate there (486^3, 1e6
+        # points: 3.1 against 8.1 ms); sparser grids favour the tiles' fast
+        # zero fill, denser ones their single visit per point (180^3, 1e6
+        # points: 1.2 against 4.2 ms). MN_T3_SPREAD=owner|tiles forces one.
+        taps = float(self.P) * self.w ** 3 / float(np.prod([float(n) for n in self.nf]))
+        mode = os.environ.get("MN_T3_SPREAD")
+        if mode not in (None, "owner", "tiles"):
+            raise ValueError(f"MN_T3_SPREAD must be 'owner' or 'tiles', not {mode!r}")
+        self.spread_owner = (mode == "owner" or
+                             (mode is None and 0.3 <= taps <= 20.0 and min(self.nf) > 18))
+        if self.spread_owner:
+            self.bins_src = E.owner_bins(self.w, self.nf)
+        else:
+            self.bins_src = E.make_bins(3, self.w, self.nf, cell_bytes=E.SPREAD_CELL_BYTES)
         self._hd = hd
         self._bf = None
         self._H = None
@@ -185,7 +202,7 @@ class GpuT3Plan:
             L.d3(self._hd), L.d3(self.D), self.isign, self._flags,
             L.ptr3([i1[d] for d in range(3)]), L.ptr3([fr[d] for d in range(3)]), L.ptr(key),
             L.ptr(pre), L.stream()), "t3 sources")
-        self.src = E.SortedPoints(self.bins_src, i1, fr, key, extra=pre)
+        self.src = E.SortedPoints(self.bins_src, i1, fr, key, extra=pre, stream=self.spread_owner)
 
     @property
     def mx_perm(self):
@@ -238,7 +255,10 @@ class GpuT3Plan:
         bf, H, H64 = self._buffers()
         out = torch.empty(self.M, dtype=torch.complex64, device=self.device)
         with tm("spread"):
-            E.spread_c128(self.src, self.beta, cd, bf, pre=self.src.extra)
+            if self.spread_owner:
+                E.spread_owner_c128(self.src, self.beta, cd, bf, pre=self.src.extra)
+            else:
+                E.spread_c128(self.src, self.beta, cd, bf, pre=self.src.extra)
         self._inner_fft(bf, H, H64, tm)
         with tm("gather"):
             E.interp(self.trg, self.beta2, H, out, post=self.trg.extra)

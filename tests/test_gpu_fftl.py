@@ -136,3 +136,84 @@ def test_type3_lines_equals_rocfft_path(X, S, isign, oracle, mn, monkeypatch):
     err = oracle.rel_l2(fl[idx], fd)
     print(f"  n_up={pl.n_up} rel_l2={err:.3e}", flush=True)
     assert err < 1e-4
+
+
+@pytest.mark.parametrize("n,w,clustered", [
+    ((40, 36, 33), 9, False),   # partial last bins; 36: reaching bins wrap into one another
+    ((50, 48, 20), 8, True),    # a 2-cell last bin; points packed at the periodic corner
+    ((16, 18, 17), 16, False),  # w = 16, bins of 16 and one-cell last bins
+    ((64, 64, 64), 2, False),
+    ((12, 30, 96), 6, True),    # a dim narrower than a bin (one bin)
+])
+def test_spread_owner_equals_tiles(n, w, clustered, mn):
+    """The owner-computes fp64 spread against the LDS-tile fp64 spread on the
+    same sorted points (two independent accumulations of the same taps)."""
+    from mlx_nufft_amd import _engine as E
+    from mlx_nufft_amd import _lib as L
+
+    print(f"case spread_owner n={n} w={w} clustered={clustered}", flush=True)
+    rng = np.random.default_rng(sum(n) + w)
+    P = 30_000
+    beta = 2.3 * w
+    if clustered:
+        i1 = np.stack([(-w // 2 + rng.integers(-3, 4, P)) % k for k in n])
+    else:
+        i1 = np.stack([rng.integers(-w, k, P) for k in n])
+    fr = rng.uniform(0, 1, (3, P)).astype(np.float32)
+    c = torch.from_numpy((rng.standard_normal(P) + 1j * rng.standard_normal(P))
+                         .astype(np.complex64)).cuda()
+    pre = torch.from_numpy(np.exp(1j * rng.uniform(0, 6.3, P)).astype(np.complex64)).cuda()
+    i1d = torch.from_numpy(i1.astype(np.int32)).cuda()
+    frd = torch.from_numpy(fr).cuda()
+
+    def keys(bins):
+        hw = w // 2
+        k = np.zeros(P, np.int64)
+        for d in range(3):
+            k = k * bins.nb[d] + ((i1[d] + hw) % n[d]) // bins.m[d]
+        return torch.from_numpy(k.astype(np.int32)).cuda()
+
+    bo = E.make_bins(3, w, n, m=[min(E.OWNER_M, k) for k in n])
+    po = E.SortedPoints(bo, i1d, frd, keys(bo), stream=True)
+    go = torch.full(n, complex(np.nan, np.nan), dtype=torch.complex128, device="cuda")
+    # pre is in sorted order in both paths: gather it by each sort's perm
+    E.spread_owner_c128(po, beta, c, go, pre=pre[po.perm.long()])
+    bt = E.make_bins(3, w, n, cell_bytes=E.SPREAD_CELL_BYTES)
+    pt = E.SortedPoints(bt, i1d, frd, keys(bt))
+    gt = torch.empty(n, dtype=torch.complex128, device="cuda")
+    E.spread_c128(pt, beta, c, gt, pre=pre[pt.perm.long()])
+    a, b = go.cpu().numpy(), gt.cpu().numpy()
+    assert np.isfinite(a).all()
+    err = np.abs(a - b).max() / np.abs(b).max()
+    assert err < 1e-12, err
+    assert L.lib().mn_spread_owner_c128 is not None
+
+
+def test_type3_owner_equals_tiles_spread(oracle, mn, monkeypatch):
+    """Type-3 through each spread (forced), equal to within the c64 rounding."""
+    print("case t3 owner vs tiles spread", flush=True)
+    x, c, s = _gen_generic(80_000, 30_000, 8.0, 12.0, seed=3)
+    monkeypatch.setenv("MN_T3_SPREAD", "owner")
+    po = mn.Type3Plan(x, s, eps=1e-6, isign=-1)
+    assert po.spread_owner
+    fo = po.execute(c.astype(np.complex64))
+    monkeypatch.setenv("MN_T3_SPREAD", "tiles")
+    pt = mn.Type3Plan(x, s, eps=1e-6, isign=-1)
+    assert not pt.spread_owner
+    ft = pt.execute(c.astype(np.complex64))
+    assert oracle.rel_l2(fo, ft) < 1e-6
+
+
+def test_type3_spread_selection(mn, monkeypatch):
+    """The automatic choice: owner spread for mid-density isotropic grids,
+    tiles for dense grids and thin slabs; MN_T3_SPREAD overrides."""
+    print("case t3 spread selection", flush=True)
+    x, c, s = _gen_generic(100_000, 2_000, 30.0, 20.0, seed=4)   # 486^3-class grid, 0.4 taps/cell
+    assert mn.Type3Plan(x, s, eps=3e-5).spread_owner
+    x, c, s = _gen_generic(200_000, 2_000, 1.0, 60.0, seed=5)    # dense: ~60^3 grid
+    assert not mn.Type3Plan(x, s, eps=1e-5).spread_owner
+    monkeypatch.setenv("MN_T3_SPREAD", "owner")
+    assert mn.Type3Plan(x, s, eps=1e-5).spread_owner
+    monkeypatch.setenv("MN_T3_SPREAD", "bogus")
+    with pytest.raises(ValueError):
+        mn.Type3Plan(x, s, eps=1e-5)
