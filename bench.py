@@ -51,6 +51,12 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--exec-only", action="store_true",
                     help="time execute() only (plan built once), for profiling")
+    ap.add_argument("--workload", choices=["t1", "t3-generic"], default="t1",
+                    help="t1: the north-star line (default). t3-generic: the reference's "
+                         "type-3 Table I case (generic geometry, 1e6 sources on a 640^3 "
+                         "grid, M = N^2 targets), execute() only")
+    ap.add_argument("--t3-N", type=int, default=1024, choices=[512, 1024, 2048],
+                    help="t3-generic: targets M = N^2")
     ap.add_argument("--copy-calibration", type=float, default=0.0, metavar="GIB",
                     help="only copy a GIB-sized device buffer 5 times: the plain copy "
                          "kernel whose FETCH_SIZE / WRITE_SIZE scale the traffic counters")
@@ -91,6 +97,74 @@ def cpu_baseline(x, c, N, eps):
             "seconds": {k: round(v, 4) for k, v in parts.items()}}
 
 
+# The reference's published type-3 execute times for this workload (M5 Max,
+# mlx-nufft.pdf p.8 Table I), by N: other hardware, context only.
+T3_REF_M5MAX_S = {512: 0.097, 1024: 0.118, 2048: 0.205}
+
+
+def bench_t3(args):
+    """Type-3, the reference's generic acceptance geometry
+    (ref: harness/gen.py:54-67, gen_generic; harness/run_acceptance.py:37-41,
+    106-125): P = 1e6 sources uniform in [-30, 30]^3, M = N^2 targets
+    uniform in [-20, 20]^3, strengths a e^{i th}, eps = 3e-5, isign = +1,
+    crit64; the fine grid is 486^3 (spread) and 640^3 (FFT). A step is one
+    execute() with the plan built and the strengths resident in HBM."""
+    import numpy as np
+    import torch
+
+    import mlx_nufft_amd as mn
+    from mlx_nufft_amd import _lib
+
+    _lib.require_gpu()
+    N, P = args.t3_N, 1_000_000
+    rng = np.random.default_rng(0)
+    x = tuple(rng.uniform(-30.0, 30.0, P) for _ in range(3))
+    s = tuple(rng.uniform(-20.0, 20.0, N * N) for _ in range(3))
+    c = (rng.uniform(0.2, 1.0, P) * np.exp(1j * rng.uniform(0, 2 * np.pi, P))).astype(np.complex64)
+    cd = torch.from_numpy(c).cuda()
+    plan = mn.Type3Plan(x, s, eps=3e-5, isign=+1, prec="crit64")
+    for _ in range(args.warmup):
+        plan.execute(cd, return_np=False)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.steps)]
+    gc.collect()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for a, b in ev:
+        a.record()
+        plan.execute(cd, return_np=False)
+        b.record()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    step_ms = sorted(a.elapsed_time(b) for a, b in ev)
+    _, st = plan.execute_profiled(cd)
+    ref_s = T3_REF_M5MAX_S[N]
+    out = {
+        "metric": "type-3 execute time, generic geometry, 1e6 sources, M = N^2 targets",
+        "value": ms * 1e-3,
+        "unit": "s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f64",
+        "data": "synthetic: numpy default_rng(0), the reference's generic type-3 geometry",
+        "config": {"workload": f"3D type-3 generic P=1e6 M={N * N} eps=3e-5 (Table I)",
+                   "P": P, "M": N * N, "eps": 3e-5, "w": plan.w, "nf": list(plan.nf),
+                   "n_up": list(plan.n_up),
+                   "spread": "owner-computes fp64" if plan.spread_owner else "LDS tiles fp64",
+                   "fft": "fp64 line passes" if plan.fft_lines else "pad + rocFFT fp64"},
+        "step_ms": {"min": step_ms[0], "median": step_ms[len(step_ms) // 2], "max": step_ms[-1]},
+        "stages_ms": {k: round(v * 1e3, 4) for k, v in st.items()},
+        "reference_m5max_s": ref_s,
+        "speedup_vs_reference_m5max": ref_s / (ms * 1e-3),
+    }
+    print(json.dumps(out))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -99,6 +173,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration > 0:
         copy_calibration(args.copy_calibration)
+        return
+    if args.workload == "t3-generic":
+        bench_t3(args)
         return
     import numpy as np
     import torch
