@@ -290,6 +290,20 @@ int mn_interp_zstream(const mn_bins *g, float beta, int64_t P, const int32_t *bi
                       mn_stream_t stream);
 
 /*
+ * Direct 3D interpolation for point sets that are sparse on their grid: one
+ * thread per sorted point reads its w^3 taps straight from the complex64
+ * grid (w contiguous z-cells per row), with no staged tile. Same inputs and
+ * outputs as mn_interp without the subproblem table: points in any order
+ * (bin-sorted for locality), out[perm[j]] = interp(point j) (times post[j]
+ * when post is not NULL). Only g->dim, g->w and g->n are used.
+ * ref: gpu_t3.py:653-693 (t3gather: the type-3 per-target gather x post),
+ * nd.py:908-972 (GM gather).
+ */
+int mn_interp_direct(const mn_bins *g, float beta, int64_t P, const uint32_t *perm,
+                     const int32_t *const i1s[3], const float *const frs[3], const void *grid,
+                     const void *post, void *out, mn_stream_t stream);
+
+/*
  * Batched spread: B strength vectors cs (B x P, caller order, row-major)
  * over the same points into B grids (B x prod n, overwritten); the ES
  * weights are computed once per point and applied to every vector.

@@ -405,6 +405,32 @@ def spread_batch(pts, beta, cs, grids):
                                     L.ptr(grids), L.stream()), "spread_batch")
 
 
+def interp_direct(pts, beta, grid, out, post=None):
+    """3D gather without staged tiles: one thread per sorted point reads its
+    w^3 taps from the grid (sparse point sets)."""
+    L.check(L.lib().mn_interp_direct(ctypes.byref(pts.bins), float(beta), pts.P, L.ptr(pts.perm),
+                                     L.ptr3(pts.i1_rows()), L.ptr3(pts.fr_rows()), L.ptr(grid),
+                                     L.ptr(post), L.ptr(out), L.stream()), "interp direct")
+
+
+def interp_direct_preferred(pts, w, n_up):
+    """True when the direct gather should beat the staged one: its w^3 taps
+    per point against the staged path's padded tile per subproblem (or ~1.7
+    reads of the grid for the z-streaming path). Measured on MI355X (taps /
+    staged cells: staged ms, direct ms): 11.4: 0.43, 0.53 (1e6 targets on
+    240^3); 2.3-2.6: 2.62, 2.20 and 6.43, 3.14 (4e6 targets on 640^3 and on
+    5400^2 x 24); 0.6: 2.42, 0.74 and 4.17, 1.19 (1e6 targets on the same
+    grids). The crossover lies between 2.6 and 11.4; 5 is used."""
+    if pts.bins.dim != 3:
+        return False
+    direct = float(pts.P) * w ** 3
+    if pts.kind == "zstream":
+        staged = 1.7 * float(np.prod([float(n) for n in n_up]))
+    else:
+        staged = float(pts.nsub) * float(np.prod([pts.bins.m[d] + w - 1 for d in range(3)]))
+    return direct < 5.0 * staged
+
+
 def interp(pts, beta, grid, out, post=None):
     if pts.kind == "zstream":
         L.check(L.lib().mn_interp_zstream(ctypes.byref(pts.bins), float(beta), pts.P,

@@ -88,6 +88,8 @@ _SIGS = [
     ("mn_interp", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int64, c_vp, c_vp, VP3, VP3,
                           c_vp, c_vp, c_vp, c_vp]),
     ("mn_bin_starts", c_int, [ctypes.POINTER(Bins), c_int64, c_vp, c_vp, c_vp]),
+    ("mn_interp_direct", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_vp, VP3, VP3, c_vp, c_vp,
+                                 c_vp, c_vp]),
     ("mn_interp_zstream", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_vp, c_vp, VP3, VP3,
                                   c_vp, c_vp, c_vp, c_vp]),
     ("mn_crop_deconv", c_int, [c_int, I64x3, I64x3, c_int64, c_vp, VP3, c_vp, c_vp]),

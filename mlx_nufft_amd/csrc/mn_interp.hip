@@ -175,6 +175,106 @@ __global__ __launch_bounds__(256) void k_interp_tiled(Geom g, float bl2e, float 
     }
 }
 
+// Direct gather (3D) for point sets that are sparse on their grid (the
+// type-3 targets): no tile is staged; each point's w^3 taps are read straight
+// from the grid through L1/L2. A group of w lanes shares one point, lane z of
+// the group taking z-offset z of every (x, y) row, so one load instruction
+// reads w contiguous cells for each of the wave's 64 / w points (a handful
+// of cache lines per instruction, not one per lane). Each lane sums its
+// column over the w^2 rows with the x and y weights, scales by its z weight,
+// and the group's first lane adds the w partial sums (shuffles) and writes
+// the point. A tile costs (m + w - 1)^3 cells per non-empty bin whatever
+// the bin holds, so with about one point per bin this reads several times
+// fewer bytes. Blocks are remapped so each XCD walks a contiguous run of
+// sorted points (neighbours share rows in its L2).
+constexpr int DI_THREADS = 256;
+
+template <int W>
+__global__ __launch_bounds__(DI_THREADS) void k_interp_direct(Geom g, float bl2e, float inv_hw,
+                                                              int64_t P, int64_t nblk,
+                                                              const uint32_t *__restrict__ perm,
+                                                              CI3s i1s, CF3s frs,
+                                                              const float2 *__restrict__ grid,
+                                                              const float2 *__restrict__ post,
+                                                              float2 *__restrict__ out) {
+    constexpr int TPW = 64 / W;                   // points per wave
+    constexpr int TPB = TPW * (DI_THREADS / 64);  // points per block
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int grp = lane / W, z = lane - grp * W;
+    const int64_t j0 = xcd_remap(blockIdx.x, nblk) * TPB + (int64_t)wv * TPW;
+    const int64_t j = j0 + grp;
+    const bool live = grp < TPW && j < P;
+    const int64_t jj = live ? j : 0;  // idle lanes read point 0 (P >= 1)
+    const int n0 = g.n[0], n1 = g.n[1], n2 = g.n[2];
+    const int i0 = i1s.p[0][jj], i1 = i1s.p[1][jj], i2 = i1s.p[2][jj];
+    const float f0 = frs.p[0][jj], f1 = frs.p[1][jj], f2 = frs.p[2][jj];
+    float w0[W], w1[W];
+    int gy[W];
+#pragma unroll
+    for (int a = 0; a < W; ++a) {
+        w0[a] = es_weight((float)a - f0, bl2e, inv_hw);
+        w1[a] = es_weight((float)a - f1, bl2e, inv_hw);
+        gy[a] = wrap_tile_i(i1 + a, n1);
+    }
+    const float wz = es_weight((float)z - f2, bl2e, inv_hw);
+    const int gz = wrap_tile_i(i2 + z, n2);
+    float ar = 0.0f, ai = 0.0f;
+    for (int a0 = 0; a0 < W; ++a0) {
+        const int64_t gx = wrap_tile_i(i0 + a0, n0);
+        const float2 *col = grid + gx * n1 * (int64_t)n2 + gz;
+        float pr = 0.0f, pi = 0.0f;
+#pragma unroll
+        for (int a1 = 0; a1 < W; ++a1) {
+            const float2 v = col[(int64_t)gy[a1] * n2];
+            pr = fmaf(v.x, w1[a1], pr);
+            pi = fmaf(v.y, w1[a1], pi);
+        }
+        ar = fmaf(pr, w0[a0], ar);
+        ai = fmaf(pi, w0[a0], ai);
+    }
+    ar *= wz;
+    ai *= wz;
+    // group sum: lane grp*W adds the other W - 1 lanes of its group
+    const int base = grp * W;
+    float sr = ar, si = ai;
+#pragma unroll
+    for (int k = 1; k < W; ++k) {
+        const int src = min(base + k, 63);
+        const float xr = __shfl(ar, src, 64), xi = __shfl(ai, src, 64);
+        sr += xr;
+        si += xi;
+    }
+    if (live && z == 0) {
+        float2 r = make_float2(sr, si);
+        if (post) {
+            const float2 pv = post[j];
+            r = make_float2(sr * pv.x - si * pv.y, sr * pv.y + si * pv.x);
+        }
+        out[perm[j]] = r;
+    }
+}
+
+template <int DIM, int W>
+struct DirectInterpLaunch {
+    static int run(const InterpArgs &a) {
+        if constexpr (DIM != 3) {
+            set_error("interp direct: 3D only");
+            return MN_EINVAL;
+        } else {
+            Geom g = make_geom(a.g);
+            const float bl2e = (float)(a.beta * 1.4426950408889634);
+            const float inv_hw = (float)(2.0 / W);
+            const int64_t P = a.nsub;  // the point count travels in nsub here
+            constexpr int TPB = (64 / W) * (DI_THREADS / 64);
+            const int64_t nblk = (P + TPB - 1) / TPB;
+            k_interp_direct<W><<<(unsigned)nblk, DI_THREADS, 0, a.s>>>(
+                g, bl2e, inv_hw, P, nblk, a.perm, a.i1s, a.frs, a.grid, a.post, a.out);
+            MN_LAUNCH_CHECK("interp direct");
+            return MN_OK;
+        }
+    }
+};
+
 int interp_threads() {
     static const int v = [] {
         const char *e = getenv("MN_INTERP_THREADS");
@@ -448,6 +548,28 @@ int mn_interp(const mn_bins *g, float beta, int64_t P, int64_t nsub, const int32
     a.out = static_cast<float2 *>(out);
     a.s = as_stream(stream);
     return select_dim_w<InterpLaunch>(g->dim, g->w, a);
+}
+
+int mn_interp_direct(const mn_bins *g, float beta, int64_t P, const uint32_t *perm,
+                     const int32_t *const i1s[3], const float *const frs[3], const void *grid,
+                     const void *post, void *out, mn_stream_t stream) {
+    clear_error();
+    int rc = check_bins(g);
+    if (rc) return rc;
+    MN_REQUIRE(g->dim == 3, "interp direct: 3D only");
+    InterpArgs a{};
+    rc = check_points(g, P, 0, nullptr, perm, i1s, frs, &a.i1s, &a.frs);
+    if (rc) return rc;
+    MN_REQUIRE(perm && grid && out, "interp direct: NULL pointer");
+    a.g = g;
+    a.beta = beta;
+    a.nsub = P;
+    a.perm = perm;
+    a.grid = static_cast<const float2 *>(grid);
+    a.post = static_cast<const float2 *>(post);
+    a.out = static_cast<float2 *>(out);
+    a.s = as_stream(stream);
+    return select_dim_w<DirectInterpLaunch>(3, g->w, a);
 }
 
 int mn_interp_zstream(const mn_bins *g, float beta, int64_t P, const int32_t *bin_start,

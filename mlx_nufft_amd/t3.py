@@ -127,6 +127,15 @@ class GpuT3Plan:
             L.ptr(t_key), L.ptr(post), L.stream()), "t3 targets")
         self.trg = E.SortedPoints(self.bins_trg, t_i1, t_fr, t_key, extra=post, stream=stream)
         del t_i1, t_fr, t_key, post
+        # gather: direct per-target reads unless the targets are dense on the
+        # grid (a staged tile per bin then serves many targets);
+        # MN_T3_GATHER=direct|staged forces one
+        gmode = os.environ.get("MN_T3_GATHER")
+        if gmode not in (None, "direct", "staged"):
+            raise ValueError(f"MN_T3_GATHER must be 'direct' or 'staged', not {gmode!r}")
+        self.gather_direct = (gmode == "direct" or
+                              (gmode is None and E.interp_direct_preferred(self.trg, self.w2,
+                                                                           self.n_up)))
 
         # ---- mode deconvolution (-1)^|q| / phihat(2 pi q / n_up), q in
         # [-nf/2, nf/2); rocFFT's backward transform is unnormalised
@@ -261,7 +270,10 @@ class GpuT3Plan:
                 E.spread_c128(self.src, self.beta, cd, bf, pre=self.src.extra)
         self._inner_fft(bf, H, H64, tm)
         with tm("gather"):
-            E.interp(self.trg, self.beta2, H, out, post=self.trg.extra)
+            if self.gather_direct:
+                E.interp_direct(self.trg, self.beta2, H, out, post=self.trg.extra)
+            else:
+                E.interp(self.trg, self.beta2, H, out, post=self.trg.extra)
         if self.low_mem:
             self._bf = self._H = self._H64 = self._T = None
         return out

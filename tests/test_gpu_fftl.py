@@ -217,3 +217,60 @@ def test_type3_spread_selection(mn, monkeypatch):
     monkeypatch.setenv("MN_T3_SPREAD", "bogus")
     with pytest.raises(ValueError):
         mn.Type3Plan(x, s, eps=1e-5)
+
+
+@pytest.mark.parametrize("n,w", [((40, 36, 24), 9), ((16, 16, 16), 16), ((64, 48, 33), 6),
+                                 ((9, 12, 10), 9)])
+def test_interp_direct_equals_tiles(n, w, oracle, mn):
+    """Direct gather against the staged-tile gather and the oracle's fp64
+    interp on the same points, footprints wrapping on every face."""
+    from mlx_nufft_amd import _engine as E
+
+    print(f"case interp_direct n={n} w={w}", flush=True)
+    rng = np.random.default_rng(sum(n) * w)
+    P, beta = 20_000, 2.3 * w
+    i1 = np.stack([rng.integers(-(w // 2), k, P) for k in n]).astype(np.int32)
+    fr = rng.uniform(0, 1, (3, P)).astype(np.float32)
+    grid = (rng.standard_normal(n) + 1j * rng.standard_normal(n)).astype(np.complex64)
+    post = np.exp(1j * rng.uniform(0, 6.3, P)).astype(np.complex64)
+    hw = w // 2
+    bins = E.make_bins(3, w, n, cell_bytes=E.INTERP_CELL_BYTES)
+    k = np.zeros(P, np.int64)
+    for d in range(3):
+        k = k * bins.nb[d] + ((i1[d] + hw) % n[d]) // bins.m[d]
+    pts = E.SortedPoints(bins, torch.from_numpy(i1).cuda(), torch.from_numpy(fr).cuda(),
+                         torch.from_numpy(k.astype(np.int32)).cuda())
+    gd = torch.from_numpy(grid).cuda()
+    ps = torch.from_numpy(post).cuda()[pts.perm.long()]
+    od = torch.full((P,), complex(np.nan, np.nan), dtype=torch.complex64, device="cuda")
+    ot = torch.empty(P, dtype=torch.complex64, device="cuda")
+    E.interp_direct(pts, beta, gd, od, post=ps)
+    E.interp(pts, beta, gd, ot, post=ps)
+    a, b = od.cpu().numpy(), ot.cpu().numpy()
+    assert np.isfinite(a).all()
+    assert oracle.rel_l2(a, b) < 1e-6
+    ref = oracle.interp(i1, fr, grid, w, beta) * post
+    # fp32 weights and sums over w^3 taps against the fp64 oracle (1.5e-6 at w = 16)
+    assert oracle.rel_l2(a, ref) < 4e-6
+
+
+def test_type3_direct_gather_selection(oracle, mn, monkeypatch):
+    """Sparse targets on a large grid take the direct gather, dense ones the
+    staged gather; forced staged and direct agree."""
+    print("case t3 gather selection", flush=True)
+    x, c, s = _gen_generic(50_000, 20_000, 30.0, 20.0, seed=6)
+    pa = mn.Type3Plan(x, s, eps=1e-5)
+    assert pa.gather_direct
+    fa = pa.execute(c.astype(np.complex64))
+    monkeypatch.setenv("MN_T3_GATHER", "staged")
+    pb = mn.Type3Plan(x, s, eps=1e-5)
+    assert not pb.gather_direct
+    fb = pb.execute(c.astype(np.complex64))
+    # two fp32 gathers in different summation orders, then the target
+    # deconvolution 1/phihat(theta) (~1e2 at the band edges): ~3e-6 apart
+    assert oracle.rel_l2(fa, fb) < 1e-5
+    idx = np.random.default_rng(2).choice(s[0].size, 400, replace=False)
+    assert oracle.rel_l2(fa[idx], oracle.dft_t3(x, c, s, +1, idx=idx)) < 1e-4
+    monkeypatch.delenv("MN_T3_GATHER")
+    x, c, s = _gen_generic(2_000, 400_000, 1.0, 25.0, seed=7)    # 400k targets on ~30^3
+    assert not mn.Type3Plan(x, s, eps=1e-5).gather_direct
