@@ -352,6 +352,18 @@ class Type2PlanND(_PointsND):
             with tm("fft"):
                 E.fft(grid, self.n_up, self.isign)
         with tm("interp"):
-            E.interp(self.pts, self.beta, grid, out)
+            if self._gather_direct():
+                E.interp_direct(self.pts, self.beta, grid, out)
+            else:
+                E.interp(self.pts, self.beta, grid, out)
         self._finish_profile(tm)
         return L.to_host(out) if return_np else out
+
+    def _gather_direct(self):
+        """3D points sparse on the fine grid read their taps directly (no
+        staged tiles); decided once per point set."""
+        pts = self.pts
+        if getattr(self, "_gd_pts", None) is not pts:
+            self._gd_pts = pts
+            self._gd = E.interp_direct_preferred(pts, self.w, self.n_up)
+        return self._gd

@@ -332,3 +332,25 @@ def test_interp_zstream_vs_tiles(N, eps, cluster, mn, monkeypatch):
     E.interp(pz.pts, pz.beta, g, oz)
     E.interp(pt.pts, pt.beta, g, ot)
     assert float((oz - ot).abs().max() / ot.abs().max()) < 1e-6
+
+
+@pytest.mark.parametrize("isign", [+1, -1])
+def test_type2_3d_sparse_direct_gather(isign, oracle, mn):
+    """A 3D type-2 with few points on a large grid gathers directly (no
+    staged tiles) and matches the direct sum; a dense one keeps the tiles."""
+    print(f"case t2 sparse direct gather isign={isign}", flush=True)
+    rng = np.random.default_rng(41)
+    N, M, eps = (96, 80, 64), 3_000, 1e-6
+    x = _pts(rng, 3, M)
+    fk = _cplx(rng, N)
+    p = mn.Type2PlanND(tuple(x), N, eps=eps, isign=isign)
+    c = p.execute(fk)
+    assert p._gather_direct()
+    idx = np.arange(0, M, 7)
+    ce = oracle.dft_t2(x, fk, isign, idx)
+    ref_err = oracle.rel_l2(oracle.nufft_t2(x, fk, eps, isign)[idx], ce)
+    err = oracle.rel_l2(c[idx], ce)
+    print(f"  err={err:.3e} ref_err={ref_err:.3e}")
+    assert err <= max(eps, 2 * ref_err)
+    pd = mn.Type2PlanND(tuple(_pts(rng, 3, 600_000)), (32, 32, 32), eps=1e-5, isign=isign)
+    assert not pd._gather_direct()
