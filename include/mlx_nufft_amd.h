@@ -234,8 +234,10 @@ int mn_spread_zsweep(const mn_bins *g, float beta, int64_t P, int zseg, const in
  * Each wavefront owns 64 consecutive x-columns over a y-segment of yseg
  * cells, walks y with a w-cell window per column in registers and stores
  * every grid cell once (no atomics; the grids are fully overwritten).
- * B strength vectors (c: B x P, caller order; grid: B x n0 x n1) run as
- * independent rows of one launch. g: dim 2, w, n (m and nb are not used).
+ * B strength vectors (c: B x P, caller order; grid: B x n0 x n1) run in
+ * groups of up to 8 per wavefront, which share the point loads, ES weights
+ * and batch lists; every vector's result is bit-identical to a B = 1 launch.
+ * g: dim 2, w, n (m and nb are not used).
  *
  * Point word (one uint32 per point, from mn_ysweep_setpts):
  *   bits 0-25  key = (bx*n1 + y)*2 + reach, where bx is the 64-column block

@@ -317,15 +317,23 @@ class YSweepPoints:
         return _rows(self.frs, 2)
 
 
+def ysweep_vectors_per_wave(B):
+    """Vectors one y-sweep wavefront carries (the kernel's rule): the
+    largest of 8, 4, 2, 1 not above B."""
+    return 8 if B >= 8 else 4 if B >= 4 else 2 if B >= 2 else 1
+
+
 def ysweep_segment(n_up, B):
     """y-segment per wavefront: the longest power of two (<= 256) that still
-    gives at least 8192 wavefronts over the B vectors, but at least 32 (each
-    segment re-reads the w - 1 rows below it to warm its window). Measured
-    at 2048^2, 1e7 points, w = 7: 64 for B = 8 (3.58 ms; 3.70 at 32), 32 for
-    B = 1 (0.49 ms; 0.58 at 16, 0.84 at 64)."""
+    gives at least 8192 / VB wavefronts (VB vectors per wavefront), but at
+    least 32 (each segment re-reads the w - 1 rows below it to warm its
+    window). Measured at 2048^2, 1e7 points, w = 7: 32 for B = 1 (0.49 ms;
+    0.58 at 16, 0.84 at 64); 64 for B = 8, VB = 8 (2.19 ms; 2.39 at 32)."""
+    vb = ysweep_vectors_per_wave(B)
+    groups = -(-B // vb)
     nbx = n_up[0] // 64
     yseg = 256
-    while yseg > 32 and nbx * (-(-n_up[1] // yseg)) * B < 8192:
+    while yseg > 32 and nbx * (-(-n_up[1] // yseg)) * groups * vb < 8192:
         yseg //= 2
     return yseg
 

@@ -17,12 +17,15 @@
 // carries the first tap's column within its block above the key.
 //
 // Per batch of up to 64 points of one y, a lane-per-point prologue builds a
-// table row: the point's x-weights times its strength for the 16 columns of
-// the two 8-column groups its footprint can touch (W <= 8), each group's
-// 8 slots followed by the W y-weights. Per group, a list holds the byte
-// offsets of the slot runs of the points touching it; the group's 8 lanes
-// walk the list, each point costing 2*W FMAs per lane. Vectors of a batch
-// are independent rows of the launch grid.
+// table row: for each of the two 8-column groups its footprint can touch
+// (W <= 8), a run of the group's 8 x-weights, the W y-weights and the
+// point's strengths in the wave's VB vectors. Per group, a list holds the
+// byte offsets of the runs of the points touching it; the group's 8 lanes
+// walk the list, each point costing, per vector, the strength times the
+// lane's x-weight and 2*W FMAs into that vector's window. One wave carries
+// VB vectors (a group of the batch's vectors per launch-grid row), so the
+// cursor, the loads, the ES weights and the lists are shared by all of
+// them; each vector's arithmetic is the same as with VB = 1.
 //
 // The cursor (mn_cursor.h) walks groups of two y-steps; batches take up to
 // 64 consecutive points of a group, with lists per y-step. Loads are issued
@@ -42,22 +45,36 @@ constexpr int YB = kYsBlock;  // columns per block (one per lane)
 constexpr int YG = 8;         // lanes (columns) per group
 constexpr int NG = YB / YG;   // groups per block
 constexpr int YST = 4;        // y-cells staged in LDS per store
-constexpr int YREC = 52;      // floats per table row (48 used; the pad spreads rows over banks)
-constexpr int YRUN = 24;      // floats per group run: 8 complex slots + 8 y-weights
+// floats per group run: 8 x-weights, 8 y-weights, VB complex strengths,
+// padded to a multiple of 4 so that every run is 16-byte aligned
+template <int VB>
+constexpr int yrun() { return (16 + 2 * VB + 3) / 4 * 4; }
+// floats per table row: two runs, padded to 4 mod 8 dwords so that the 16-byte
+// row stores of neighbouring lanes spread over the LDS banks
+template <int VB>
+constexpr int yrec() { return (2 * yrun<VB>()) % 8 == 4 ? 2 * yrun<VB>() : 2 * yrun<VB>() + 4; }
 
-// Stage the finished cell of each column; every YST cells (or at the segment
-// end) the wave writes them out, YST consecutive lanes per column storing
-// YST consecutive y.
-__device__ __forceinline__ void ys_store_stage(float2 (*stage)[64], float2 *__restrict__ grid,
-                                               int lane, int s, int yw, int n1, int bx, float wr,
-                                               float wi, bool last) {
-    stage[s][lane] = make_float2(wr, wi);
+// Stage the finished cell of each column of every vector; every YST cells
+// (or at the segment end) the wave writes them out, YST consecutive lanes
+// per column storing YST consecutive y.
+template <int VB>
+__device__ __forceinline__ void ys_store_stage(float2 (*stage)[YST][64], float2 *__restrict__ grid,
+                                               int64_t gsz, int nv, int lane, int s, int yw, int n1,
+                                               int bx, const float *wr, const float *wi,
+                                               bool last) {
+#pragma unroll
+    for (int v = 0; v < VB; ++v) stage[v][s][lane] = make_float2(wr[v], wi[v]);
     if (s == YST - 1 || last) {
         __syncthreads();
         const int yb = yw - s, ny = s + 1;
-        for (int colb = 0; colb < 64; colb += 64 / YST) {
-            const int col = colb + lane / YST, yo = lane % YST;
-            if (yo < ny) grid[(int64_t)(YB * bx + col) * n1 + yb + yo] = stage[yo][col];
+#pragma unroll
+        for (int v = 0; v < VB; ++v) {
+            if (v >= nv) break;
+            for (int colb = 0; colb < 64; colb += 64 / YST) {
+                const int col = colb + lane / YST, yo = lane % YST;
+                if (yo < ny)
+                    grid[v * gsz + (int64_t)(YB * bx + col) * n1 + yb + yo] = stage[v][yo][col];
+            }
         }
         __syncthreads();
     }
@@ -120,9 +137,9 @@ __device__ __forceinline__ YPoint yp_next(SweepCursor &k, const YFetch yf, int l
     return q;
 }
 
-template <int W>
+template <int W, int VB>
 __global__ __launch_bounds__(64) void k_spread_ysweep(int n1, int nbx, int yseg, int nseg,
-                                                      float bl2e, int64_t P,
+                                                      float bl2e, int64_t P, int64_t B,
                                                       const int32_t *__restrict__ ystart,
                                                       const uint32_t *__restrict__ perm,
                                                       const uint32_t *__restrict__ word,
@@ -130,44 +147,56 @@ __global__ __launch_bounds__(64) void k_spread_ysweep(int n1, int nbx, int yseg,
                                                       const float *__restrict__ fy,
                                                       const float2 *__restrict__ c,
                                                       float2 *__restrict__ grid, int64_t gsz) {
+    constexpr int YRUN = yrun<VB>(), YREC = yrec<VB>();
     __shared__ __align__(16) float table[(64 + 1) * YREC];
     __shared__ __align__(16) uint16_t lists[YZ][NG][64];
-    __shared__ float2 stage[YST][64];
+    __shared__ float2 stage[VB][YST][64];
     __shared__ SweepRanges<NQY> rg;
     __shared__ uint8_t qidx[64];
     constexpr uint32_t kPad = 64u * YREC * 4u;  // byte offset of the zero row
-    const int vec = blockIdx.y;
-    c += (int64_t)vec * P;
-    grid += (int64_t)vec * gsz;
+    static_assert(kPad + YREC * 4u < 65536u, "list offsets are 16-bit");
+    const int64_t v0 = (int64_t)blockIdx.y * VB;
+    const int nv = (int)min((int64_t)VB, B - v0);  // vectors of this wave (>= 1)
+    c += v0 * P;
+    grid += v0 * gsz;
     const int wid = (int)xcd_remap(blockIdx.x, (int64_t)nbx * nseg);
     const int seg = wid % nseg, bx = wid / nseg;
     const int bxm = bx == 0 ? nbx - 1 : bx - 1;
     const int y0 = seg * yseg, yend = min(y0 + yseg, n1);
     const int lane = threadIdx.x, grp = lane / YG, slot = lane % YG;
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    if (lane < YREC) table[64 * YREC + lane] = 0.f;
-    float wre[W], wim[W];
+    for (int i = lane; i < YREC; i += 64) table[64 * YREC + i] = 0.f;
+    float wre[VB][W], wim[VB][W];
 #pragma unroll
-    for (int a = 0; a < W; ++a) wre[a] = wim[a] = 0.f;
+    for (int v = 0; v < VB; ++v)
+#pragma unroll
+        for (int a = 0; a < W; ++a) wre[v][a] = wim[v][a] = 0.f;
     int yw = y0 - (W - 1);  // y of window cell 0
 
     // Window cell 0 moves up by one: cell yw is complete (staged and stored
     // if this segment owns it).
     auto step = [&]() {
-        if (yw >= y0)
-            ys_store_stage(stage, grid, lane, (yw - y0) % YST, yw, n1, bx, wre[0], wim[0],
-                           yw == yend - 1);
+        if (yw >= y0) {
+            float c0r[VB], c0i[VB];
 #pragma unroll
-        for (int a = 0; a < W - 1; ++a) {
-            wre[a] = wre[a + 1];
-            wim[a] = wim[a + 1];
+            for (int v = 0; v < VB; ++v) c0r[v] = wre[v][0], c0i[v] = wim[v][0];
+            ys_store_stage<VB>(stage, grid, gsz, nv, lane, (yw - y0) % YST, yw, n1, bx, c0r, c0i,
+                               yw == yend - 1);
         }
-        wre[W - 1] = wim[W - 1] = 0.f;
+#pragma unroll
+        for (int v = 0; v < VB; ++v) {
+#pragma unroll
+            for (int a = 0; a < W - 1; ++a) {
+                wre[v][a] = wre[v][a + 1];
+                wim[v][a] = wim[v][a + 1];
+            }
+            wre[v][W - 1] = wim[v][W - 1] = 0.f;
+        }
         ++yw;
     };
 
-    // Build and sweep one batch p whose strengths are cp.
-    auto process = [&](const YPoint &p, const float2 cp) __attribute__((always_inline)) {
+    // Build and sweep one batch p whose strengths (per vector) are cp.
+    auto process = [&](const YPoint &p, const float2 *cp) __attribute__((always_inline)) {
         __syncthreads();
 #pragma unroll
         for (int k = 0; k < YZ * NG * 32; k += 64)
@@ -186,19 +215,23 @@ __global__ __launch_bounds__(64) void k_spread_ysweep(int n1, int nbx, int yseg,
             for (int a = 0; a < 8; ++a) wy[a] = a < W ? es_weight_z((float)a * ih - sy, bl2e) : 0.f;
 #pragma unroll
             for (int r = 0; r < 2; ++r) {
-                float4 *run = reinterpret_cast<float4 *>(rec + r * YRUN);
+                float *run = rec + r * YRUN;
+                float wx[YG];
 #pragma unroll
-                for (int q = 0; q < YG; q += 2) {
-                    // columns YG*g0 + s, s = YG*r + q (+1): tap s + YG*g0 - ox
+                for (int q = 0; q < YG; ++q) {
+                    // column YG*g0 + s, s = YG*r + q: tap s + YG*g0 - ox
                     const int s = YG * r + q, a0 = YG * g0 + s - ox;
-                    const float e0 = es_weight_z((float)s * ih + sx, bl2e);
-                    const float e1 = es_weight_z((float)(s + 1) * ih + sx, bl2e);
-                    const float w0 = (unsigned)a0 < (unsigned)W ? e0 : 0.f;
-                    const float w1 = (unsigned)(a0 + 1) < (unsigned)W ? e1 : 0.f;
-                    run[q / 2] = make_float4(cp.x * w0, cp.y * w0, cp.x * w1, cp.y * w1);
+                    const float e = es_weight_z((float)s * ih + sx, bl2e);
+                    wx[q] = (unsigned)a0 < (unsigned)W ? e : 0.f;
                 }
-                run[4] = make_float4(wy[0], wy[1], wy[2], wy[3]);
-                run[5] = make_float4(wy[4], wy[5], wy[6], wy[7]);
+                float4 *r4 = reinterpret_cast<float4 *>(run);
+                r4[0] = make_float4(wx[0], wx[1], wx[2], wx[3]);
+                r4[1] = make_float4(wx[4], wx[5], wx[6], wx[7]);
+                r4[2] = make_float4(wy[0], wy[1], wy[2], wy[3]);
+                r4[3] = make_float4(wy[4], wy[5], wy[6], wy[7]);
+                float2 *r2 = reinterpret_cast<float2 *>(run + 16);
+#pragma unroll
+                for (int v = 0; v < VB; ++v) r2[v] = cp[v];
             }
         }
         // per y-step and group: the batch runs that touch it, in order
@@ -234,21 +267,34 @@ __global__ __launch_bounds__(64) void k_spread_ysweep(int n1, int nbx, int yseg,
             }
             const uint16_t *lq = lists[t][grp];
             for (int it = 0; it < nit; ++it) {
-                const char *run = tb + lq[it];
-                const float2 v = *reinterpret_cast<const float2 *>(run + 8 * slot);
-                const float4 z0 = *reinterpret_cast<const float4 *>(run + 64);
+                const float *run = reinterpret_cast<const float *>(tb + lq[it]);
+                const float wxs = run[slot];
+                const float4 z0 = *reinterpret_cast<const float4 *>(run + 8);
                 float wz[8] = {z0.x, z0.y, z0.z, z0.w, 0.f, 0.f, 0.f, 0.f};
                 if constexpr (W > 4) {
-                    const float4 z1 = *reinterpret_cast<const float4 *>(run + 80);
+                    const float4 z1 = *reinterpret_cast<const float4 *>(run + 12);
                     wz[4] = z1.x, wz[5] = z1.y, wz[6] = z1.z, wz[7] = z1.w;
                 }
+                const float2 *cv = reinterpret_cast<const float2 *>(run + 16);
 #pragma unroll
-                for (int a = 0; a < W; ++a) {
-                    wre[a] = fmaf(v.x, wz[a], wre[a]);
-                    wim[a] = fmaf(v.y, wz[a], wim[a]);
+                for (int v = 0; v < VB; ++v) {
+                    const float2 cw = cv[v];
+                    const float vr = cw.x * wxs, vi = cw.y * wxs;
+#pragma unroll
+                    for (int a = 0; a < W; ++a) {
+                        wre[v][a] = fmaf(vr, wz[a], wre[v][a]);
+                        wim[v][a] = fmaf(vi, wz[a], wim[v][a]);
+                    }
                 }
             }
         }
+    };
+
+    // Strengths of one batch in every vector of the wave (vectors past nv
+    // read the last valid one; their windows are never stored).
+    auto gather = [&](const YPoint &p, float2 *cp) __attribute__((always_inline)) {
+#pragma unroll
+        for (int v = 0; v < VB; ++v) cp[v] = c[(int64_t)min(v, nv - 1) * P + p.src];
     };
 
     // The batch loop, unrolled three ways with rotating names (A, B, C) so
@@ -260,22 +306,22 @@ __global__ __launch_bounds__(64) void k_spread_ysweep(int n1, int nbx, int yseg,
     cur.pzc = INT32_MIN;
     sweep_load<NQY, YZ>(cur, y0 - (W - 1), rg, lane, yf);
     YPoint pa = yp_next(cur, yf, lane, rg, qidx, perm, word, fx, fy);
-    float2 ca = c[pa.src];  // idle lanes read c[perm[0]]: their rows are never used
+    float2 ca[VB], cb[VB], cc[VB];
+    gather(pa, ca);  // idle lanes read c[perm[0]]: their rows are never used
     YPoint pb = yp_next(cur, yf, lane, rg, qidx, perm, word, fx, fy);
     YPoint pc;
-    float2 cb, cc;
     for (;;) {
         if (pa.nb == 0) break;
         pc = yp_next(cur, yf, lane, rg, qidx, perm, word, fx, fy);
-        cb = c[pb.src];
+        gather(pb, cb);
         process(pa, ca);
         if (pb.nb == 0) break;
         pa = yp_next(cur, yf, lane, rg, qidx, perm, word, fx, fy);
-        cc = c[pc.src];
+        gather(pc, cc);
         process(pb, cb);
         if (pc.nb == 0) break;
         pb = yp_next(cur, yf, lane, rg, qidx, perm, word, fx, fy);
-        ca = c[pa.src];
+        gather(pa, ca);
         process(pc, cc);
     }
     while (yw < yend) step();  // drain the window up to the segment end
@@ -293,13 +339,29 @@ struct YsArgs {
     hipStream_t s;
 };
 
-template <int W>
-int ys_launch(const YsArgs &a) {
-    const dim3 blocks((unsigned)(a.nbx * a.nseg), (unsigned)a.B);
-    k_spread_ysweep<W><<<blocks, 64, 0, a.s>>>(a.n1, a.nbx, a.yseg, a.nseg, a.bl2e, a.P, a.ystart,
-                                               a.perm, a.word, a.fx, a.fy, a.c, a.grid, a.gsz);
+// Vectors per wave: the largest of 8, 4, 2, 1 not above B (measured at
+// 2048^2, 1e7 points, w = 7, B = 8: 2.19 ms at VB = 8 with 64-row segments,
+// 2.3-2.4 ms at VB = 2 or 4, 5.5 ms at VB = 1).
+inline int ys_vb(int64_t B) { return B >= 8 ? 8 : (B >= 4 ? 4 : (B >= 2 ? 2 : 1)); }
+
+template <int W, int VB>
+int ys_launch_vb(const YsArgs &a) {
+    const dim3 blocks((unsigned)(a.nbx * a.nseg), (unsigned)((a.B + VB - 1) / VB));
+    k_spread_ysweep<W, VB><<<blocks, 64, 0, a.s>>>(a.n1, a.nbx, a.yseg, a.nseg, a.bl2e, a.P, a.B,
+                                                   a.ystart, a.perm, a.word, a.fx, a.fy, a.c,
+                                                   a.grid, a.gsz);
     MN_LAUNCH_CHECK("spread_ysweep");
     return MN_OK;
+}
+
+template <int W>
+int ys_launch(const YsArgs &a) {
+    switch (ys_vb(a.B)) {
+        case 8: return ys_launch_vb<W, 8>(a);
+        case 4: return ys_launch_vb<W, 4>(a);
+        case 2: return ys_launch_vb<W, 2>(a);
+        default: return ys_launch_vb<W, 1>(a);
+    }
 }
 
 }  // namespace
