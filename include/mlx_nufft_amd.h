@@ -7,8 +7,9 @@
  *   MN_OK (0), MN_EINVAL (-1, bad argument), MN_ERUNTIME (-2, HIP/rocFFT
  *   failure), MN_ENOTIMPL (-3, unsupported combination).
  * On a non-zero status, mn_last_error() returns a message for the calling
- * thread. The library owns no caller data; it keeps only a mutex-guarded
- * rocFFT plan cache (plus the plans' work buffers).
+ * thread. The library owns no caller data; it keeps only mutex-guarded
+ * caches: rocFFT plans (plus their work buffers) and the twiddle tables of
+ * the fp64 line FFTs, both released by mn_fft_cache_clear.
  *
  * Complex data are interleaved complex64 (float re, float im) -- the
  * layout of numpy/torch complex64. Grids are C-ordered (last dim fastest).
