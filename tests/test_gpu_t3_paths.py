@@ -1,14 +1,18 @@
-"""GPU checks of the fp64 zero-padding line FFT (mn_fft64_lines) and of the
-type-3 pipeline built on it.
+"""GPU checks of the type-3 execution paths and the kernels behind them.
 
-* one pass against numpy's FFT of the explicitly padded, deconvolved lines,
-  for every radix (2, 3, 4, 5, 8 and mixes), odd and even nin, nin = 1 and
-  nin = n, contiguous (B = 1) and strided (B > 1) lines, partial last tiles,
-  both signs and both output precisions;
-* three passes (z, y, x) against numpy's ifftn / fftn of the padded grid;
-* invalid lengths and shapes raise;
+* the fp64 zero-padding line FFT (mn_fft64_lines): one pass against numpy's
+  FFT of the explicitly padded, deconvolved lines, for every radix (2, 3,
+  4, 5, 8 and mixes), odd and even nin, nin = 1 and nin = n, contiguous
+  (B = 1) and strided (B > 1) lines, partial last tiles, both signs and
+  both output precisions; three passes (z, y, x) against numpy's ifftn /
+  fftn of the padded grid; invalid lengths and shapes raise;
 * type-3 through the line passes equals type-3 through pad + rocFFT, and
-  matches the direct sum.
+  matches the direct sum;
+* the owner-computes fp64 spread equals the LDS-tile fp64 spread on awkward
+  grids (partial and wrapping bins, w up to 16, clustered points), in
+  isolation and through the type-3 plan, and the plan's spread selection;
+* the direct gather equals the staged gather and the oracle's fp64 interp
+  (footprints wrapping on every face), and the plan's gather selection.
 """
 
 import numpy as np
