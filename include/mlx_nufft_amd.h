@@ -449,7 +449,8 @@ int mn_round_c64(int64_t n, const void *in, void *out, mn_stream_t stream);
  * Batched zero-padding line FFTs in double precision: one axis pass of the
  * type-3 inner-grid transform, with that axis's pad and deconvolution fused.
  * `in` is complex128 of shape (A, nin, B), C order; `out` has shape
- * (A, n, B), complex128, or complex64 when out_c64 != 0. Line (a, b) is
+ * (A, n, B), or (n, A*B) with the line index fastest when lines_last != 0,
+ * complex128, or complex64 when out_c64 != 0. Line (a, b) is
  * in[a, :, b]: element m, times dec[m] (fp64, length nin; NULL for none),
  * sits at FFT index (m - nin/2) mod n with zeros elsewhere, and
  *   out[a, r, b] = sum_p x[p] exp(isign 2 pi i p r / n)   (unnormalised).
@@ -464,7 +465,19 @@ int mn_round_c64(int64_t n, const void *in, void *out, mn_stream_t stream);
  */
 int mn_fft64_lines_supported(int64_t n);
 int mn_fft64_lines(int64_t A, int64_t nin, int64_t B, int64_t n, int isign, const void *in,
-                   const double *dec, void *out, int out_c64, mn_stream_t stream);
+                   const double *dec, void *out, int out_c64, int lines_last,
+                   mn_stream_t stream);
+
+/*
+ * Batched transpose of complex128 matrices: out[b][c][r] = in[b][r][c] for
+ * in (Bt, R, C) and out (Bt, C, R), Bt <= 65535; in and out must not
+ * overlap. Between the type-3 line passes it turns a strided axis of long
+ * lines (which fill the LDS one line per workgroup) into a contiguous one.
+ * ref: gpu_t3.py:151-199 (fft_axis_scrambled: the reference's four-step
+ * reordering for long axes).
+ */
+int mn_transpose_c128(int64_t Bt, int64_t R, int64_t C, const void *in, void *out,
+                      mn_stream_t stream);
 
 /* Destroy all cached FFT plans and line-FFT twiddle tables (call with no
  * transform in flight). */

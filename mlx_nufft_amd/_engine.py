@@ -515,16 +515,25 @@ def fft64_lines_supported(n):
     return bool(L.lib().mn_fft64_lines_supported(int(n)))
 
 
-def fft64_lines(A, nin, B, n, isign, src128, dec64, out):
+def fft64_lines(A, nin, B, n, isign, src128, dec64, out, lines_last=False):
     """One axis pass of the zero-padding fp64 line FFT: src128 (A, nin, B)
-    complex128 -> out (A, n, B), complex128 or complex64 (by out's dtype)."""
+    complex128 -> out (A, n, B), or (n, A*B) with lines_last, complex128 or
+    complex64 (by out's dtype)."""
     c64 = out.dtype == torch.complex64
     assert src128.dtype == torch.complex128 and src128.numel() >= A * nin * B
     assert out.numel() >= A * n * B and (c64 or out.dtype == torch.complex128)
     assert dec64 is None or (dec64.dtype == torch.float64 and dec64.numel() >= nin)
     L.check(L.lib().mn_fft64_lines(int(A), int(nin), int(B), int(n), int(isign), L.ptr(src128),
                                    None if dec64 is None else L.ptr(dec64), L.ptr(out), int(c64),
-                                   L.stream()), "fft64_lines")
+                                   int(bool(lines_last)), L.stream()), "fft64_lines")
+
+
+def transpose_c128(Bt, R, C, src, out):
+    """out[b][c][r] = src[b][r][c] for complex128 (Bt, R, C) -> (Bt, C, R)."""
+    assert src.dtype == torch.complex128 and out.dtype == torch.complex128
+    assert src.numel() >= Bt * R * C and out.numel() >= Bt * R * C
+    L.check(L.lib().mn_transpose_c128(int(Bt), int(R), int(C), L.ptr(src), L.ptr(out),
+                                      L.stream()), "transpose_c128")
 
 
 def fft(grid, n_up, isign, batch=1):

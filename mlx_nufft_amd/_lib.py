@@ -106,7 +106,8 @@ _SIGS = [
     ("mn_round_c64", c_int, [c_int64, c_vp, c_vp, c_vp]),
     ("mn_fft64_lines_supported", c_int, [c_int64]),
     ("mn_fft64_lines", c_int, [c_int64, c_int64, c_int64, c_int64, c_int, c_vp, c_vp, c_vp, c_int,
-                               c_vp]),
+                               c_int, c_vp]),
+    ("mn_transpose_c128", c_int, [c_int64, c_int64, c_int64, c_vp, c_vp, c_vp]),
     ("mn_fftp_supported", c_int, [c_int, I64x3]),
     ("mn_fftp_work_bytes", c_int64, [c_int, I64x3, I64x3, c_int64]),
     ("mn_fft_crop_deconv", c_int, [c_int, I64x3, I64x3, c_int64, c_int, c_vp, VP3, c_vp, c_int64,

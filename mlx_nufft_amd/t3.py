@@ -107,10 +107,30 @@ class GpuT3Plan:
         self.n_up = [next235even(int(np.ceil(self.sigma_in * nf))) for nf in self.nf]
         self.slab_mode = False
 
+        # ---- inner-grid transform: three fused pad + deconvolve + line-FFT
+        # passes when every axis length is 2^a 3^b 5^c <= 8192 and the line
+        # counts fit, else pad + rocFFT (MN_T3_FFT=rocfft forces the latter).
+        # When an x or y line is too long for two lines per LDS tile, the
+        # passes run in reversed axis order so that every long line is
+        # contiguous (z written axis-outermost, y, a transpose, x): the grid
+        # then comes out as (n2, n1, n0) and the targets are set up with
+        # their axes reversed to gather from it.
+        nf, nu = self.nf, self.n_up
+        self.fft_lines = (os.environ.get("MN_T3_FFT", "lines") != "rocfft"
+                          and all(E.fft64_lines_supported(n) for n in nu)
+                          and nf[0] * nf[1] < 2**31 and nf[0] * nu[2] < 2**31
+                          and nu[1] * nu[2] < 2**31)
+        self.fft_rev = (self.fft_lines and max(nu[0], nu[1]) > 1365 and nu[2] <= 65535
+                        and (nf[0] + 31) // 32 <= 65535 and nu[2] * nf[0] < 2**31
+                        and nu[2] * nu[1] < 2**31)
+        ax = [2, 1, 0] if self.fft_rev else [0, 1, 2]   # grid axis k holds axis ax[k]
+        self.grid_shape = [nu[a] for a in ax]
+
         # ---- targets: rescale, post factor, bin sort (device fp64) ----------
         stream = E.zstream_eligible(3, self.w2)
-        self.bins_trg = (E.make_bins(3, self.w2, self.n_up, m=E.ZSTREAM_M) if stream else
-                         E.make_bins(3, self.w2, self.n_up, cell_bytes=E.INTERP_CELL_BYTES))
+        self.bins_trg = (E.make_bins(3, self.w2, self.grid_shape, m=E.ZSTREAM_M) if stream else
+                         E.make_bins(3, self.w2, self.grid_shape,
+                                     cell_bytes=E.INTERP_CELL_BYTES))
         hd = [2.0 * PI / nf for nf in self.nf]
         hg = [hd[d] * self.gam[d] for d in range(3)]
         h2 = [2.0 * PI / n for n in self.n_up]
@@ -121,8 +141,9 @@ class GpuT3Plan:
         t_key = torch.empty(self.M, dtype=torch.int32, device=self.device)
         post = torch.empty(self.M, dtype=torch.complex64, device=self.device)
         L.check(L.lib().mn_t3_setpts_trg(
-            L.ctypes.byref(self.bins_trg), self.M, L.ptr3(s64), L.d3(self.D), L.d3(hg), L.d3(h2),
-            L.d3(self.C), self.isign, self._flags, L.ptr(quad), len(dq),
+            L.ctypes.byref(self.bins_trg), self.M, L.ptr3([s64[a] for a in ax]),
+            L.d3([self.D[a] for a in ax]), L.d3([hg[a] for a in ax]), L.d3([h2[a] for a in ax]),
+            L.d3([self.C[a] for a in ax]), self.isign, self._flags, L.ptr(quad), len(dq),
             L.ptr3([t_i1[d] for d in range(3)]), L.ptr3([t_fr[d] for d in range(3)]),
             L.ptr(t_key), L.ptr(post), L.stream()), "t3 targets")
         self.trg = E.SortedPoints(self.bins_trg, t_i1, t_fr, t_key, extra=post, stream=stream)
@@ -135,7 +156,7 @@ class GpuT3Plan:
             raise ValueError(f"MN_T3_GATHER must be 'direct' or 'staged', not {gmode!r}")
         self.gather_direct = (gmode == "direct" or
                               (gmode is None and E.interp_direct_preferred(self.trg, self.w2,
-                                                                           self.n_up)))
+                                                                           self.grid_shape)))
 
         # ---- mode deconvolution (-1)^|q| / phihat(2 pi q / n_up), q in
         # [-nf/2, nf/2); rocFFT's backward transform is unnormalised
@@ -170,14 +191,6 @@ class GpuT3Plan:
         self._hd = hd
         self._bf = None
         self._H = None
-        # inner-grid transform: three fused pad + deconvolve + line-FFT passes
-        # when every axis length is 2^a 3^b 5^c <= 8192 and the line counts
-        # fit, else pad + rocFFT (MN_T3_FFT=rocfft forces the latter)
-        nf, nu = self.nf, self.n_up
-        self.fft_lines = (os.environ.get("MN_T3_FFT", "lines") != "rocfft"
-                          and all(E.fft64_lines_supported(n) for n in nu)
-                          and nf[0] * nf[1] < 2**31 and nf[0] * nu[2] < 2**31
-                          and nu[1] * nu[2] < 2**31)
         self.low_mem = bool(low_mem) if low_mem is not None else False
         self.set_sources(x64)
 
@@ -225,12 +238,16 @@ class GpuT3Plan:
         if self._bf is None:
             nf, nu = self.nf, self.n_up
             self._bf = torch.empty(nf, dtype=torch.complex128, device=self.device)
-            self._H = torch.empty(nu, dtype=torch.complex64, device=self.device)
-            if self.fft_lines:
-                self._T = (torch.empty((nf[0], nf[1], nu[2]), dtype=torch.complex128,
-                                       device=self.device),
-                           torch.empty((nf[0], nu[1], nu[2]), dtype=torch.complex128,
-                                       device=self.device))
+            self._H = torch.empty(self.grid_shape, dtype=torch.complex64, device=self.device)
+            c128 = dict(dtype=torch.complex128, device=self.device)
+            if self.fft_rev:
+                self._T = (torch.empty((nu[2], nf[0], nf[1]), **c128),
+                           torch.empty((nu[2], nf[0], nu[1]), **c128),
+                           torch.empty((nu[2], nu[1], nf[0]), **c128))
+                self._H64 = None
+            elif self.fft_lines:
+                self._T = (torch.empty((nf[0], nf[1], nu[2]), **c128),
+                           torch.empty((nf[0], nu[1], nu[2]), **c128))
                 self._H64 = None
             else:
                 self._T = None
@@ -240,6 +257,17 @@ class GpuT3Plan:
     def _inner_fft(self, bf, H, H64, tm):
         """H = (complex64) FFT(pad(bf * dec0 x dec1 x dec2)) on the n_up grid."""
         nf, nu, d = self.nf, self.n_up, self.dev_dec64
+        if self.fft_rev:
+            T1, T2, T3 = self._T
+            with tm("fft"):
+                # z lines -> (n2, nf0, nf1); y lines -> (n2, nf0, n1); transpose
+                # -> (n2, n1, nf0); x lines -> H (n2, n1, n0)
+                E.fft64_lines(nf[0] * nf[1], nf[2], 1, nu[2], self.isign, bf, d[2], T1,
+                              lines_last=True)
+                E.fft64_lines(nu[2] * nf[0], nf[1], 1, nu[1], self.isign, T1, d[1], T2)
+                E.transpose_c128(nu[2], nf[0], nu[1], T2, T3)
+                E.fft64_lines(nu[2] * nu[1], nf[0], 1, nu[0], self.isign, T3, d[0], H)
+            return
         if self.fft_lines:
             T1, T2 = self._T
             with tm("fft"):

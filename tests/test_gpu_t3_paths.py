@@ -94,6 +94,37 @@ def test_fft64_lines_three_passes_vs_fftn(nf, nu, isign, mn):
     assert err < 1e-13, err
 
 
+@pytest.mark.parametrize("A,nin,B,n", [(7, 18, 1, 24), (300, 18, 1, 24), (6, 5, 4, 8),
+                                        (2, 486, 1, 640), (1, 30, 64, 40)])
+def test_fft64_lines_lines_last(A, nin, B, n, mn):
+    """lines_last: the same transform written as (n, A*B), line index fastest."""
+    from mlx_nufft_amd import _engine as E
+
+    print(f"case fft64_lines lines_last A={A} nin={nin} B={B} n={n}", flush=True)
+    rng = np.random.default_rng(A + nin + B + n)
+    x = rng.standard_normal((A, nin, B)) + 1j * rng.standard_normal((A, nin, B))
+    dec = rng.uniform(0.5, 2.0, nin)
+    ref = _ref(x, dec, n, +1)                                 # (A, n, B)
+    ref_t = np.transpose(ref, (1, 0, 2)).reshape(n, A * B)   # (n, lines)
+    out = torch.full((n, A * B), complex(np.nan, np.nan), dtype=torch.complex128, device="cuda")
+    E.fft64_lines(A, nin, B, n, +1, torch.from_numpy(x).cuda(), torch.from_numpy(dec).cuda(),
+                  out, lines_last=True)
+    err = np.abs(out.cpu().numpy() - ref_t).max() / np.abs(ref_t).max()
+    assert err < 1e-13, err
+
+
+@pytest.mark.parametrize("Bt,R,C", [(1, 1, 1), (3, 37, 70), (24, 64, 96), (2, 200, 33)])
+def test_transpose_c128(Bt, R, C, mn):
+    from mlx_nufft_amd import _engine as E
+
+    print(f"case transpose Bt={Bt} R={R} C={C}", flush=True)
+    rng = np.random.default_rng(R * C + Bt)
+    a = rng.standard_normal((Bt, R, C)) + 1j * rng.standard_normal((Bt, R, C))
+    out = torch.full((Bt, C, R), complex(np.nan, np.nan), dtype=torch.complex128, device="cuda")
+    E.transpose_c128(Bt, R, C, torch.from_numpy(a).cuda(), out)
+    assert np.array_equal(out.cpu().numpy(), np.transpose(a, (0, 2, 1)))
+
+
 def test_fft64_lines_rejects_bad_shapes(mn):
     from mlx_nufft_amd import _engine as E
     from mlx_nufft_amd import _lib as L
@@ -107,11 +138,13 @@ def test_fft64_lines_rejects_bad_shapes(mn):
     with pytest.raises(ValueError):
         E.fft64_lines(2, 8, 1, 14, +1, x, None, out)     # 14 = 2 * 7
     with pytest.raises(ValueError):
-        L.check(L.lib().mn_fft64_lines(2, 17, 1, 16, 1, L.ptr(x), None, L.ptr(out), 0,
+        L.check(L.lib().mn_fft64_lines(2, 17, 1, 16, 1, L.ptr(x), None, L.ptr(out), 0, 0,
                                        L.stream()), "nin > n")
     with pytest.raises(ValueError):
-        L.check(L.lib().mn_fft64_lines(2, 8, 1, 16, 1, L.ptr(x), None, L.ptr(x), 0,
+        L.check(L.lib().mn_fft64_lines(2, 8, 1, 16, 1, L.ptr(x), None, L.ptr(x), 0, 0,
                                        L.stream()), "aliasing")
+    with pytest.raises(ValueError):
+        L.check(L.lib().mn_transpose_c128(2, 4, 4, L.ptr(x), L.ptr(x), L.stream()), "aliasing")
 
 
 def _gen_generic(P, M, X, S, seed):
@@ -278,3 +311,31 @@ def test_type3_direct_gather_selection(oracle, mn, monkeypatch):
     monkeypatch.delenv("MN_T3_GATHER")
     x, c, s = _gen_generic(2_000, 400_000, 1.0, 25.0, seed=7)    # 400k targets on ~30^3
     assert not mn.Type3Plan(x, s, eps=1e-5).gather_direct
+
+
+def test_type3_reversed_axis_pipeline(oracle, mn, monkeypatch):
+    """Grids with a long x or y axis take the reversed-axis line pipeline
+    (z-pass written axis-outermost, contiguous y-pass, transpose, contiguous
+    x-pass, targets gathered with their axes reversed); it equals the pad +
+    rocFFT path and matches the direct sum."""
+    import sys
+    import pathlib
+    sys.path.insert(0, str(pathlib.Path(__file__).parent))
+    from test_gpu_t3_large import gen_anisotropic
+
+    print("case t3 reversed-axis pipeline", flush=True)
+    x, c, s = gen_anisotropic(64, 5_000, 0.5)
+    for isign in (+1, -1):
+        monkeypatch.delenv("MN_T3_FFT", raising=False)
+        pl = mn.Type3Plan(x, s, eps=1e-5, isign=isign)
+        assert pl.fft_lines and pl.fft_rev and max(pl.n_up[:2]) > 1365, pl.n_up
+        fl = pl.execute(c.astype(np.complex64))
+        monkeypatch.setenv("MN_T3_FFT", "rocfft")
+        pr = mn.Type3Plan(x, s, eps=1e-5, isign=isign)
+        assert not pr.fft_lines
+        fr = pr.execute(c.astype(np.complex64))
+        assert oracle.rel_l2(fl, fr) < 1e-5
+        idx = np.random.default_rng(3).choice(s[0].size, 500, replace=False)
+        err = oracle.rel_l2(fl[idx], oracle.dft_t3(x, c, s, isign, idx=idx))
+        print(f"  isign={isign} n_up={pl.n_up} rel_l2={err:.3e}", flush=True)
+        assert err < 1e-4
