@@ -18,8 +18,11 @@ pass rounding to complex64 (csrc/mn_fftl.hip). It never materialises a
 padded fp64 grid; this is the role of the reference's slab mode
 (gpu_t3.py:697-1041: fused pad, deconv and z-DFT, then per-slab lateral
 FFTs), generalised to every axis. Axes longer than 8192 or not 5-smooth
-fall back to pad + rocFFT. MI355X holds every grid the reference handles in
-HBM, so there is no slab switch.
+fall back to pad + rocFFT. When an x or y line is long (> 1365 points), the
+passes run in reversed axis order with one transpose, so every long line is
+read contiguously, and the grid comes out as (n2, n1, n0); the targets are
+then set up with their axes reversed. MI355X holds every grid the reference
+handles in HBM, so there is no slab switch.
 """
 
 import os
