@@ -32,6 +32,7 @@
 // and z-DFT, which this generalises to every axis).
 #include "mn_common.h"
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -305,6 +306,72 @@ __global__ __launch_bounds__(256) void k_transpose_c128(const double2 *__restric
     }
 }
 
+// Long contiguous lines (n > 4096, B == 1, one line per tile): a persistent
+// workgroup per CU walks lines gridDim.x apart. The next line's inputs are
+// loaded into registers (up to 8 complex128 per thread) right after the
+// current line is in LDS, so they arrive while its stages run, and the LDS
+// fill of a line is register to LDS. One 7200-point fp64 line fills the
+// LDS, so without this a CU loads, transforms and stores strictly in turn.
+constexpr int FLL_THREADS = 1024;
+constexpr int FLL_PT = FL_NMAX / FLL_THREADS;  // input values per thread
+
+template <int S, bool C64OUT>
+__global__ __launch_bounds__(FLL_THREADS) void k_fft64_long(const double2 *__restrict__ in,
+                                                            void *__restrict__ out,
+                                                            const double *__restrict__ dec,
+                                                            const double2 *__restrict__ tw,
+                                                            int nlines, FlPlan p) {
+    extern __shared__ double2 fl_buf[];
+    const int n = p.n, nin = p.nin, tid = threadIdx.x;
+    const int half = nin / 2, gap0 = nin - half;
+    double2 nxt[FLL_PT];
+    auto load = [&](int line) {
+        const double2 *src = in + (int64_t)line * nin;
+#pragma unroll
+        for (int i = 0; i < FLL_PT; ++i) {
+            const int e = tid + i * FLL_THREADS;
+            nxt[i] = e < nin ? src[e] : make_double2(0.0, 0.0);
+        }
+    };
+    int line = blockIdx.x;
+    if (line < nlines) load(line);
+    for (; line < nlines; line += gridDim.x) {
+        for (int e = tid; e < n - nin; e += FLL_THREADS) fl_buf[gap0 + e] = make_double2(0.0, 0.0);
+#pragma unroll
+        for (int i = 0; i < FLL_PT; ++i) {
+            const int e = tid + i * FLL_THREADS;
+            if (e < nin) {
+                double2 v = nxt[i];
+                if (dec) v = dscale(v, dec[e]);
+                fl_buf[e < half ? e - half + n : e - half] = v;
+            }
+        }
+        __syncthreads();
+        const int nl = line + gridDim.x;
+        if (nl < nlines) load(nl);
+        for (int st = 0; st < p.nst; ++st) {
+            const int Ns = p.ns[st];
+            const float rNs = p.rns[st];
+            switch (p.rad[st]) {
+                case 8: fl_stage<S, 8, FLL_THREADS, FL_NMAX>(fl_buf, tw, n, 0, 1, Ns, rNs, tid); break;
+                case 4: fl_stage<S, 4, FLL_THREADS, FL_NMAX>(fl_buf, tw, n, 0, 1, Ns, rNs, tid); break;
+                case 2: fl_stage<S, 2, FLL_THREADS, FL_NMAX>(fl_buf, tw, n, 0, 1, Ns, rNs, tid); break;
+                case 3: fl_stage<S, 3, FLL_THREADS, FL_NMAX>(fl_buf, tw, n, 0, 1, Ns, rNs, tid); break;
+                default: fl_stage<S, 5, FLL_THREADS, FL_NMAX>(fl_buf, tw, n, 0, 1, Ns, rNs, tid); break;
+            }
+        }
+        const int64_t base = (int64_t)line * n;
+        for (int e = tid; e < n; e += FLL_THREADS) {
+            const double2 v = fl_buf[e];
+            if constexpr (C64OUT)
+                reinterpret_cast<float2 *>(out)[base + e] = make_float2((float)v.x, (float)v.y);
+            else
+                reinterpret_cast<double2 *>(out)[base + e] = v;
+        }
+        __syncthreads();  // the stores have read fl_buf before the next fill
+    }
+}
+
 // tw[m] = exp(S 2 pi i m / n)
 __global__ void k_fl_twiddles(double2 *tw, int n, int S) {
     const int m = blockIdx.x * blockDim.x + threadIdx.x;
@@ -425,6 +492,22 @@ int mn_fft64_lines(int64_t A, int64_t nin, int64_t B, int64_t n, int isign, cons
     if (rc) return rc;
     const size_t lds = sizeof(double2) * (size_t)n * (size_t)p.ts;
     MN_REQUIRE(lds <= (size_t)max_lds_per_block(), "fft64_lines: line does not fit in LDS");
+    if (longl && B == 1 && Bo == 1) {
+        int dev = 0, ncu = 0;
+        MN_HIP_CHECK(hipGetDevice(&dev));
+        MN_HIP_CHECK(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
+        const int nwg = (int)std::min<int64_t>(nlines, std::max(1, ncu));
+        auto lk = S > 0 ? (out_c64 ? k_fft64_long<1, true> : k_fft64_long<1, false>)
+                        : (out_c64 ? k_fft64_long<-1, true> : k_fft64_long<-1, false>);
+        const size_t llds = sizeof(double2) * (size_t)n;
+        if (llds > 65536)
+            MN_HIP_CHECK(hipFuncSetAttribute((const void *)lk,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)llds));
+        lk<<<(unsigned)nwg, FLL_THREADS, llds, s>>>(static_cast<const double2 *>(in), out, dec, tw,
+                                                    nlines, p);
+        MN_LAUNCH_CHECK("fft64_lines (long)");
+        return MN_OK;
+    }
     using K = void (*)(const double2 *, void *, const double *, const double2 *, int, int, int,
                        int, FlPlan);
     K kern;
