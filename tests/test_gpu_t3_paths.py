@@ -12,7 +12,10 @@
   grids (partial and wrapping bins, w up to 16, clustered points), in
   isolation and through the type-3 plan, and the plan's spread selection;
 * the direct gather equals the staged gather and the oracle's fp64 interp
-  (footprints wrapping on every face), and the plan's gather selection.
+  (footprints wrapping on every face), and the plan's gather selection;
+* moving sources: set_sources within a planned source_extent (P changing,
+  both backends, both spreads) equals a fresh plan, and sources past the
+  extent's guard band raise.
 """
 
 import numpy as np
@@ -339,3 +342,36 @@ def test_type3_reversed_axis_pipeline(oracle, mn, monkeypatch):
         err = oracle.rel_l2(fl[idx], oracle.dft_t3(x, c, s, isign, idx=idx))
         print(f"  isign={isign} n_up={pl.n_up} rel_l2={err:.3e}", flush=True)
         assert err < 1e-4
+
+
+@pytest.mark.parametrize("spread", ["owner", "tiles"])
+def test_type3_set_sources(spread, oracle, mn, monkeypatch):
+    """Moving sources (ref: gpu_t3.py:444-506): a plan sized with
+    source_extent takes new frames (P may change) and equals a fresh plan of
+    the same extent; sources past the extent plus the guard band raise."""
+    print(f"case t3 set_sources spread={spread}", flush=True)
+    monkeypatch.setenv("MN_T3_SPREAD", spread)
+    rng = np.random.default_rng(11)
+    ext = [(-2.2, 2.2)] * 3
+    s = tuple(rng.uniform(-15.0, 15.0, 20_000) for _ in range(3))
+    x1 = tuple(rng.uniform(-2.0, 2.0, 30_000) for _ in range(3))
+    p = mn.Type3Plan(x1, s, eps=1e-6, isign=-1, source_extent=ext)
+    assert p.spread_owner == (spread == "owner")
+    for P, backend in [(30_000, "host"), (45_000, "gpu"), (12_345, "host")]:
+        x2 = tuple(rng.uniform(-2.2, 2.2, P) for _ in range(3))
+        c2 = (rng.standard_normal(P) + 1j * rng.standard_normal(P)).astype(np.complex64)
+        p.set_sources(x2, backend=backend)
+        assert p.P == P
+        f = p.execute(c2)
+        fresh = mn.Type3Plan(x2, s, eps=1e-6, isign=-1, source_extent=ext).execute(c2)
+        assert oracle.rel_l2(f, fresh) < 1e-6
+        idx = np.random.default_rng(P).choice(s[0].size, 300, replace=False)
+        err = oracle.rel_l2(f[idx], oracle.dft_t3(x2, c2, s, -1, idx=idx))
+        print(f"  P={P} backend={backend} rel_l2={err:.3e}", flush=True)
+        assert err < 1e-4
+    far = tuple(v.copy() for v in x1)
+    far[1][7] = 3.5  # past 2.2 + guard
+    with pytest.raises(ValueError):
+        p.set_sources(far)
+    with pytest.raises(ValueError):
+        p.set_sources(x1, backend="cuda")
