@@ -354,3 +354,31 @@ def test_type2_3d_sparse_direct_gather(isign, oracle, mn):
     assert err <= max(eps, 2 * ref_err)
     pd = mn.Type2PlanND(tuple(_pts(rng, 3, 600_000)), (32, 32, 32), eps=1e-5, isign=isign)
     assert not pd._gather_direct()
+
+
+@pytest.mark.parametrize("dim,N", [(1, (200,)), (2, (64, 48)), (3, (32, 24, 20))])
+def test_execute_disjoint(dim, N, oracle, mn):
+    """ref: nd.py:796-855. G transforms of disjoint point subsets of one plan
+    equal fresh plans of each subset (an empty group gives zeros) and the
+    direct sum, after a re-point that changes P."""
+    print(f"case execute_disjoint dim={dim}", flush=True)
+    rng = np.random.default_rng(47 + dim)
+    eps = 1e-5
+    p = mn.Type1PlanND(tuple(_pts(rng, dim, 9_000)), N, eps=eps)
+    M = 12_000
+    x = _pts(rng, dim, M)
+    p.set_sources(tuple(x))
+    c = _cplx(rng, M)
+    groups = rng.choice([0, 1, 3], M)          # group 2 stays empty
+    out = np.asarray(p.execute_disjoint(c, groups))
+    assert out.shape == (4, *N)
+    assert np.abs(out[2]).max() == 0.0
+    modes = [np.arange(-(n // 2), n - n // 2) for n in N]
+    for g in (0, 1, 3):
+        sel = groups == g
+        xs = [v[sel] for v in x]
+        fresh = mn.Type1PlanND(tuple(xs), N, eps=eps).execute(c[sel])
+        assert oracle.rel_l2(out[g], fresh) < 1e-5
+        fe = oracle.dft_t1(xs, c[sel], modes, +1)
+        ref_err = oracle.rel_l2(oracle.nufft_t1(xs, c[sel], N, eps, +1), fe)
+        assert oracle.rel_l2(out[g], fe) <= max(eps, 2 * ref_err)
