@@ -11,7 +11,9 @@ ref: harness/test_large_t3_batch.py:68-140:
 * single execute at n_up = (10800, 10800, 24), 2.8e9 cells: every grid index
   on the path is past 2^31;
 * execute_batch with three channels at n_up = (2700, 2700, 24) and at
-  (7200, 7200, 24), each channel against its own direct sum.
+  (7200, 7200, 24), each channel against its own direct sum;
+* a small anisotropic case for every precision flag at eps 1e-4 .. 1e-6 and
+  the swapped-role adjoint (ref: harness/test_gpu_small.py:13-33).
 
 Every result is checked against the oracle's exact fp64 direct sum on a
 random target subset. The plan's grid sizes are checked against the sizes
@@ -106,3 +108,34 @@ def test_t3_large_execute_batch(lat, P, n_up, oracle, mn):
     finally:
         del plan
         _release(mn)
+
+
+@pytest.mark.parametrize("prec", ["crit64", "coords64", "phases64", "fp32"])
+def test_t3_small_anisotropic_precisions(prec, oracle, mn):
+    """ref: harness/test_gpu_small.py:13-33 -- a small anisotropic type-3 at
+    eps 1e-4, 1e-5, 1e-6 for each precision flag, and the adjoint convention
+    (sources and targets swapped, isign -1).
+
+    The contract bound is max(eps, 2 x the reference's own error); that
+    pipeline spreads in fp32 (ref_t3.py:168), whose error the oracle's
+    spread64=False restatement gives (2.5e-5 here at eps 1e-6). This engine
+    is also held within 3x the all-fp64 restatement's error: at eps 1e-6 the
+    complex64 inner grid's rounding, amplified by the target deconvolution,
+    puts it at about 2.3x (7.6e-6 against 3.3e-6)."""
+    print(f"case t3 small anisotropic prec={prec}", flush=True)
+    x, c, s = gen_anisotropic(64, 2000, 0.02)
+    fd = oracle.dft_t3(x, c, s, +1)
+    for eps in (1e-4, 1e-5, 1e-6):
+        f = mn.Type3Plan(x, s, eps=eps, isign=+1, prec=prec).execute(c)
+        err = oracle.rel_l2(f, fd)
+        ref64 = oracle.rel_l2(oracle.nufft_t3(x, c, s, eps, +1), fd)
+        ref32 = oracle.rel_l2(oracle.nufft_t3(x, c, s, eps, +1, spread64=False), fd)
+        print(f"  eps={eps:.0e} err={err:.3e} fp64 restatement {ref64:.3e} "
+              f"fp32-spread restatement {ref32:.3e}", flush=True)
+        assert err <= max(eps, 2 * ref32)
+        assert err <= max(eps, 3 * ref64)
+    if prec == "crit64":
+        ones = np.ones(s[0].size)
+        fa = mn.Type3Plan(s, x, eps=1e-5, isign=-1).execute(ones.astype(np.complex64))
+        fa_ref = oracle.dft_t3(s, ones + 0j, x, -1)
+        assert oracle.rel_l2(fa, fa_ref) < 1e-4
