@@ -119,9 +119,10 @@ def test_t3_small_anisotropic_precisions(prec, oracle, mn):
     The contract bound is max(eps, 2 x the reference's own error); that
     pipeline spreads in fp32 (ref_t3.py:168), whose error the oracle's
     spread64=False restatement gives (2.5e-5 here at eps 1e-6). This engine
-    is also held within 3x the all-fp64 restatement's error: at eps 1e-6 the
-    complex64 inner grid's rounding, amplified by the target deconvolution,
-    puts it at about 2.3x (7.6e-6 against 3.3e-6)."""
+    is also held within 3x the all-fp64 restatement's error: at eps 1e-6 it
+    sits at about 2.3x (7.6e-6 against 3.3e-6). A complex128 inner grid
+    leaves that unchanged, so the grid's complex64 rounding is not the
+    cause."""
     print(f"case t3 small anisotropic prec={prec}", flush=True)
     x, c, s = gen_anisotropic(64, 2000, 0.02)
     fd = oracle.dft_t3(x, c, s, +1)
