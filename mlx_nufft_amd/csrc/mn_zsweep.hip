@@ -290,6 +290,28 @@ __device__ __forceinline__ ZPoint zp_next(SweepCursor &k, const ZFetch zf, int l
     return q;
 }
 
+// Workgroup index -> (column block bx, by; z-segment seg). The segment
+// varies slowest; within a segment the blocks go in bands of ZS_BAND
+// consecutive bx rows, bx fastest inside a band. The -x, -y and -xy
+// neighbours of a block, which read the same reaching points, are then
+// dispatched at most ZS_BAND + 1 workgroups earlier (except across a band
+// edge) and run on the same XCD at about the same z. Measured on MI355X with
+// 2e7 uniform points on a 512^3 grid: 18 % less HBM fetch than the
+// segment-fastest order, and the same time within noise (the kernel is
+// bound by instruction issue).
+constexpr int ZS_BAND = 16;
+__device__ __forceinline__ void zs_block(int64_t wid, int nbx, int nby, int &bx, int &by,
+                                         int &seg) {
+    const int64_t plane = (int64_t)nbx * nby;
+    seg = (int)(wid / plane);
+    const int64_t r = wid % plane, bandc = (int64_t)ZS_BAND * nby;
+    const int b0 = (int)(r / bandc) * ZS_BAND;
+    const int tx = min(ZS_BAND, nbx - b0);
+    const int local = (int)(r % bandc);
+    by = local / tx;
+    bx = b0 + local % tx;
+}
+
 template <int W>
 __global__ __launch_bounds__(64) void k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby,
                                                       int zseg, int nseg, float bl2e,
@@ -310,11 +332,8 @@ __global__ __launch_bounds__(64) void k_spread_zsweep(int n0, int n1, int n2, in
     constexpr uint32_t kPad = 64u * REC * 4u;  // byte offset of the zero row
     __shared__ float2 stage[ZST][64];
     __shared__ ZRanges<ZCH> rg;
-    const int64_t nw = (int64_t)nbx * nby * nseg;
-    int64_t wid = xcd_remap(blockIdx.x, nw);
-    const int seg = (int)(wid % nseg);
-    wid /= nseg;
-    const int by = (int)(wid % nby), bx = (int)(wid / nby);
+    int bx, by, seg;
+    zs_block(xcd_remap(blockIdx.x, (int64_t)nbx * nby * nseg), nbx, nby, bx, by, seg);
     const int z0 = seg * zseg, zend = min(z0 + zseg, n2);
     const int lane = threadIdx.x, grp = lane >> 4;
     const int cxl = lane_cx(lane), cyl = lane_cy(lane);
@@ -594,11 +613,8 @@ __global__ __launch_bounds__(64) ZM_WPE void k_spread_zsweep_mfma(
     __shared__ SweepRanges<ZG * NR> rg;
     __shared__ uint8_t qidx[64];
     constexpr uint32_t kPad = 64u * MREC * 4u;  // byte offset of the zero row
-    const int64_t nw = (int64_t)nbx * nby * nseg;
-    int64_t wid = xcd_remap(blockIdx.x, nw);
-    const int seg = (int)(wid % nseg);
-    wid /= nseg;
-    const int by = (int)(wid % nby), bx = (int)(wid / nby);
+    int bx, by, seg;
+    zs_block(xcd_remap(blockIdx.x, (int64_t)nbx * nby * nseg), nbx, nby, bx, by, seg);
     const int z0 = seg * zseg, zend = min(z0 + zseg, n2);
     const int lane = threadIdx.x, li = lane & 15, lk = lane >> 4;
     if (lane < MREC) table[64 * MREC + lane] = 0.f;
