@@ -55,8 +55,14 @@ def bin_sizes(dim, w, n_up, cell_bytes=SPREAD_CELL_BYTES):
     elif cell_bytes == INTERP_CELL_BYTES:
         # interp is bound by staging tiles: small bins keep about 9
         # workgroups resident per CU, which beats the smaller halo re-read of
-        # big tiles (MI355X, 3D type 2 at 512^3: 2.0 ms at m = 8, 3.1 ms at 16)
-        m = [8, 8, 8]
+        # big tiles (MI355X, 3D type 2 at 512^3: 2.0 ms at m = 8, 3.1 ms at
+        # 16). Along z (the contiguous axis) the padded tile row is made 17
+        # cells for w >= 5: rows of 16 (and 12) cells put the lane pairs'
+        # LDS reads on conflicting banks. Type-2 execute, 2e7 points on
+        # 512^3, m = (8, 8, m2): w = 5: 2.11 ms at m2 = 8, 1.94 at 13;
+        # w = 6: 2.44 at 8, 2.35 at 12, 3.07 at 11; w = 7: 3.13 at 8, 3.03
+        # at 11, 4.19 at 10. At w = 4, 8 is best within 2 %.
+        m = [8, 8, max(8, 18 - w) if w >= 5 else 8]
     else:
         side = int(round((budget / cell_bytes) ** (1.0 / 3.0) - 1e-9))
         while cell_bytes * side ** 3 > budget:
