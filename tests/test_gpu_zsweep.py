@@ -111,6 +111,24 @@ def test_zsweep_clustered_and_wrapping(kernel, oracle, mn, monkeypatch):
 
 
 @pytest.mark.parametrize("kernel", KERNELS)
+def test_zsweep_partial_band(kernel, oracle, mn, monkeypatch):
+    """Workgroups go segment-major in bands of 16 block rows along x: a grid
+    of more than 16 block rows that is not a multiple of 16 ends in a partial
+    band, and three z-segments repeat the bands. Every cell must still be
+    written exactly once."""
+    print(f"case zsweep partial band kernel={kernel}", flush=True)
+    monkeypatch.setenv("MN_ZSWEEP_KERNEL", kernel)
+    rng = np.random.default_rng(27)
+    M = 30_000
+    x = [rng.uniform(-np.pi, np.pi, M) for _ in range(3)]
+    c = (rng.standard_normal(M) + 1j * rng.standard_normal(M)).astype(np.complex64)
+    p = _grid_check(oracle, mn, x, c, (76, 20, 150), 1e-5)
+    nbx = p.n_up[0] // 8
+    assert nbx > 16 and nbx % 16 != 0, p.n_up
+    assert p.n_up[2] > 2 * 128, p.n_up
+
+
+@pytest.mark.parametrize("kernel", KERNELS)
 def test_zsweep_partial_segment(kernel, oracle, mn, monkeypatch):
     """A z extent (n2 = 300) that is not a multiple of the 128-cell segment."""
     print(f"case zsweep partial segment kernel={kernel}", flush=True)
