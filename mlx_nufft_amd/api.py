@@ -1,4 +1,4 @@
-"""finufft-compatible API (drop-in mirror of the reference's surface).
+"""finufft-style functional and Plan surface over the engine's plans.
 
     import mlx_nufft_amd as finufft
     fk = finufft.nufft2d1(x, y, c, (N1, N2), eps=1e-6)
@@ -6,18 +6,28 @@
     plan.setpts(x, y)
     fk = plan.execute(c)
 
-Semantics follow the reference (ref: mlx_nufft/api.py:1-388), itself a
-mirror of finufft 2.x: modeord=0 mode boxes (even or odd N), isign >= 0
-means +i (type 1/3 default +1, type 2 default -1), a leading n_trans axis
-on strengths/modes, out= filled in place and returned, complex128 in ->
-complex128 out, eps below 1e-6 clamped with a warning, modeord=1 raises
-NotImplementedError, 1D/2D type 3 run as degenerate 3D type 3.
+The public names, signatures, defaults, option keywords and exception
+classes are the reference's interface (ref: mlx_nufft/api.py:167-388), which
+mirrors finufft 2.x: modeord=0 mode boxes (even or odd N); isign >= 0 means
++i (type 1 and 3 default +1, type 2 default -1); a leading n_trans axis on
+strengths and mode arrays; out= filled in place and returned; complex128 or
+float64 data in gives complex128 out; eps below 1e-6 is raised to 1e-6 with
+a warning (the fp32 pipeline's floor); modeord=1 raises
+NotImplementedError; 1D and 2D type 3 run as 3D type 3 with zero
+coordinates on the missing axes.
 
-Plan.execute with n_trans > 1 runs one batched spread + batched FFT for
-type 1 (the reference loops single transforms, api.py:342).
+Below that interface the module is organised around three pieces:
+- `_Options`, the keyword options parsed once per call or plan;
+- `_KINDS`, one entry per transform type saying how it builds an engine
+  plan, what data it takes, how it runs n vectors and what its adjoint is;
+- `_deliver`, which turns the stacked device result into the caller's
+  array (dtype, squeezed single vector, out=).
+Many vectors run as one batched engine call where the engine has one
+(type-1 execute_batch, type-3 execute_batch); the reference loops.
 """
 
 import warnings
+from dataclasses import dataclass
 
 import numpy as np
 import torch
@@ -25,352 +35,409 @@ import torch
 from .nd import Type1PlanND, Type2PlanND
 from .t3 import GpuT3Plan
 
-_EPS_FLOOR = 1e-6
-_IGNORED_OPTS = {
+_MIN_EPS = 1e-6
+
+# finufft options that tune its CPU library (threads, sorting and kernel
+# evaluation heuristics, debug output). They have no meaning here and are
+# accepted silently, as the reference does.
+_CPU_LIBRARY_OPTIONS = frozenset((
     "nthreads", "debug", "spread_debug", "showwarn", "fftw", "spread_sort",
-    "spread_kerevalmeth", "spread_kerpad", "chkbnds", "maxbatchsize",
-    "spread_thread", "spread_nthr_atomic", "spread_max_sp_size",
-}
+    "spread_kerevalmeth", "spread_kerpad", "chkbnds", "maxbatchsize", "spread_thread",
+    "spread_nthr_atomic", "spread_max_sp_size",
+))
 
 
-def _check_opts(kwargs):
-    """ref: api.py:47-61."""
-    opts = dict(kwargs)
-    if opts.pop("modeord", 0) not in (0,):
-        raise NotImplementedError("modeord=1 (FFT ordering) not implemented")
-    upsampfac = opts.pop("upsampfac", None)
-    if upsampfac in (0, 0.0):
-        upsampfac = None
-    prec = opts.pop("prec", "crit64")
-    fft_backend = opts.pop("fft_backend", "mlx")
-    for k in list(opts):
-        if k in _IGNORED_OPTS:
-            opts.pop(k)
-    if opts:
-        warnings.warn(f"mlx-nufft: ignoring unknown options {sorted(opts)}")
-    return upsampfac, prec, fft_backend
+@dataclass(frozen=True)
+class _Options:
+    """Keyword options of one call or plan, after validation."""
+
+    eps: float
+    upsampfac: object   # None: the engine plan's own default
+    prec: str
+    fft_backend: str
+
+    @classmethod
+    def parse(cls, eps, kwargs):
+        opts = dict(kwargs)
+        if opts.pop("modeord", 0) != 0:
+            raise NotImplementedError("modeord=1 (FFT-ordered modes) is not supported; "
+                                      "use modeord=0")
+        sigma = opts.pop("upsampfac", None)
+        if sigma == 0:
+            sigma = None   # finufft's "choose for me"
+        prec = opts.pop("prec", "crit64")
+        backend = opts.pop("fft_backend", "mlx")
+        unknown = sorted(k for k in opts if k not in _CPU_LIBRARY_OPTIONS)
+        if unknown:
+            warnings.warn(f"mlx_nufft_amd: unrecognised options {unknown} have no effect")
+        eps = float(eps)
+        if eps < _MIN_EPS:
+            warnings.warn(f"mlx_nufft_amd: eps={eps:g} lies below what the fp32 pipeline "
+                          f"can deliver; running at eps={_MIN_EPS:g}")
+            eps = _MIN_EPS
+        return cls(eps, sigma, prec, backend)
+
+    def sigma_kw(self):
+        return {} if self.upsampfac is None else {"upsampfac": self.upsampfac}
 
 
-def _norm_eps(eps):
-    """ref: api.py:64-71."""
-    eps = float(eps)
-    if eps < _EPS_FLOOR:
-        warnings.warn(f"mlx-nufft: eps={eps:g} is below the fp32 pipeline floor; clamping to "
-                      f"{_EPS_FLOOR:g}")
-        eps = _EPS_FLOOR
-    return eps
-
-
-def _norm_isign(isign, default):
+def _sign(isign, default):
     if isign is None:
         return default
-    return +1 if isign >= 0 else -1
+    return 1 if isign >= 0 else -1
 
 
-def _np(a):
-    return a.detach().cpu().numpy() if isinstance(a, torch.Tensor) else np.asarray(a)
+def _is_wide(a):
+    """complex128/float64 data asks for complex128 results."""
+    dt = a.dtype if isinstance(a, torch.Tensor) else np.asarray(a).dtype
+    return dt in (np.complex128, np.float64, torch.complex128, torch.float64)
 
 
-def _out_dtype(*arrays):
-    """ref: api.py:80-84."""
-    for a in arrays:
-        dt = a.dtype if isinstance(a, torch.Tensor) else np.asarray(a).dtype
-        if dt in (np.complex128, np.float64, torch.complex128, torch.float64):
-            return np.complex128
-    return np.complex64
+def _ndim(a):
+    return a.dim() if isinstance(a, torch.Tensor) else np.ndim(a)
 
 
-def _vec_shape(data, inner_ndim, inner_shape=None):
-    """Split into (n_trans, stacked data); strict trailing-shape check.
-    ref: api.py:87-102."""
-    data = _np(data)
-    if data.ndim == inner_ndim:
-        out = 1, data[None, ...]
-    elif data.ndim == inner_ndim + 1:
-        out = data.shape[0], data
+def _shape(a):
+    return tuple(a.shape) if isinstance(a, torch.Tensor) else np.shape(a)
+
+
+def _size(a):
+    return a.numel() if isinstance(a, torch.Tensor) else np.size(a)
+
+
+def _host_f64(a):
+    if isinstance(a, torch.Tensor):
+        a = a.detach().cpu().numpy()
+    return np.asarray(a, dtype=np.float64).ravel()
+
+
+def _as_3d(coords, dim):
+    """Coordinates of a dim < 3 type-3 problem as 3 arrays (zeros appended)."""
+    arrs = [_host_f64(a) for a in coords]
+    return tuple(arrs) + tuple(np.zeros(arrs[0].size) for _ in range(3 - dim))
+
+
+def _vectors(data, rank, inner=None):
+    """data as (n, single): n vectors of `rank` dims each; single says the
+    caller passed one unstacked vector. The inner shape must equal `inner`
+    when given (no silent truncation)."""
+    nd = _ndim(data)
+    if nd == rank:
+        n, single = 1, True
+        shape = _shape(data)
+    elif nd == rank + 1:
+        n, single = _shape(data)[0], False
+        shape = _shape(data)[1:]
     else:
-        raise ValueError(f"data must have {inner_ndim} or {inner_ndim + 1} dims, got shape "
-                         f"{data.shape}")
-    if inner_shape is not None and out[1].shape[1:] != tuple(inner_shape):
-        raise ValueError(f"data inner shape {out[1].shape[1:]} must be {tuple(inner_shape)}")
+        raise ValueError(f"expected data with {rank} dims (one vector) or {rank + 1} "
+                         f"(a stack of vectors); got shape {_shape(data)}")
+    if inner is not None and tuple(shape) != tuple(inner):
+        raise ValueError(f"each data vector must have shape {tuple(inner)}, got "
+                         f"{tuple(shape)}")
+    return int(n), single
+
+
+def _stack_view(data, rank):
+    """data with a leading vector axis (a view when possible)."""
+    if _ndim(data) == rank:
+        return data[None] if isinstance(data, torch.Tensor) else np.asarray(data)[None]
+    return data if isinstance(data, torch.Tensor) else np.asarray(data)
+
+
+def _deliver(res, single, dtype, out):
+    """Device result (n, ...) -> the caller's array: one D2H copy, squeezed
+    for a single vector, cast to dtype, copied into out= when given (and out
+    itself returned)."""
+    host = res.detach().cpu().numpy()
+    if single:
+        host = host[0]
+    host = host.astype(dtype, copy=False)
+    if out is None:
+        return host
+    oshape = tuple(out.shape)
+    if oshape not in (host.shape, (1,) + host.shape) and (1,) + oshape != host.shape:
+        raise ValueError(f"out has shape {oshape}; the result has shape {host.shape}")
+    np.copyto(out, host.reshape(oshape))
     return out
 
 
-def _fill_out(out, res, dtype):
-    """ref: api.py:105-115."""
-    res = res.astype(dtype, copy=False)
-    if out is not None:
-        if out.shape != res.shape and out.shape != (1,) + res.shape \
-                and (1,) + out.shape != res.shape:
-            raise ValueError(f"out.shape {out.shape} does not match result shape {res.shape}")
-        np.copyto(out, res.reshape(out.shape))
-        return out
-    return res
+# ---------------------------------------------------------------------------
+# The three transform kinds
 
 
-def _embed3(arrs, dim):
-    """Zero-pad a dim<3 coordinate tuple to 3 components (ref: api.py:118-122)."""
-    arrs = [_np(a).astype(np.float64).ravel() for a in arrs]
-    z = np.zeros(arrs[0].size)
-    return tuple(arrs) + (z,) * (3 - dim)
+class _Type1:
+    """Nonuniform points -> modes."""
+
+    code = 1
+    default_isign = +1
+    adjoint_code = 2
+
+    @staticmethod
+    def rank(dim):
+        return 1
+
+    @staticmethod
+    def build(dim, coords, targets, n_modes, opts, isign):
+        if opts.fft_backend != "mlx":
+            _warn_backend(opts.fft_backend, "type 1")
+        return Type1PlanND(tuple(coords), n_modes, eps=opts.eps, isign=isign, prec=opts.prec,
+                           **opts.sigma_kw())
+
+    @staticmethod
+    def inner(plan, n_modes):
+        return (plan.P,)
+
+    @staticmethod
+    def run(plan, stack, n):
+        if n == 1:
+            return plan.execute(stack[0], return_np=False)[None]
+        return plan.execute_batch(stack, return_np=False)
 
 
-def _modes_tuple(n_modes, dim, out, out_offset=0):
-    """ref: api.py:125-135."""
-    if n_modes is None:
-        if out is None:
-            raise ValueError("either n_modes or out must be supplied")
-        shape = out.shape[out_offset:]
-        if len(shape) != dim:
-            raise ValueError(f"out shape {out.shape} does not match dim {dim}")
-        return tuple(int(n) for n in shape)
+class _Type2:
+    """Modes -> nonuniform points."""
+
+    code = 2
+    default_isign = -1
+    adjoint_code = 1
+
+    @staticmethod
+    def rank(dim):
+        return dim
+
+    @staticmethod
+    def build(dim, coords, targets, n_modes, opts, isign):
+        if opts.fft_backend != "mlx":
+            _warn_backend(opts.fft_backend, "type 2")
+        return Type2PlanND(tuple(coords), n_modes, eps=opts.eps, isign=isign, prec=opts.prec,
+                           **opts.sigma_kw())
+
+    @staticmethod
+    def inner(plan, n_modes):
+        return tuple(n_modes)
+
+    @staticmethod
+    def run(plan, stack, n):
+        return torch.stack([plan.execute(stack[k], return_np=False) for k in range(n)])
+
+
+class _Type3:
+    """Nonuniform sources -> nonuniform targets."""
+
+    code = 3
+    default_isign = +1
+    adjoint_code = 3
+
+    @staticmethod
+    def rank(dim):
+        return 1
+
+    @staticmethod
+    def build(dim, coords, targets, n_modes, opts, isign):
+        if opts.upsampfac is not None and opts.upsampfac != 1.25:
+            warnings.warn("mlx_nufft_amd: type 3 always runs at upsampfac=1.25; the "
+                          "requested value has no effect")
+        return GpuT3Plan(_as_3d(coords, dim), _as_3d(targets, dim), eps=opts.eps, isign=isign,
+                         prec=opts.prec, fft_backend=opts.fft_backend)
+
+    @staticmethod
+    def inner(plan, n_modes):
+        return (plan.P,)
+
+    @staticmethod
+    def run(plan, stack, n):
+        if n == 1:
+            return plan.execute(stack[0], return_np=False)[None]
+        return plan.execute_batch(stack, return_np=False)
+
+
+_KINDS = {1: _Type1, 2: _Type2, 3: _Type3}
+
+
+def _warn_backend(backend, what):
+    warnings.warn(f"mlx_nufft_amd: fft_backend={backend!r} only concerns 3D type 3; "
+                  f"{what} uses the built-in FFT")
+
+
+def _modes_from_out(out, dim, stacked):
+    shape = tuple(out.shape)[1 if stacked else 0:]
+    if len(shape) != dim:
+        raise ValueError(f"out has shape {tuple(out.shape)}, which holds no {dim}D mode box")
+    return tuple(int(n) for n in shape)
+
+
+def _mode_box(n_modes, dim):
     if np.isscalar(n_modes):
         return (int(n_modes),) * dim
     return tuple(int(n) for n in n_modes)
 
 
-def _warn_no_vkfft(fft_backend, what):
-    if fft_backend != "mlx":
-        warnings.warn(f"mlx-nufft: fft_backend={fft_backend!r} applies only to 3D type-3 "
-                      f"(slab); ignored for {what}")
-
-
-def _t1_run(plan, cv, n_tr):
-    if n_tr == 1:
-        return plan.execute(cv[0])[None]
-    return plan.execute_batch(cv)
+def _oneshot(code, dim, coords, data, targets, n_modes, out, eps, isign, kwargs):
+    """Plan, run and deliver one finufft-style call."""
+    kind = _KINDS[code]
+    opts = _Options.parse(eps, kwargs)
+    sign = _sign(isign, kind.default_isign)
+    wide = _is_wide(data)
+    rank = kind.rank(dim)
+    if code == 2:
+        n, single = _vectors(data, rank)
+        n_modes = _shape(data)[-dim:]
+    else:
+        n, single = _vectors(data, rank, inner=(_size(coords[0]),))
+        if code == 1:
+            if n_modes is None:
+                if out is None:
+                    raise ValueError("type 1 needs n_modes, or out= to take the mode box from")
+                n_modes = _modes_from_out(out, dim, stacked=n > 1)
+            n_modes = _mode_box(n_modes, dim)
+    plan = kind.build(dim, coords, targets, n_modes, opts, sign)
+    res = kind.run(plan, _stack_view(data, rank), n)
+    return _deliver(res, single, np.complex128 if wide else np.complex64, out)
 
 
 # ---------------------------------------------------------------------------
-# type 1
-
-
-def _nufft_t1(dim, coords, c, n_modes, out, eps, isign, kwargs):
-    """ref: api.py:148-164."""
-    upsampfac, prec, fft_backend = _check_opts(kwargs)
-    _warn_no_vkfft(fft_backend, "type-1")
-    eps = _norm_eps(eps)
-    isign = _norm_isign(isign, +1)
-    dtype = _out_dtype(c)
-    M = _np(coords[0]).size
-    n_tr, cv = _vec_shape(c, 1, inner_shape=(M,))
-    if out is not None and n_modes is None:
-        n_modes = _modes_tuple(None, dim, out, out_offset=(1 if n_tr > 1 else 0))
-    N = _modes_tuple(n_modes, dim, out)
-    kw = {} if upsampfac is None else {"upsampfac": upsampfac}
-    plan = Type1PlanND(coords, N, eps=eps, isign=isign, prec=prec, **kw)
-    res = _t1_run(plan, cv, n_tr)
-    if n_tr == 1 and _np(c).ndim == 1:
-        res = res[0]
-    return _fill_out(out, res, dtype)
+# finufft-style functions (signatures and defaults: ref api.py:167-251)
 
 
 def nufft1d1(x, c, n_modes=None, out=None, eps=1e-6, isign=1, **kwargs):
-    """1D type-1: f[k] = sum_j c[j] exp(+/-i k x(j))."""
-    return _nufft_t1(1, (x,), c, n_modes, out, eps, isign, kwargs)
+    """1D type 1: f[k] = sum_j c[j] exp(+/-i k x[j])."""
+    return _oneshot(1, 1, (x,), c, None, n_modes, out, eps, isign, kwargs)
 
 
 def nufft2d1(x, y, c, n_modes=None, out=None, eps=1e-6, isign=1, **kwargs):
-    """2D type-1: f[k1,k2] = sum_j c[j] exp(+/-i (k1 x(j) + k2 y(j)))."""
-    return _nufft_t1(2, (x, y), c, n_modes, out, eps, isign, kwargs)
+    """2D type 1: f[k1,k2] = sum_j c[j] exp(+/-i (k1 x[j] + k2 y[j]))."""
+    return _oneshot(1, 2, (x, y), c, None, n_modes, out, eps, isign, kwargs)
 
 
 def nufft3d1(x, y, z, c, n_modes=None, out=None, eps=1e-6, isign=1, **kwargs):
-    """3D type-1: f[k1,k2,k3] = sum_j c[j] exp(+/-i k . x_j)."""
-    return _nufft_t1(3, (x, y, z), c, n_modes, out, eps, isign, kwargs)
-
-
-# ---------------------------------------------------------------------------
-# type 2
-
-
-def _nufft_t2(dim, coords, f, out, eps, isign, kwargs):
-    """ref: api.py:186-199."""
-    upsampfac, prec, fft_backend = _check_opts(kwargs)
-    _warn_no_vkfft(fft_backend, "type-2")
-    eps = _norm_eps(eps)
-    isign = _norm_isign(isign, -1)
-    dtype = _out_dtype(f)
-    n_tr, fv = _vec_shape(f, dim)
-    N = fv.shape[1:]
-    kw = {} if upsampfac is None else {"upsampfac": upsampfac}
-    plan = Type2PlanND(coords, N, eps=eps, isign=isign, prec=prec, **kw)
-    res = np.stack([plan.execute(fv[t]) for t in range(n_tr)])
-    if n_tr == 1 and _np(f).ndim == dim:
-        res = res[0]
-    return _fill_out(out, res, dtype)
+    """3D type 1: f[k] = sum_j c[j] exp(+/-i k . (x[j], y[j], z[j]))."""
+    return _oneshot(1, 3, (x, y, z), c, None, n_modes, out, eps, isign, kwargs)
 
 
 def nufft1d2(x, f, out=None, eps=1e-6, isign=-1, **kwargs):
-    """1D type-2: c[j] = sum_k f[k] exp(+/-i k x(j))."""
-    return _nufft_t2(1, (x,), f, out, eps, isign, kwargs)
+    """1D type 2: c[j] = sum_k f[k] exp(+/-i k x[j])."""
+    return _oneshot(2, 1, (x,), f, None, None, out, eps, isign, kwargs)
 
 
 def nufft2d2(x, y, f, out=None, eps=1e-6, isign=-1, **kwargs):
-    """2D type-2: c[j] = sum_{k1,k2} f[k1,k2] exp(+/-i (k1 x(j) + k2 y(j)))."""
-    return _nufft_t2(2, (x, y), f, out, eps, isign, kwargs)
+    """2D type 2: c[j] = sum_{k1,k2} f[k1,k2] exp(+/-i (k1 x[j] + k2 y[j]))."""
+    return _oneshot(2, 2, (x, y), f, None, None, out, eps, isign, kwargs)
 
 
 def nufft3d2(x, y, z, f, out=None, eps=1e-6, isign=-1, **kwargs):
-    """3D type-2: c[j] = sum_k f[k] exp(+/-i k . x_j)."""
-    return _nufft_t2(3, (x, y, z), f, out, eps, isign, kwargs)
-
-
-# ---------------------------------------------------------------------------
-# type 3
-
-
-def _nufft_t3(dim, src, c, trg, out, eps, isign, kwargs):
-    """ref: api.py:221-236."""
-    upsampfac, prec, fft_backend = _check_opts(kwargs)
-    if upsampfac is not None and upsampfac != 1.25:
-        warnings.warn("mlx-nufft: type-3 runs the validated sigma=1.25 pipeline; "
-                      "upsampfac ignored")
-    eps = _norm_eps(eps)
-    isign = _norm_isign(isign, +1)
-    dtype = _out_dtype(c)
-    M = _np(src[0]).size
-    n_tr, cv = _vec_shape(c, 1, inner_shape=(M,))
-    plan = GpuT3Plan(_embed3(src, dim), _embed3(trg, dim), eps=eps, isign=isign, prec=prec,
-                     fft_backend=fft_backend)
-    res = np.stack([plan.execute(cv[t]) for t in range(n_tr)])
-    if n_tr == 1 and _np(c).ndim == 1:
-        res = res[0]
-    return _fill_out(out, res, dtype)
+    """3D type 2: c[j] = sum_k f[k] exp(+/-i k . (x[j], y[j], z[j]))."""
+    return _oneshot(2, 3, (x, y, z), f, None, None, out, eps, isign, kwargs)
 
 
 def nufft1d3(x, c, s, out=None, eps=1e-6, isign=1, **kwargs):
-    """1D type-3: f[k] = sum_j c[j] exp(+/-i s[k] x[j])."""
-    return _nufft_t3(1, (x,), c, (s,), out, eps, isign, kwargs)
+    """1D type 3: f[k] = sum_j c[j] exp(+/-i s[k] x[j])."""
+    return _oneshot(3, 1, (x,), c, (s,), None, out, eps, isign, kwargs)
 
 
 def nufft2d3(x, y, c, s, t, out=None, eps=1e-6, isign=1, **kwargs):
-    """2D type-3: f[k] = sum_j c[j] exp(+/-i (s[k] x[j] + t[k] y[j]))."""
-    return _nufft_t3(2, (x, y), c, (s, t), out, eps, isign, kwargs)
+    """2D type 3: f[k] = sum_j c[j] exp(+/-i (s[k] x[j] + t[k] y[j]))."""
+    return _oneshot(3, 2, (x, y), c, (s, t), None, out, eps, isign, kwargs)
 
 
 def nufft3d3(x, y, z, c, s, t, u, out=None, eps=1e-6, isign=1, **kwargs):
-    """3D type-3: f[k] = sum_j c[j] exp(+/-i (s,t,u)_k . (x,y,z)_j)."""
-    return _nufft_t3(3, (x, y, z), c, (s, t, u), out, eps, isign, kwargs)
+    """3D type 3: f[k] = sum_j c[j] exp(+/-i (s[k], t[k], u[k]) . (x[j], y[j], z[j]))."""
+    return _oneshot(3, 3, (x, y, z), c, (s, t, u), None, out, eps, isign, kwargs)
 
 
 # ---------------------------------------------------------------------------
-# Plan interface
+# Plan (ref api.py:258-388)
 
 
 class Plan:
-    """finufft.Plan-compatible plan/setpts/execute interface.
+    """finufft.Plan-style interface: Plan(type, n_modes_or_dim, ...), then
+    setpts(...) once per point set and execute(...) per data stack.
 
-    Plan(nufft_type, n_modes_or_dim, n_trans=1, eps=1e-6, isign=None,
-         dtype='complex128', **kwargs)
-    ref: api.py:258-388.
+    For types 1 and 2, n_modes_or_dim is the mode box (its length is the
+    dimension); for type 3 it is the dimension. setpts builds the engine
+    plan (point setup and sort run there); execute runs n_trans vectors
+    through it, and execute_adjoint runs the adjoint transform (built on
+    first use and kept until the next setpts).
     """
 
     def __init__(self, nufft_type, n_modes_or_dim, n_trans=1, eps=1e-6, isign=None,
                  dtype="complex128", **kwargs):
-        if nufft_type not in (1, 2, 3):
-            raise ValueError("nufft_type must be 1, 2 or 3")
-        self.type = int(nufft_type)
+        if nufft_type not in _KINDS:
+            raise ValueError(f"nufft_type must be 1, 2 or 3, got {nufft_type!r}")
+        self._kind = _KINDS[nufft_type]
+        self.type = self._kind.code
         self.n_trans = int(n_trans)
-        self.eps = _norm_eps(eps)
-        self.isign = _norm_isign(isign, -1 if self.type == 2 else +1)
         self.dtype = np.dtype(dtype)
         if self.dtype not in (np.complex64, np.complex128):
-            raise ValueError("dtype must be complex64 or complex128")
-        self._upsampfac, self._prec, self._fft_backend = _check_opts(kwargs)
-        if self._fft_backend != "mlx" and self.type != 3:
-            _warn_no_vkfft(self._fft_backend, f"type-{self.type}")
-            self._fft_backend = "mlx"
+            raise ValueError(f"dtype must be complex64 or complex128, got {self.dtype}")
+        self._opts = _Options.parse(eps, kwargs)
+        self.eps = self._opts.eps
+        self.isign = _sign(isign, self._kind.default_isign)
         if self.type == 3:
-            self.dim = int(n_modes_or_dim)
-            self.n_modes = None
+            self.dim, self.n_modes = int(n_modes_or_dim), None
         else:
-            if np.isscalar(n_modes_or_dim):
-                n_modes_or_dim = (n_modes_or_dim,)
-            self.n_modes = tuple(int(n) for n in n_modes_or_dim)
+            box = (n_modes_or_dim,) if np.isscalar(n_modes_or_dim) else n_modes_or_dim
+            self.n_modes = tuple(int(n) for n in box)
             self.dim = len(self.n_modes)
+            if self._opts.fft_backend != "mlx":
+                _warn_backend(self._opts.fft_backend, f"type {self.type}")
+                self._opts = _Options(self._opts.eps, self._opts.upsampfac, self._opts.prec,
+                                      "mlx")
         if self.dim not in (1, 2, 3):
-            raise ValueError("dim must be 1, 2 or 3")
+            raise ValueError(f"the dimension must be 1, 2 or 3, got {self.dim}")
         self._plan = None
         self._adjoint = None
-        self._n_targets = None
+        self._points = None    # source coordinates of the current setpts
+        self._targets = None   # type-3 target coordinates
 
     def setpts(self, x=None, y=None, z=None, s=None, t=None, u=None):
-        coords = [v for v in (x, y, z) if v is not None]
-        if len(coords) != self.dim:
-            raise ValueError(f"expected {self.dim} coordinate arrays, got {len(coords)}")
-        kw = {} if self._upsampfac is None else {"upsampfac": self._upsampfac}
-        self._adjoint = None
-        if self.type == 1:
-            self._plan = Type1PlanND(tuple(coords), self.n_modes, eps=self.eps, isign=self.isign,
-                                     prec=self._prec, **kw)
-        elif self.type == 2:
-            self._plan = Type2PlanND(tuple(coords), self.n_modes, eps=self.eps, isign=self.isign,
-                                     prec=self._prec, **kw)
-        else:
-            if self._upsampfac is not None and self._upsampfac != 1.25:
-                warnings.warn("mlx-nufft: type-3 runs the validated sigma=1.25 pipeline; "
-                              "upsampfac ignored")
-            trg = [v for v in (s, t, u) if v is not None]
+        pts = tuple(v for v in (x, y, z) if v is not None)
+        if len(pts) != self.dim:
+            raise ValueError(f"a {self.dim}D plan takes {self.dim} coordinate arrays, got "
+                             f"{len(pts)}")
+        trg = None
+        if self.type == 3:
+            trg = tuple(v for v in (s, t, u) if v is not None)
             if len(trg) != self.dim:
-                raise ValueError(f"expected {self.dim} target arrays, got {len(trg)}")
-            self._plan = GpuT3Plan(_embed3(coords, self.dim), _embed3(trg, self.dim),
-                                   eps=self.eps, isign=self.isign, prec=self._prec,
-                                   fft_backend=self._fft_backend)
-            self._n_targets = _np(trg[0]).size
-        self._coords = [_np(v) for v in coords]
-        self._targets = None if self.type != 3 else [_np(v) for v in (s, t, u) if v is not None]
+                raise ValueError(f"a {self.dim}D type-3 plan takes {self.dim} target arrays, "
+                                 f"got {len(trg)}")
+        self._plan = self._kind.build(self.dim, pts, trg, self.n_modes, self._opts, self.isign)
+        self._adjoint = None
+        self._points, self._targets = pts, trg
+
+    def _apply(self, kind, plan, data, inner, out, what):
+        rank = kind.rank(self.dim)
+        n, single = _vectors(data, rank, inner=inner)
+        if n != self.n_trans:
+            raise ValueError(f"{what} got {n} vectors; the plan was made for "
+                             f"n_trans={self.n_trans}")
+        res = kind.run(plan, _stack_view(data, rank), n)
+        return _deliver(res, single and self.n_trans == 1, self.dtype, out)
 
     def execute(self, data, out=None):
         if self._plan is None:
-            raise RuntimeError("setpts() must be called before execute()")
-        if self.type == 2:
-            inner, ishape = self.dim, self.n_modes
-        else:
-            inner, ishape = 1, (self._plan.P,)
-        n_tr, dv = _vec_shape(data, inner, inner_shape=ishape)
-        if n_tr != self.n_trans:
-            raise ValueError(f"data has {n_tr} vectors, plan has n_trans={self.n_trans}")
-        if self.type == 1:
-            res = _t1_run(self._plan, dv, n_tr)
-        else:
-            res = np.stack([self._plan.execute(dv[k]) for k in range(self.n_trans)])
-        if self.n_trans == 1 and _np(data).ndim == inner:
-            res = res[0]
-        return _fill_out(out, res, self.dtype)
+            raise RuntimeError("call setpts() before execute()")
+        inner = self._kind.inner(self._plan, self.n_modes)
+        return self._apply(self._kind, self._plan, data, inner, out, "execute")
 
     def execute_adjoint(self, data, out=None):
-        """Adjoint of the planned transform: the sibling transform with isign
-        negated (type 1 <-> type 2; type 3 with sources and targets swapped).
-        ref: api.py:347-388."""
+        """The adjoint of the planned transform: the sibling transform with
+        the opposite sign (type 1 <-> type 2 at the same points; type 3 with
+        sources and targets exchanged)."""
         if self._plan is None:
-            raise RuntimeError("setpts() must be called before execute_adjoint()")
+            raise RuntimeError("call setpts() before execute_adjoint()")
+        adj = _KINDS[self._kind.adjoint_code]
         if self._adjoint is None:
-            kw = {} if self._upsampfac is None else {"upsampfac": self._upsampfac}
-            if self.type == 1:
-                self._adjoint = Type2PlanND(tuple(self._coords), self.n_modes, eps=self.eps,
-                                            isign=-self.isign, prec=self._prec, **kw)
-            elif self.type == 2:
-                self._adjoint = Type1PlanND(tuple(self._coords), self.n_modes, eps=self.eps,
-                                            isign=-self.isign, prec=self._prec, **kw)
+            if self.type == 3:
+                self._adjoint = adj.build(self.dim, self._targets, self._points, None,
+                                          self._opts, -self.isign)
             else:
-                self._adjoint = GpuT3Plan(_embed3(self._targets, self.dim),
-                                          _embed3(self._coords, self.dim), eps=self.eps,
-                                          isign=-self.isign, prec=self._prec,
-                                          fft_backend=self._fft_backend)
+                self._adjoint = adj.build(self.dim, self._points, None, self.n_modes,
+                                          self._opts, -self.isign)
+        # the adjoint consumes what execute produces
         if self.type == 1:
-            inner, ishape = self.dim, self.n_modes
+            inner = tuple(self.n_modes)
         elif self.type == 2:
-            inner, ishape = 1, (self._plan.P,)
+            inner = (self._plan.P,)
         else:
-            inner, ishape = 1, (self._n_targets,)
-        n_tr, dv = _vec_shape(data, inner, inner_shape=ishape)
-        if n_tr != self.n_trans:
-            raise ValueError(f"data has {n_tr} vectors, plan has n_trans={self.n_trans}")
-        if self.type == 2:
-            res = _t1_run(self._adjoint, dv, n_tr)
-        else:
-            res = np.stack([self._adjoint.execute(dv[k]) for k in range(self.n_trans)])
-        if self.n_trans == 1 and _np(data).ndim == inner:
-            res = res[0]
-        return _fill_out(out, res, self.dtype)
+            inner = (self._plan.M,)
+        return self._apply(adj, self._adjoint, data, inner, out, "execute_adjoint")

@@ -32,12 +32,37 @@ def _as_coord_tuple(x):
     return tuple(x)
 
 
+class PlanArgumentError(ValueError, AssertionError):
+    """An invalid plan option. It is a ValueError; it is an AssertionError as
+    well because the reference rejects these options with assert
+    statements (ref: nd.py:399, 871; types12.py:36-37), so callers that
+    catch either keep working."""
+
+
+SPREAD_METHODS = ("auto", "od", "gm")
+
+
+def od_applicable(dim, w, n_up, P):
+    """The reference's rule for when its output-driven (bin-tiled) spread and
+    interp apply: w <= 8, at least 20000 points, and a padded bin tile of
+    m + w cells per dim (m = 2048 in 1D, 48 - w in 2D, 15 - w in 3D) that
+    fits 28 KB and the fine grid (ref: nd.py:281-305, 329). A forced
+    spread_method="od" outside it raises ValueError, as there; the engine's
+    own kernels apply more widely."""
+    if w > 8 or P < 20000:
+        return False
+    m = {1: [2048], 2: [48 - w] * 2, 3: [15 - w] * 3}[dim]
+    tile = [mi + w for mi in m]
+    return (min(m) >= 1 and 8 * int(np.prod(tile)) <= 28 * 1024
+            and all(n >= t for n, t in zip(n_up, tile)))
+
+
 class _PointsND:
     """Shared point/kernel setup for ND types 1 and 2 (ref: nd.py:94-150)."""
 
     def __init__(self, x, n_modes, eps, isign, upsampfac, prec, sort_points):
         if prec not in ("fp32", "crit64"):
-            raise ValueError("prec must be 'fp32' or 'crit64'")
+            raise PlanArgumentError("prec must be 'fp32' or 'crit64'")
         x = _as_coord_tuple(x)
         self.dim = len(x)
         if self.dim not in (1, 2, 3):
@@ -64,6 +89,12 @@ class _PointsND:
         self.profile_deferred = False
         self.last_profile = {}
         self._deferred = []
+
+        npts = x[0].numel() if isinstance(x[0], torch.Tensor) else np.size(x[0])
+        if self.spread_method == "od" and not od_applicable(self.dim, self.w, self.n_up, npts):
+            raise ValueError(f"spread_method='od' does not apply here (w={self.w}, "
+                             f"n_up={tuple(self.n_up)}, P={npts}): it needs w <= 8, "
+                             f"P >= 20000 and a fine grid at least one padded bin wide")
 
         self.device = L.require_gpu()
         x64 = self._coords(x)
@@ -202,13 +233,21 @@ class Type1PlanND(_PointsND):
     """
 
     _cell_bytes = E.SPREAD_CELL_BYTES
-    _use_zsweep = True
     _use_zstream = False
 
     def __init__(self, x, n_modes, eps=1e-6, isign=+1, upsampfac=2.0, prec="crit64",
                  sort_points=True, spread_method="auto"):
-        assert spread_method in ("auto", "od", "gm")
+        """spread_method: "auto" picks the fastest spread for the geometry
+        (3D: the owner-computes z-sweep; 2D: the y-sweep; else LDS tiles);
+        "od" does the same but first raises ValueError where the reference's
+        output-driven spread would not apply; "gm" forces the LDS-tile
+        spread with its atomic flush, this engine's counterpart of the
+        reference's global-memory atomic spread (ref: nd.py:397-404)."""
+        if spread_method not in SPREAD_METHODS:
+            raise PlanArgumentError(f"spread_method must be one of {SPREAD_METHODS}, got "
+                                    f"{spread_method!r}")
         self.spread_method = spread_method
+        self._use_zsweep = spread_method != "gm"
         super().__init__(x, n_modes, eps, isign, upsampfac, prec, sort_points)
 
     def _strengths(self, c):
@@ -328,7 +367,18 @@ class Type2PlanND(_PointsND):
 
     def __init__(self, x, n_modes, eps=1e-6, isign=-1, upsampfac=2.0, prec="crit64",
                  sort_points=False, spread_method="auto"):
-        assert spread_method in ("auto", "od", "gm")
+        """spread_method selects the interpolation: "auto" the staged-tile
+        gather (or, for 3D points sparse on their grid, the direct gather);
+        "od" the same after raising ValueError where the reference's
+        output-driven gather would not apply; "gm" the direct gather, which
+        reads each point's taps straight from the grid as the reference's
+        global-memory gather does (3D; 1D and 2D keep the tiles)
+        (ref: nd.py:869-874). sort_points is accepted for the interface: the
+        gathers always run in bin order and write results in caller order,
+        which is the order the reference returns for either value."""
+        if spread_method not in SPREAD_METHODS:
+            raise PlanArgumentError(f"spread_method must be one of {SPREAD_METHODS}, got "
+                                    f"{spread_method!r}")
         self.spread_method = spread_method
         super().__init__(x, n_modes, eps, isign, upsampfac, prec, sort_points)
 
@@ -365,5 +415,8 @@ class Type2PlanND(_PointsND):
         pts = self.pts
         if getattr(self, "_gd_pts", None) is not pts:
             self._gd_pts = pts
-            self._gd = E.interp_direct_preferred(pts, self.w, self.n_up)
+            if self.spread_method == "gm":
+                self._gd = self.dim == 3
+            else:
+                self._gd = E.interp_direct_preferred(pts, self.w, self.n_up)
         return self._gd

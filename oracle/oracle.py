@@ -265,16 +265,31 @@ def spread_f32(i1, fr, c, n, w, beta):
     return grid.astype(np.complex128)
 
 
-def nufft_t3(x, c, s, eps=1e-5, isign=+1, upsampfac=1.25, spread64=True):
-    """CPU type-3 (3D), following ref_t3.py:48-221: all stages fp64, or with
-    the spread stage in fp32 (spread64=False, the reference's most
-    precision-sensitive fp32 stage, ref: harness/diagnose_ref.py:21-41)."""
+T3_PRECISIONS = ("fp32", "coords64", "phases64", "crit64")
+
+
+def t3_setup(x, s, eps=1e-5, isign=+1, upsampfac=1.25, prec="crit64"):
+    """Type-3 plan setup (3D) as the reference's host path computes it, in
+    each precision mode: the sizing scalars (C, D, nf, h, gam, n_up;
+    ref: gpu_t3.py:326-342), the targets' cells, fractions, theta and
+    post factor (ref: gpu_t3.py:344-377) and the sources' cells, fractions
+    and prephase (ref: gpu_t3.py:474-488). prec picks the dtype of the
+    coordinate rescale (rdt: fp64 for crit64/coords64) and of the phase
+    angles (pdt: fp64 for crit64/phases64); the operation order is the
+    reference's, elementwise, so every fp32 step rounds where it does
+    there. Returned arrays are in caller order."""
+    if prec not in T3_PRECISIONS:
+        raise ValueError(prec)
+    rdt = np.float64 if prec in ("crit64", "coords64") else np.float32
+    pdt = np.float64 if prec in ("crit64", "phases64") else np.float32
     w, beta = kernel_params(eps, upsampfac)
+    isign = 1 if isign >= 0 else -1
     x = [np.asarray(v, np.float64).ravel() for v in x]
     s = [np.asarray(v, np.float64).ravel() for v in s]
     nf, h, gam, C, D = [], [], [], [], []
     for d in range(3):
-        xlo, xhi, slo, shi = x[d].min(), x[d].max(), s[d].min(), s[d].max()
+        xlo, xhi = float(x[d].min()), float(x[d].max())
+        slo, shi = s[d].min(), s[d].max()
         C.append(0.5 * (xlo + xhi))
         D.append(0.5 * (slo + shi))
         a, b, g = set_nhg_type3(0.5 * (shi - slo), 0.5 * (xhi - xlo), upsampfac, w)
@@ -282,14 +297,50 @@ def nufft_t3(x, c, s, eps=1e-5, isign=+1, upsampfac=1.25, spread64=True):
         h.append(b)
         gam.append(g)
     n_up = [next235even(int(np.ceil(upsampfac * n))) for n in nf]
+    out = dict(w=w, beta=beta, nf=nf, h=h, gam=gam, C=C, D=D, n_up=n_up)
+
+    ss = [v.astype(rdt) for v in s]
+    t_i1 = np.empty((3, s[0].size), np.int32)
+    t_fr = np.empty((3, s[0].size), np.float32)
+    theta = []
+    for d in range(3):
+        hd = 2.0 * PI / nf[d]
+        th = (ss[d] - rdt(D[d])) * rdt(hd * gam[d])
+        theta.append(th.astype(np.float64))
+        lam = th / rdt(2.0 * PI / n_up[d]) + rdt(n_up[d] / 2.0)
+        t_i1[d] = np.ceil(lam - rdt(w / 2.0)).astype(np.int32)
+        t_fr[d] = (lam - t_i1[d].astype(rdt)).astype(np.float32)
+    sp = [v.astype(pdt) for v in s]
+    post_ang = sum(pdt(C[d]) * (sp[d] - pdt(D[d])) for d in range(3))
+    tdec = np.ones(s[0].size)
+    for d in range(3):
+        tdec *= kernel_ft(theta[d], beta, w)
+    out.update(t_i1=t_i1, t_fr=t_fr, theta=theta, tdec=tdec,
+               post=np.exp(1j * isign * post_ang.astype(np.float64)) / tdec)
+
+    xs = [v.astype(rdt) for v in x]
     i1 = np.empty((3, x[0].size), np.int32)
     fr = np.empty((3, x[0].size), np.float32)
     for d in range(3):
-        xi = (x[d] - C[d]) / gam[d] / h[d] + nf[d] / 2.0
-        i1[d] = np.ceil(xi - w / 2.0).astype(np.int32)
-        fr[d] = (xi - i1[d]).astype(np.float32)
-    pre = np.exp(1j * isign * (D[0] * x[0] + D[1] * x[1] + D[2] * x[2]))
-    b = (spread if spread64 else spread_f32)(i1, fr, np.asarray(c, np.complex128) * pre, nf, w,
+        hd = 2.0 * PI / nf[d]
+        xi = (xs[d] - rdt(C[d])) / rdt(gam[d]) / rdt(hd) + rdt(nf[d] / 2.0)
+        i1[d] = np.ceil(xi - rdt(w / 2.0)).astype(np.int32)
+        fr[d] = (xi - i1[d].astype(rdt)).astype(np.float32)
+    xp = [v.astype(pdt) for v in x]
+    pre_ang = sum(pdt(D[d]) * xp[d] for d in range(3))
+    out.update(i1=i1, fr=fr, pre=np.exp(1j * isign * pre_ang.astype(np.float64)))
+    return out
+
+
+def nufft_t3(x, c, s, eps=1e-5, isign=+1, upsampfac=1.25, spread64=True):
+    """CPU type-3 (3D), following ref_t3.py:48-221 with the crit64 setup of
+    t3_setup: all stages fp64, or with the spread stage in fp32
+    (spread64=False, the reference's most precision-sensitive fp32 stage,
+    ref: harness/diagnose_ref.py:21-41)."""
+    st = t3_setup(x, s, eps, isign, upsampfac, "crit64")
+    w, beta, nf, n_up = st["w"], st["beta"], st["nf"], st["n_up"]
+    b = (spread if spread64 else spread_f32)(st["i1"], st["fr"],
+                                             np.asarray(c, np.complex128) * st["pre"], nf, w,
                                              beta)
     decs = []
     for d in range(3):
@@ -299,20 +350,7 @@ def nufft_t3(x, c, s, eps=1e-5, isign=+1, upsampfac=1.25, spread64=True):
     H[np.ix_(*[np.arange(-nf[d] // 2, nf[d] // 2) % n_up[d] for d in range(3)])] = \
         b * _outer(decs)
     v = _fftn(H, isign)
-    t_i1 = np.empty((3, s[0].size), np.int32)
-    t_fr = np.empty((3, s[0].size), np.float32)
-    theta = []
-    for d in range(3):
-        th = (s[d] - D[d]) * (h[d] * gam[d])
-        theta.append(th)
-        lam = th / (2.0 * PI / n_up[d]) + n_up[d] / 2.0
-        t_i1[d] = np.ceil(lam - w / 2.0).astype(np.int32)
-        t_fr[d] = (lam - t_i1[d]).astype(np.float32)
-    tdec = np.ones(s[0].size)
-    for d in range(3):
-        tdec *= kernel_ft(theta[d], beta, w)
-    post = np.exp(1j * isign * sum(C[d] * (s[d] - D[d]) for d in range(3))) / tdec
-    return interp(t_i1, t_fr, v, w, beta) * post
+    return interp(st["t_i1"], st["t_fr"], v, w, beta) * st["post"]
 
 
 # ----------------------------------------------------------- direct sums ---

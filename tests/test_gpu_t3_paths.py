@@ -375,3 +375,96 @@ def test_type3_set_sources(spread, oracle, mn, monkeypatch):
         p.set_sources(far)
     with pytest.raises(ValueError):
         p.set_sources(x1, backend="cuda")
+
+
+@pytest.mark.parametrize("prec", ["crit64", "coords64", "phases64", "fp32"])
+def test_type3_setup_bit_exact(prec, oracle, mn):
+    """Type-3 point setup against the oracle's restatement of the
+    reference's host path (ref: gpu_t3.py:326-377, 474-488), in every
+    precision mode: the plan's sizing scalars equal the oracle's exactly;
+    the unsorted source and target cells and fractions that
+    mn_t3_setpts_src / mn_t3_setpts_trg write are bit-identical, and the
+    bin keys equal the key definition; pre and post agree to complex64
+    rounding (their sincos and quadrature sums are fp64 in a different
+    order). The sets hold exact ties (a source at the centre C gives
+    xi - w/2 an integer; a target at D gives lam - w/2 an integer) and the
+    sources that fix the extent."""
+    import ctypes
+
+    from mlx_nufft_amd import _lib as L
+    from mlx_nufft_amd.sizing import quadrature
+
+    rng = np.random.default_rng(44)
+    P, M = 20000, 12000
+    x = [1.5 * d + rng.uniform(-1, 1, P) for d in range(3)]
+    s = [30.0 * (d - 1) + rng.uniform(-80, 80, M) for d in range(3)]
+    for d in range(3):
+        lo, hi = x[d][16:].min(), x[d][16:].max()
+        x[d][:4] = [lo, hi, 0.5 * (lo + hi), 0.5 * (lo + hi)]   # extent edges and centre
+        x[d][4:16] = lo + (hi - lo) * np.arange(1, 13) / 13.0
+        slo, shi = s[d][4:].min(), s[d][4:].max()
+        s[d][:4] = [slo, shi, 0.5 * (slo + shi), 0.5 * (slo + shi)]
+    for isign, eps in ((+1, 1e-5), (-1, 3e-5)):   # w = 9 and w = 8
+        print(f"case t3 setup prec={prec} isign={isign} eps={eps}", flush=True)
+        st = oracle.t3_setup(x, s, eps, isign, 1.25, prec)
+        plan = mn.Type3Plan(x, s, eps=eps, isign=isign, prec=prec)
+        assert plan.nf == st["nf"] and plan.n_up == st["n_up"]
+        assert plan.C == st["C"] and plan.D == st["D"] and plan.gam == st["gam"]
+        assert not plan.fft_rev
+        dev = torch.device("cuda")
+        x64 = [torch.from_numpy(v).to(dev) for v in x]
+        s64 = [torch.from_numpy(v).to(dev) for v in s]
+
+        i1 = torch.empty((3, P), dtype=torch.int32, device=dev)
+        fr = torch.empty((3, P), dtype=torch.float32, device=dev)
+        key = torch.empty(P, dtype=torch.int32, device=dev)
+        pre = torch.empty(P, dtype=torch.complex64, device=dev)
+        hd = [2.0 * np.pi / n for n in st["nf"]]
+        L.check(L.lib().mn_t3_setpts_src(
+            ctypes.byref(plan.bins_src), P, L.ptr3(x64), L.d3(st["C"]), L.d3(st["gam"]),
+            L.d3(hd), L.d3(st["D"]), isign, plan._flags, L.ptr3([i1[d] for d in range(3)]),
+            L.ptr3([fr[d] for d in range(3)]), L.ptr(key), L.ptr(pre), L.stream()), "src")
+        i1h, frh = i1.cpu().numpy(), fr.cpu().numpy()
+        assert np.array_equal(i1h, st["i1"])
+        assert np.array_equal(frh.view(np.int32), st["fr"].view(np.int32))
+        g = plan.bins_src
+        want_key, _ = oracle.bin_keys(st["i1"], st["nf"], [g.m[d] for d in range(3)], st["w"])
+        assert np.array_equal(key.cpu().numpy().astype(np.int64), want_key.astype(np.int64))
+        assert np.abs(pre.cpu().numpy() - st["pre"]).max() <= 1.2e-7
+        # the plan's sorted state is a permutation of the same values
+        perm = plan.src.perm.cpu().numpy().astype(np.int64)
+        assert np.array_equal(plan.src.i1s.cpu().numpy(), st["i1"][:, perm])
+        assert np.array_equal(plan.src.frs.cpu().numpy().view(np.int32),
+                              st["fr"][:, perm].view(np.int32))
+
+        ti1 = torch.empty((3, M), dtype=torch.int32, device=dev)
+        tfr = torch.empty((3, M), dtype=torch.float32, device=dev)
+        tkey = torch.empty(M, dtype=torch.int32, device=dev)
+        post = torch.empty(M, dtype=torch.complex64, device=dev)
+        dq, fq = quadrature(st["beta"], st["w"])
+        quad = torch.from_numpy(np.concatenate([dq, fq])).to(dev)
+        hg = [hd[d] * st["gam"][d] for d in range(3)]
+        h2 = [2.0 * np.pi / n for n in st["n_up"]]
+        L.check(L.lib().mn_t3_setpts_trg(
+            ctypes.byref(plan.bins_trg), M, L.ptr3(s64), L.d3(st["D"]), L.d3(hg), L.d3(h2),
+            L.d3(st["C"]), isign, plan._flags, L.ptr(quad), len(dq),
+            L.ptr3([ti1[d] for d in range(3)]), L.ptr3([tfr[d] for d in range(3)]), L.ptr(tkey),
+            L.ptr(post), L.stream()), "trg")
+        assert np.array_equal(ti1.cpu().numpy(), st["t_i1"])
+        assert np.array_equal(tfr.cpu().numpy().view(np.int32), st["t_fr"].view(np.int32))
+        gt = plan.bins_trg
+        want_tkey, _ = oracle.bin_keys(st["t_i1"], st["n_up"], [gt.m[d] for d in range(3)],
+                                       st["w"])
+        assert np.array_equal(tkey.cpu().numpy().astype(np.int64), want_tkey.astype(np.int64))
+        ph = post.cpu().numpy()
+        assert np.all(np.abs(ph - st["post"]) <= 2.5e-7 * np.abs(st["post"]))
+        # the centre source: xi = nf/2 exactly, so i1 = ceil(nf/2 - w/2) and
+        # fr = nf/2 - i1 (an exact tie, fr = w/2, when w is even); likewise
+        # the target at D with lam = n_up/2
+        for d in range(3):
+            ci = int(np.ceil(st["nf"][d] / 2 - st["w"] / 2))
+            assert i1h[d][2] == ci and frh[d][2] == st["nf"][d] / 2 - ci
+            ti = int(np.ceil(st["n_up"][d] / 2 - st["w"] / 2))
+            assert ti1.cpu().numpy()[d][2] == ti
+        if st["w"] % 2 == 0:
+            assert frh[0][2] == st["w"] / 2

@@ -160,6 +160,82 @@ def test_api_validation_errors(mn):
         p.execute(np.zeros(10, complex))
 
 
+def test_spread_method_and_legacy_validation(mn):
+    """Option checks that raise before any device work (ref: nd.py:281-305,
+    397-404, 869-874; types12.py:36-37, 159-186)."""
+    import inspect
+
+    from mlx_nufft_amd.nd import PlanArgumentError, od_applicable
+
+    x = np.zeros(10)
+    for cls in (mn.Type1PlanND, mn.Type2PlanND):
+        # an unknown method: a ValueError that is also the reference's
+        # AssertionError
+        for exc in (ValueError, AssertionError):
+            with pytest.raises(exc):
+                cls((x, x), (8, 8), spread_method="atomic")
+        # a forced "od" outside the reference's output-driven rule
+        with pytest.raises(ValueError, match="od"):
+            cls((x, x), (64, 64), spread_method="od")            # P < 20000
+        big = np.zeros(30000)
+        with pytest.raises(ValueError, match="od"):
+            cls((big, big), (64, 64), eps=1e-9, spread_method="od")   # w = 10 > 8
+        with pytest.raises(ValueError, match="od"):
+            cls((big,) * 3, (4, 4, 4), eps=1e-5, spread_method="od")   # grid 12^3 < tile 15^3
+    # the rule itself, against the reference's tile sizes
+    assert od_applicable(3, 6, [512] * 3, 20000)
+    assert not od_applicable(3, 6, [512] * 3, 19999)
+    assert not od_applicable(3, 9, [512] * 3, 10 ** 6)
+    assert not od_applicable(3, 6, [14, 512, 512], 10 ** 6)
+    assert od_applicable(3, 6, [15, 512, 512], 10 ** 6)
+    assert od_applicable(2, 7, [48, 48], 10 ** 6) and not od_applicable(2, 7, [47, 48], 10 ** 6)
+    assert od_applicable(1, 8, [2056], 10 ** 6) and not od_applicable(1, 8, [2055], 10 ** 6)
+
+    # legacy plans: 3D, even mode sizes, and the reference's defaults
+    for cls in (mn.Type1Plan, mn.Type2Plan):
+        for bad in ((8, 8, 7), (8, 8), 9):
+            with pytest.raises(PlanArgumentError):
+                cls((x, x, x), bad)
+        with pytest.raises(AssertionError):
+            cls((x, x), (8, 8, 8))
+        with pytest.raises(ValueError):
+            cls((x, x, x), (8, 8, 8), prec="fp16")
+    d1 = inspect.signature(mn.Type1Plan).parameters
+    d2 = inspect.signature(mn.Type2Plan).parameters
+    assert (d1["eps"].default, d1["isign"].default, d1["upsampfac"].default,
+            d1["sort_points"].default) == (1e-5, 1, 1.25, True)
+    assert (d2["eps"].default, d2["isign"].default, d2["upsampfac"].default,
+            d2["sort_points"].default) == (1e-5, 1, 1.25, False)
+
+
+def test_api_signatures(mn):
+    """The finufft-style functions keep the reference's parameter names and
+    defaults (ref: api.py:167-251, 258-260)."""
+    import inspect
+
+    want = {
+        "nufft1d1": "x c n_modes out eps isign kwargs", "nufft2d1": "x y c n_modes out eps isign kwargs",
+        "nufft3d1": "x y z c n_modes out eps isign kwargs", "nufft1d2": "x f out eps isign kwargs",
+        "nufft2d2": "x y f out eps isign kwargs", "nufft3d2": "x y z f out eps isign kwargs",
+        "nufft1d3": "x c s out eps isign kwargs", "nufft2d3": "x y c s t out eps isign kwargs",
+        "nufft3d3": "x y z c s t u out eps isign kwargs",
+    }
+    for name, params in want.items():
+        sig = inspect.signature(getattr(mn, name)).parameters
+        assert " ".join(sig) == params, name
+        assert sig["eps"].default == 1e-6 and sig["out"].default is None
+        assert sig["isign"].default == (-1 if name[-1] == "2" else 1)
+    ps = inspect.signature(mn.Plan).parameters
+    assert (ps["n_trans"].default, ps["eps"].default, ps["isign"].default,
+            ps["dtype"].default) == (1, 1e-6, None, "complex128")
+    with pytest.warns(UserWarning, match="eps"):
+        p = mn.Plan(1, (8, 8), eps=1e-9)
+    assert p.eps == 1e-6 and p.isign == 1 and mn.Plan(2, 8).isign == -1
+    with pytest.warns(UserWarning, match="unrecognised"):
+        mn.Plan(1, (8, 8), bogus_option=3)
+    mn.Plan(1, (8, 8), nthreads=4, spread_sort=2)   # finufft CPU options: silent
+
+
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU failure")
 def test_no_gpu_fails_loudly(mn):
     """Without a ROCm device every compute entry raises; nothing falls back

@@ -247,3 +247,55 @@ def test_cpu_baseline_port_accuracy(oracle):
     ks = [np.arange(-(n // 2), n - n // 2) for n in N]
     assert oracle.rel_l2(f, oracle.dft_t1(x, c, ks, +1)) < 1e-4
     assert t["total"] > 0
+
+
+@pytest.mark.parametrize("prec", ["crit64", "coords64", "phases64", "fp32"])
+def test_type3_setup_modes(oracle, prec):
+    """t3_setup in each precision mode against what the mathematics fixes:
+    - the cells and fractions rebuild the coordinate: the source at
+      C + gam h (i1 + fr - nf/2), the target theta = h2 (i1 + fr - n_up/2),
+      with fr in (w/2 - 1, w/2], to the rounding of the mode's rescale
+      dtype (an off-by-one cell, a dropped centre or scale fails this);
+    - pre = exp(i isign D.x) and post = exp(i isign C.(s - D)) / prod
+      phihat(theta), evaluated here in fp64 with numpy's dot (another
+      summation order), agree to the rounding of the mode's phase dtype;
+    - a mode whose rescale (or phase) dtype is fp32 does round: its
+      fractions (angles) differ from the fp64 mode's somewhere.
+    The crit64 mode is also pinned end to end through nufft_t3 above."""
+    rng = np.random.default_rng(12)
+    x = [2.5 + rng.uniform(-1, 1, 3000) for _ in range(3)]
+    s = [40.0 * (d + 1) + rng.uniform(-60, 60, 2000) for d in range(3)]
+    for isign in (+1, -1):
+        st = oracle.t3_setup(x, s, 1e-5, isign, 1.25, prec)
+        ref = oracle.t3_setup(x, s, 1e-5, isign, 1.25, "crit64")
+        w = st["w"]
+        r32 = prec in ("fp32", "phases64")
+        p32 = prec in ("fp32", "coords64")
+        tol_r = 4e-7 if r32 else 1e-14
+        for d in range(3):
+            fr, i1 = st["fr"][d].astype(np.float64), st["i1"][d]
+            assert fr.min() > w / 2 - 1 - 1e-5 and fr.max() <= w / 2 + 1e-5
+            xr = st["C"][d] + st["gam"][d] * st["h"][d] * (i1 + fr - st["nf"][d] / 2)
+            scale = st["gam"][d] * st["h"][d] * st["nf"][d]
+            assert np.abs(xr - x[d]).max() <= (tol_r + 1.2e-7 * w) * scale
+            tf, ti = st["t_fr"][d].astype(np.float64), st["t_i1"][d]
+            assert tf.min() > w / 2 - 1 - 1e-5 and tf.max() <= w / 2 + 1e-5
+            h2 = 2 * np.pi / st["n_up"][d]
+            th = h2 * (ti + tf - st["n_up"][d] / 2)
+            assert np.abs(th - st["theta"][d]).max() <= (tol_r + 1.2e-7 * w) * h2 * st["n_up"][d]
+            th_exact = (s[d] - st["D"][d]) * (st["h"][d] * st["gam"][d])
+            assert np.abs(st["theta"][d] - th_exact).max() <= tol_r * np.pi * 2
+        X = np.stack(x)
+        S = np.stack(s)
+        ang_pre = np.asarray(st["D"]) @ X
+        ang_post = np.asarray(st["C"]) @ (S - np.asarray(st["D"])[:, None])
+        tol_p = 2e-7 * np.abs(ang_pre).max() if p32 else 1e-12
+        assert np.abs(st["pre"] - np.exp(1j * isign * ang_pre)).max() <= tol_p
+        tdec = np.prod([oracle.kernel_ft(th, st["beta"], w) for th in st["theta"]], axis=0)
+        post = np.exp(1j * isign * ang_post) / tdec
+        tol_q = 2e-7 * np.abs(ang_post).max() if p32 else 1e-12
+        assert np.abs(st["post"] * tdec - post * tdec).max() <= tol_q
+        if r32:
+            assert not np.array_equal(st["fr"], ref["fr"])
+        if p32:
+            assert not np.array_equal(st["pre"], ref["pre"])
