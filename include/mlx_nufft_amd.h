@@ -105,6 +105,23 @@ int mn_sort_pairs(int64_t P, int key_bits, const uint32_t *key_in, uint32_t *key
                   mn_stream_t stream);
 
 /*
+ * mn_sort_pairs without a workspace argument: it allocates nothing and
+ * calls no allocating routine; its workspace is a 96 MiB device array in
+ * the library (one per GPU, held until the process ends). No counterpart
+ * in the reference: it is for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Limit: mn_sort_pairs_workspace_bytes(P, ncols) <= 96 MiB, about 1.2e7
+ * points with no payload column and 5.0e6 with 3; larger sorts return
+ * MN_EINVAL with a message. Every call on one GPU shares that GPU's array,
+ * so calls that overlap on one GPU (other streams, other host threads) race;
+ * calls on one stream are ordered and safe. Results are bit-identical to
+ * mn_sort_pairs.
+ */
+int mn_sort_pairs_noalloc(int64_t P, int key_bits, const uint32_t *key_in, uint32_t *key_out,
+                          uint32_t *perm_out, int ncols, const uint32_t *const *cols_in,
+                          uint32_t *const *cols_out, mn_stream_t stream);
+
+/*
  * Gather per-point arrays into sorted order: out[j] = in[perm[j]] for i1
  * and fr of each dim, and for an optional complex64 array (extra_in may
  * be NULL). ref: nd.py:316-318, nd.py:339-340, gpu_t3.py:496-501.

@@ -59,6 +59,8 @@ _SIGS = [
     ("mn_sort_pairs_workspace_bytes", c_int64, [c_int64, c_int]),
     ("mn_sort_pairs", c_int, [c_int64, c_int, c_vp, c_vp, c_vp, c_int, ctypes.POINTER(c_vp),
                               ctypes.POINTER(c_vp), c_vp, c_int64, c_vp]),
+    ("mn_sort_pairs_noalloc", c_int, [c_int64, c_int, c_vp, c_vp, c_vp, c_int,
+                                      ctypes.POINTER(c_vp), ctypes.POINTER(c_vp), c_vp]),
     ("mn_gather_points", c_int, [c_int, c_int64, c_vp, VP3, VP3, VP3, VP3, c_vp, c_vp, c_vp]),
     ("mn_subproblem_workspace_bytes", c_int64, [ctypes.POINTER(Bins)]),
     ("mn_build_subproblems", c_int, [ctypes.POINTER(Bins), c_int64, c_vp, c_int32, c_vp,

@@ -10,6 +10,8 @@
 //
 // The subproblem table replaces the reference's host-side construction
 // (ref: nd.py:347-372) with three device kernels and one 8-byte read-back.
+#include <mutex>
+
 #include "mn_common.h"
 
 namespace mn {
@@ -399,6 +401,34 @@ SortWs sort_layout(int64_t P, int ncols, char *base) {
     return w;
 }
 
+// ---- the no-allocation sort ----------------------------------------------
+// Its workspace is this file-scope device array: each GPU the library runs on
+// holds its own copy, at its own address, until the process ends. In host
+// code the name `scratch` is only a stand-in for the symbol; the device
+// address comes from hipGetSymbolAddress, taken once per device with that
+// device current, and only that address is ever handed to a kernel.
+constexpr int64_t kSortScratchBytes = int64_t(96) << 20;
+static __device__ __align__(256) unsigned char scratch[kSortScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_address(void **out) {
+    int dev = -1;
+    MN_HIP_CHECK(hipGetDevice(&dev));
+    MN_REQUIRE(dev >= 0 && dev < kMaxDevices, "sort (no-alloc): device index out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        MN_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        MN_REQUIRE(p != nullptr, "sort (no-alloc): no device address for the scratch array");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return MN_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -455,6 +485,27 @@ int mn_sort_pairs(int64_t P, int key_bits, const uint32_t *key_in, uint32_t *key
         for (int c = 0; c < ncols; ++c) cur.in[c] = cur.out[c];
     }
     return MN_OK;
+}
+
+int mn_sort_pairs_noalloc(int64_t P, int key_bits, const uint32_t *key_in, uint32_t *key_out,
+                          uint32_t *perm_out, int ncols, const uint32_t *const *cols_in,
+                          uint32_t *const *cols_out, mn_stream_t stream) {
+    clear_error();
+    MN_REQUIRE(P >= 1 && P < (int64_t(1) << 32), "sort: P must be in [1, 2^32)");
+    MN_REQUIRE(ncols >= 0 && ncols <= MN_SORT_MAX_COLS, "sort: ncols out of range");
+    const int64_t need = sort_layout(P, ncols, nullptr).bytes;
+    if (need > kSortScratchBytes) {
+        set_error("sort (no-alloc): P = " + std::to_string(P) + " with " + std::to_string(ncols) +
+                  " payload columns needs " + std::to_string(need) +
+                  " bytes of workspace, above the " + std::to_string(kSortScratchBytes) +
+                  "-byte scratch array; use mn_sort_pairs with a workspace");
+        return MN_EINVAL;
+    }
+    void *ws = nullptr;
+    int rc = scratch_address(&ws);
+    if (rc) return rc;
+    return mn_sort_pairs(P, key_bits, key_in, key_out, perm_out, ncols, cols_in, cols_out, ws,
+                         kSortScratchBytes, stream);
 }
 
 int mn_sort_keys(int64_t P, int key_bits, const uint32_t *key_in, uint32_t *key_out,
