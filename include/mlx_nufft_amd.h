@@ -210,18 +210,24 @@ int mn_spread_owner_c128(const mn_bins *g, float beta, int64_t P, const int32_t 
 
 /*
  * Owner-computes 3D spread ("z-sweep"), the fast path for 3D type-1 grids
- * with n0, n1 multiples of 8 (>= 16), w <= 8 and n0*n1*n2/16 <= 2^26 keys.
- * Each wavefront owns an 8x8 (x, y) column block over a z-segment of zseg
- * cells, sweeps z with a w-cell window per column in registers and stores
- * every grid cell exactly once (no atomics; grid is fully overwritten).
+ * with n0, n1 multiples of 8 (>= 16), n2 >= 8, w <= 8 and at most 2^23 sort
+ * keys ((n0/8)(n1/8) ceil(n2/8) 16: 512^3 or 1024^2 x 256). Each wavefront
+ * owns an 8x8 (x, y) column block over a z-segment of zseg cells (a positive
+ * multiple of 8), sweeps it upwards in 8-cell z-chunks with the z-window of
+ * each 4x4 quadrant in matrix-core accumulators, and stores every grid cell
+ * exactly once (no atomics; grid is fully overwritten).
  * g: dim 3, w, n (m and nb are not used).
  *
  * Point word (one uint32 per point, from mn_zsweep_setpts):
- *   bits 0-25  key = ((bx*(n1/8) + by)*n2 + z)*4 + class, where (bx, by)
- *              is the 8x8 block of the first tap, z its cell, and class in
- *              [00, 01, 11, 10] order of whether the footprint reaches the
- *              next block in x and in y;
- *   bits 26-28 / 29-31  x / y cell of the first tap within its block.
+ *   bits  0-22  key = ((bx*(n1/8) + by)*ceil(n2/8) + z/8)*16 + rank, where
+ *               (bx, by) is the 8x8 block of the first tap, z its cell, and
+ *               rank orders the point's class: per axis, whether the
+ *               footprint reaches the next block and which halves of the two
+ *               blocks it covers, ranked so that the points a block receives
+ *               from itself and from its -x, -y and -xy neighbours in one
+ *               z-chunk are four contiguous key ranges;
+ *   bits 23-25 / 26-28  x / y cell of the first tap within its block;
+ *   bits 29-31  z cell of the first tap within its 8-cell z-chunk.
  * mn_zsweep_setpts computes the words and fr exactly as mn_setpts_t12 does
  * the cells (crit64, bit for bit); sort them with mn_sort_pairs(key_bits =
  * bits of mn_zsweep_nkeys() - 1, fr as payload) and build zstart
@@ -229,10 +235,10 @@ int mn_spread_owner_c128(const mn_bins *g, float beta, int64_t P, const int32_t 
  * >= k) with mn_zsweep_starts. The spread reads the sorted words and
  * fractions; strengths are c[perm[j]] (caller order), or c[j] when perm is
  * NULL (c already in sorted order); pre: optional sorted-order multiplier.
- * mn_spread_zsweep runs the matrix-core kernel (one 16x16x4 f32 MFMA
- * accumulator per 4x4 column quadrant holds the z-window); with the
- * environment variable MN_ZSWEEP_KERNEL=valu it runs the per-lane register
- * kernel, which gives the same grid within fp32 rounding.
+ * Products are formed in fp16 hi/lo halves on v_mfma_f32_16x16x32_f16 (three
+ * products per term, about 2^-22 relative) and accumulated in f32, with a
+ * per-wave power-of-two scale on the strengths, so any finite strength
+ * magnitude is handled.
  * ref: nd.py:152-165 (cells), nd.py:492-579 (output-driven spread),
  * nd.py:298-372 (bin sort).
  */

@@ -218,12 +218,14 @@ ZSEG = 128  # z-segment (cells) owned by one z-sweep wavefront
 
 def zsweep_eligible(dim, w, n_up):
     """True when the owner-computes z-sweep spread applies: 3D, w <= 8, the
-    x and y fine-grid sizes multiples of 8 (>= 16) and at most 2^26 sort keys
-    (n0*n1*n2/16). MN_SPREAD=tiles forces the LDS-tile spread instead."""
+    x and y fine-grid sizes multiples of 8 (>= 16) and at most 2^23 sort keys
+    ((n0/8)(n1/8) ceil(n2/8) 16, e.g. 512^3 or 1024^2 x 256). MN_SPREAD=tiles
+    forces the LDS-tile spread instead."""
     if os.environ.get("MN_SPREAD", "") == "tiles":
         return False
-    return (dim == 3 and w <= 8 and all(n % 8 == 0 and n >= 16 for n in n_up[:2])
-            and n_up[0] * n_up[1] * n_up[2] // 16 <= 1 << 26)
+    if dim != 3 or w > 8 or not all(n % 8 == 0 and n >= 16 for n in n_up[:2]) or n_up[2] < 8:
+        return False
+    return (n_up[0] // 8) * (n_up[1] // 8) * (-(-n_up[2] // 8)) * 16 <= 1 << 23
 
 
 class ZSweepPoints:

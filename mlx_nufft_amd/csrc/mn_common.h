@@ -158,28 +158,53 @@ struct CF3s { const float *p[3]; };
 
 // ---- z-sweep point word ----------------------------------------------------
 // The 3D owner-computes spread sorts one 32-bit word per point:
-//   bits  0-25  key = ((bx*nby + by)*n2 + z)*4 + reach class (sorted on)
-//   bits 26-28  x cell of the first tap within its 8-column block
-//   bits 29-31  y cell likewise
-// where (bx, by) is the 8x8 column block of the first tap (x, y), z its cell,
-// and the reach class says whether the footprint crosses into the next
-// block along x and along y, ordered [00, 01, 11, 10].
+//   bits  0-22  key = ((bx*nby + by)*nzc + zc)*16 + rank(cx, cy) (sorted on)
+//   bits 23-25  x cell of the first tap within its 8-column block
+//   bits 26-28  y cell likewise
+//   bits 29-31  z cell of the first tap within its 8-cell z-chunk
+// where (bx, by) is the 8x8 column block of the first tap (x, y), zc = z / 8
+// its z-chunk (nzc = ceil(n2 / 8) chunks), and (cx, cy) the reach codes of
+// the first tap along x and y (zs_reach). Inside a (block, chunk) the order
+// of the points does not matter to the spread (its z-window spans the whole
+// chunk), so the key stops at the chunk and the low bits group the points
+// by how their footprint meets the blocks.
 constexpr int kZsBlock = 8;
-constexpr int kZsKeyBits = 26;
+constexpr int kZsChunk = 8;
+constexpr int kZsKeyBits = 23;
 constexpr uint32_t kZsKeyMask = (1u << kZsKeyBits) - 1u;
 
-__device__ __forceinline__ uint32_t zs_word(int x, int y, int z, int n1, int n2, int w) {
-    const int cut = kZsBlock - (w - 1);
-    const int lx = x & (kZsBlock - 1), ly = y & (kZsBlock - 1);
-    const int cx = lx >= cut, cy = ly >= cut;
-    const int cp = cx ? (cy ? 2 : 3) : (cy ? 1 : 0);
+// Reach code of a first tap at cell o (0..7) of its block for width w:
+// 0 when the footprint stays inside the block, else it reaches the next
+// block and is 1 when it also covers the lower half (cells 0..3) of its own
+// block, 3 when it also covers the upper half of the next block, 2 when
+// neither.
+__host__ __device__ __forceinline__ int zs_reach(int o, int w) {
+    if (o + w - 1 < kZsBlock) return 0;
+    if (o <= 3) return 1;
+    return (o + w - 1 >= kZsBlock + 4) ? 3 : 2;
+}
+
+// Rank of the class (cx, cy) in the key. Classes that reach along x (cx >
+// 0) take ranks 3..14 and those that reach along y (cy > 0) ranks 0..11, so
+// the points a block receives from each neighbour are one key range:
+// own block [0, 16), -x neighbour [3, 15), -y neighbour [0, 12), -xy
+// neighbour [3, 12).
+__host__ __device__ __forceinline__ int zs_rank(int cx, int cy) {
+    if (cx == 0) return cy == 0 ? 15 : cy - 1;
+    return cy == 0 ? 11 + cx : 3 * cx + cy - 1;
+}
+
+__device__ __forceinline__ uint32_t zs_word(int x, int y, int z, int n1, int nzc, int w) {
+    const int lx = x & (kZsBlock - 1), ly = y & (kZsBlock - 1), lz = z & (kZsChunk - 1);
     const uint32_t blk = (uint32_t)((x / kZsBlock) * (n1 / kZsBlock) + y / kZsBlock);
-    const uint32_t key = (blk * (uint32_t)n2 + (uint32_t)z) * 4u + (uint32_t)cp;
-    return key | ((uint32_t)lx << kZsKeyBits) | ((uint32_t)ly << (kZsKeyBits + 3));
+    const uint32_t key = (blk * (uint32_t)nzc + (uint32_t)(z / kZsChunk)) * 16u +
+                         (uint32_t)zs_rank(zs_reach(lx, w), zs_reach(ly, w));
+    return key | ((uint32_t)lx << 23) | ((uint32_t)ly << 26) | ((uint32_t)lz << 29);
 }
 
 // Validate a z-sweep geometry (3D, 2 <= w <= 8, n0 and n1 multiples of 8 and
-// >= 16, key space within kZsKeyBits); number of keys K = nbx*nby*n2*4.
+// >= 16, key space within kZsKeyBits); number of keys
+// K = nbx*nby*ceil(n2/8)*16.
 int zsweep_check(const mn_bins *g);
 int64_t zsweep_nkeys(const mn_bins *g);
 

@@ -88,7 +88,8 @@ __global__ void k_zs_setpts(int64_t P, D3 x, int n0, int n1, int n2, int w, doub
     cell_t12(x.p[0][j], h0, halfw, prec64, ix, fx);
     cell_t12(x.p[1][j], h1, halfw, prec64, iy, fy);
     cell_t12(x.p[2][j], h2, halfw, prec64, iz, fz);
-    word[j] = zs_word(pmod(ix, n0), pmod(iy, n1), pmod(iz, n2), n1, n2, w);
+    word[j] = zs_word(pmod(ix, n0), pmod(iy, n1), pmod(iz, n2), n1, (n2 + kZsChunk - 1) / kZsChunk,
+                      w);
     fro.p[0][j] = fx;
     fro.p[1][j] = fy;
     fro.p[2][j] = fz;

@@ -14,21 +14,9 @@
 import numpy as np
 import pytest
 import torch
+from zsweep_words import words_numpy as _words_numpy
 
 pytestmark = pytest.mark.gpu
-
-
-def _words_numpy(i1, n, w):
-    """The z-sweep point word: key ((bx*nby + by)*n2 + z)*4 + class in bits
-    0-25, the in-block x / y cell of the first tap in bits 26-28 / 29-31."""
-    x, y, z = (i1[d].astype(np.int64) % n[d] for d in range(3))
-    cut = 8 - (w - 1)
-    cx, cy = (x % 8) >= cut, (y % 8) >= cut
-    cp = np.where(cx, np.where(cy, 2, 3), np.where(cy, 1, 0))
-    blk = (x // 8) * (n[1] // 8) + y // 8
-    key = (blk * n[2] + z) * 4 + cp
-    word = key | ((x % 8) << 26) | ((y % 8) << 29)
-    return key.astype(np.uint32), word.astype(np.uint32), (n[0] // 8) * (n[1] // 8) * n[2] * 4
 
 
 @pytest.mark.parametrize("N,eps", [((32, 24, 20), 1e-5), ((8, 8, 20), 1e-3), ((64, 64, 64), 1e-6)])
@@ -60,7 +48,7 @@ def test_zsweep_starts_sparse(mn):
     rng = np.random.default_rng(26)
     x = [rng.uniform(-np.pi, np.pi, 7) for _ in range(3)]
     p = mn.Type1PlanND(tuple(x), (64, 64, 64), eps=1e-5)
-    key = p.pts.word.cpu().numpy().view(np.uint32) & ((1 << 26) - 1)
+    key = p.pts.word.cpu().numpy().view(np.uint32) & ((1 << 23) - 1)
     zs = p.pts.zstart.cpu().numpy().astype(np.int64)
     assert np.array_equal(zs, np.searchsorted(key, np.arange(p.pts.K + 1), side="left"))
 
@@ -79,15 +67,10 @@ def _grid_check(oracle, mn, x, c, N, eps, tol=1e-5):
     return p
 
 
-KERNELS = ["mfma", "valu"]
-
-
-@pytest.mark.parametrize("kernel", KERNELS)
 @pytest.mark.parametrize("eps", [1e-1, 1e-2, 1e-3, 1e-4, 1e-5, 1e-6, 1e-7])
-def test_zsweep_widths(eps, kernel, oracle, mn, monkeypatch):
-    """w = 2 .. 8 through eps (sigma = 2), both sweep kernels."""
-    print(f"case zsweep width eps={eps} kernel={kernel}", flush=True)
-    monkeypatch.setenv("MN_ZSWEEP_KERNEL", kernel)
+def test_zsweep_widths(eps, oracle, mn):
+    """w = 2 .. 8 through eps (sigma = 2)."""
+    print(f"case zsweep width eps={eps}", flush=True)
     rng = np.random.default_rng(22)
     M = 20_000
     x = [rng.uniform(-np.pi, np.pi, M) for _ in range(3)]
@@ -95,12 +78,10 @@ def test_zsweep_widths(eps, kernel, oracle, mn, monkeypatch):
     _grid_check(oracle, mn, x, c, (24, 20, 18), eps)
 
 
-@pytest.mark.parametrize("kernel", KERNELS)
-def test_zsweep_clustered_and_wrapping(kernel, oracle, mn, monkeypatch):
+def test_zsweep_clustered_and_wrapping(oracle, mn):
     """Points clustered at the periodic corner (many per block and z, and
     footprints wrapping in x, y, z) on a 16x16 grid."""
-    print(f"case zsweep clustered kernel={kernel}", flush=True)
-    monkeypatch.setenv("MN_ZSWEEP_KERNEL", kernel)
+    print("case zsweep clustered", flush=True)
     rng = np.random.default_rng(23)
     M = 40_000
     h = 2 * np.pi / 16
@@ -110,14 +91,12 @@ def test_zsweep_clustered_and_wrapping(kernel, oracle, mn, monkeypatch):
     _grid_check(oracle, mn, x, c, (8, 8, 8), 1e-5)
 
 
-@pytest.mark.parametrize("kernel", KERNELS)
-def test_zsweep_partial_band(kernel, oracle, mn, monkeypatch):
+def test_zsweep_partial_band(oracle, mn):
     """Workgroups go segment-major in bands of 16 block rows along x: a grid
     of more than 16 block rows that is not a multiple of 16 ends in a partial
     band, and three z-segments repeat the bands. Every cell must still be
     written exactly once."""
-    print(f"case zsweep partial band kernel={kernel}", flush=True)
-    monkeypatch.setenv("MN_ZSWEEP_KERNEL", kernel)
+    print("case zsweep partial band", flush=True)
     rng = np.random.default_rng(27)
     M = 30_000
     x = [rng.uniform(-np.pi, np.pi, M) for _ in range(3)]
@@ -128,17 +107,17 @@ def test_zsweep_partial_band(kernel, oracle, mn, monkeypatch):
     assert p.n_up[2] > 2 * 128, p.n_up
 
 
-@pytest.mark.parametrize("kernel", KERNELS)
-def test_zsweep_partial_segment(kernel, oracle, mn, monkeypatch):
-    """A z extent (n2 = 300) that is not a multiple of the 128-cell segment."""
-    print(f"case zsweep partial segment kernel={kernel}", flush=True)
-    monkeypatch.setenv("MN_ZSWEEP_KERNEL", kernel)
+def test_zsweep_partial_segment(oracle, mn):
+    """A z extent (n2 = 300) that is a multiple of neither the 128-cell
+    segment nor the 8-cell chunk: the last chunk is partial, and the
+    periodic chunk below z = 0 starts its slots 4 cells up."""
+    print("case zsweep partial segment", flush=True)
     rng = np.random.default_rng(24)
     M = 60_000
     x = [rng.uniform(-np.pi, np.pi, M) for _ in range(3)]
     c = (rng.standard_normal(M) + 1j * rng.standard_normal(M)).astype(np.complex64)
     p = _grid_check(oracle, mn, x, c, (16, 16, 150), 1e-5)
-    assert p.n_up[2] % 128 != 0
+    assert p.n_up[2] % 128 != 0 and p.n_up[2] % 8 != 0
 
 
 def test_zsweep_matches_tiles(mn, monkeypatch):
@@ -168,42 +147,45 @@ def test_zsweep_matches_tiles(mn, monkeypatch):
 
 
 @pytest.mark.parametrize("N,eps", [((64, 64, 48), 1e-5), ((32, 48, 40), 1e-7), ((48, 32, 64), 1e-2)])
-def test_zsweep_mfma_equals_valu(N, eps, mn, monkeypatch):
-    """The MFMA accumulator sweep and the per-lane register sweep spread the
-    same points to the same grid (fp32 rounding apart), with segments
-    shorter than the grid so segment edges are exercised."""
+def test_zsweep_segments(N, eps, oracle, mn):
+    """Segments of 8, 16, 128 and 256 cells (8 and 16 put a segment edge in
+    most footprints) spread the same points to the same grid within fp32
+    rounding, every cell written (the grid starts as NaN), and the 128-cell
+    grid matches the oracle."""
     from mlx_nufft_amd import _engine as E
 
-    print(f"case zsweep mfma vs valu N={N} eps={eps}", flush=True)
+    print(f"case zsweep segments N={N} eps={eps}", flush=True)
     rng = np.random.default_rng(27)
     M = 150_000
     x = [rng.uniform(-np.pi, np.pi, M) for _ in range(3)]
-    c = torch.from_numpy((rng.standard_normal(M) + 1j * rng.standard_normal(M))
-                         .astype(np.complex64)).cuda()
+    c = (rng.standard_normal(M) + 1j * rng.standard_normal(M)).astype(np.complex64)
+    cd = torch.from_numpy(c).cuda()
     p = mn.Type1PlanND(tuple(x), N, eps=eps)
     assert p.pts.kind == "zsweep"
     grids = {}
-    for kernel in KERNELS:
-        monkeypatch.setenv("MN_ZSWEEP_KERNEL", kernel)
-        for zseg in (16, 128):
-            g = torch.full(p.n_up, float("nan"), dtype=torch.complex64, device="cuda")
-            E.spread_zsweep(p.pts, p.beta, c, g, zseg=zseg)
-            assert bool(torch.isfinite(torch.view_as_real(g)).all()), (kernel, zseg)
-            grids[kernel, zseg] = g
-    ref = grids["valu", 128]
-    for key, g in grids.items():
+    for zseg in (8, 16, 128, 256):
+        g = torch.full(p.n_up, float("nan"), dtype=torch.complex64, device="cuda")
+        E.spread_zsweep(p.pts, p.beta, cd, g, zseg=zseg)
+        assert bool(torch.isfinite(torch.view_as_real(g)).all()), zseg
+        grids[zseg] = g
+    ref = grids[128]
+    for zseg, g in grids.items():
         rel = float((g - ref).abs().norm() / ref.abs().norm())
-        print(f"  {key}: rel diff {rel:.2e}")
-        assert rel < 1e-6, key
+        print(f"  zseg {zseg}: rel diff {rel:.2e}")
+        assert rel < 1e-6, zseg
+    i1o, fro = oracle.setpts_t12(x, p.n_up, p.w)
+    go = oracle.spread(i1o, fro, c, p.n_up, p.w, p.beta)
+    assert oracle.rel_l2(ref.cpu().numpy(), go) < 1e-5
 
 
-@pytest.mark.parametrize("case", ["tiny", "huge", "mixed", "sparse"])
-def test_zsweep_mfma_strength_range(case, mn, monkeypatch):
+@pytest.mark.parametrize("case", ["tiny", "huge", "mixed", "sparse", "tiny36", "huge36"])
+def test_zsweep_mfma_strength_range(case, oracle, mn):
     """The fp16 product path scales strengths per wave by a power of two
     (rescaling what it holds when a batch brings a larger one): strengths
-    at 1e-30 and 1e30, a mix where 1 % of the points are 1e8 times larger,
-    and mostly-zero strengths (whole batches of zeros) all give the
-    register kernel's grid, finite, within 1e-6."""
+    at 1e-30 and 1e30, at 1e-36 and 1e36 (near the ends of fp32's range), a
+    mix where 1 % of the points are 1e8 times larger, and mostly-zero
+    strengths (whole batches of zeros) all give the oracle's fp64 grid
+    within 1e-5, with every cell finite."""
     from mlx_nufft_amd import _engine as E
 
     print(f"case zsweep strength range {case}", flush=True)
@@ -211,24 +193,20 @@ def test_zsweep_mfma_strength_range(case, mn, monkeypatch):
     M = 120_000
     x = [rng.uniform(-np.pi, np.pi, M) for _ in range(3)]
     c = rng.standard_normal(M) + 1j * rng.standard_normal(M)
-    if case == "tiny":
-        c *= 1e-30
-    elif case == "huge":
-        c *= 1e30
-    elif case == "mixed":
+    scale = {"tiny": 1e-30, "huge": 1e30, "tiny36": 1e-36, "huge36": 1e36}.get(case, 1.0)
+    c *= scale
+    if case == "mixed":
         c[rng.random(M) < 0.01] *= 1e8
-    else:
+    elif case == "sparse":
         c[rng.random(M) < 0.98] = 0
-    cd = torch.from_numpy(c.astype(np.complex64)).cuda()
+    c64 = c.astype(np.complex64)
     p = mn.Type1PlanND(tuple(x), (64, 64, 48), eps=1e-5)
     assert p.pts.kind == "zsweep" and p.w == 6
-    grids = {}
-    for kernel in KERNELS:
-        monkeypatch.setenv("MN_ZSWEEP_KERNEL", kernel)
-        g = torch.empty(p.n_up, dtype=torch.complex64, device="cuda")
-        E.spread_zsweep(p.pts, p.beta, cd, g)
-        assert bool(torch.isfinite(torch.view_as_real(g)).all()), kernel
-        grids[kernel] = g.to(torch.complex128)
-    rel = float((grids["mfma"] - grids["valu"]).abs().norm() / grids["valu"].abs().norm())
-    print(f"  rel diff {rel:.2e}")
-    assert rel < 1e-6
+    g = torch.empty(p.n_up, dtype=torch.complex64, device="cuda")
+    E.spread_zsweep(p.pts, p.beta, torch.from_numpy(c64).cuda(), g)
+    assert bool(torch.isfinite(torch.view_as_real(g)).all())
+    i1o, fro = oracle.setpts_t12(x, p.n_up, p.w)
+    go = oracle.spread(i1o, fro, c64, p.n_up, p.w, p.beta)
+    err = oracle.rel_l2(g.cpu().numpy().astype(np.complex128), go)
+    print(f"  vs oracle: {err:.2e}")
+    assert err < 1e-5

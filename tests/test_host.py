@@ -56,14 +56,18 @@ def test_pure_queries(clib):
     assert ws[-1] >= 2 * 4 * 20_000_000
 
     g = _lib.Bins.make(3, 6, [512, 512, 512], [8, 8, 1])
-    assert clib.mn_zsweep_nkeys(ctypes.byref(g)) == 64 * 64 * 512 * 4
+    assert clib.mn_zsweep_nkeys(ctypes.byref(g)) == 64 * 64 * 64 * 16
+    # n2 not a multiple of 8: the last z-chunk is partial
+    g = _lib.Bins.make(3, 6, [64, 64, 300], [8, 8, 1])
+    assert clib.mn_zsweep_nkeys(ctypes.byref(g)) == 8 * 8 * 38 * 16
     # payload columns add one P-length alternate buffer each
     assert (clib.mn_sort_pairs_workspace_bytes(1 << 20, 3)
             >= clib.mn_sort_pairs_workspace_bytes(1 << 20, 0) + 3 * 4 * (1 << 20))
     assert clib.mn_sort_pairs_workspace_bytes(1000, 9) == -1
-    # the z-sweep key space is capped at 2^26 keys
-    assert clib.mn_zsweep_nkeys(ctypes.byref(_lib.Bins.make(3, 6, [1024] * 3, [8, 8, 1]))) == 1 << 26
-    assert clib.mn_zsweep_nkeys(ctypes.byref(_lib.Bins.make(3, 6, [1024, 1024, 1040],
+    # the z-sweep key space is capped at 2^23 keys
+    assert clib.mn_zsweep_nkeys(ctypes.byref(_lib.Bins.make(3, 6, [1024, 1024, 256],
+                                                            [8, 8, 1]))) == 1 << 23
+    assert clib.mn_zsweep_nkeys(ctypes.byref(_lib.Bins.make(3, 6, [1024, 1024, 264],
                                                             [8, 8, 1]))) == -1
     assert clib.mn_subproblem_workspace_bytes(ctypes.byref(_lib.Bins.make(3, 6, [64] * 3,
                                                                           [11] * 3))) > 0
@@ -120,10 +124,33 @@ def test_engine_bin_geometry(monkeypatch):
     assert not E.zsweep_eligible(3, 9, [512, 512, 512])
     assert not E.zsweep_eligible(3, 6, [514, 512, 512])
     assert not E.zsweep_eligible(2, 6, [512, 512])
-    assert E.zsweep_eligible(3, 6, [1024] * 3)
-    assert not E.zsweep_eligible(3, 6, [1024, 1024, 1040])
+    assert E.zsweep_eligible(3, 6, [1024, 1024, 256])
+    assert not E.zsweep_eligible(3, 6, [1024, 1024, 264])
     g = E.make_bins(3, 6, [512] * 3, m=(8, 8, 1))
     assert E.key_bits(g) == (64 * 64 * 512 - 1).bit_length()
+
+
+def test_zsweep_class_ranks():
+    """The z-sweep key's class ranking: for every width, the classes a
+    neighbour's points must carry to reach a block (along x: cx > 0, along
+    y: cy > 0, both for the -xy neighbour) are exactly the key-rank ranges
+    the sweep reads, [3, 15), [0, 12) and [3, 12); a reach code is nonzero
+    exactly when the footprint crosses into the next block."""
+    from zsweep_words import rank, reach
+
+    cx, cy = np.meshgrid(np.arange(4), np.arange(4), indexing="ij")
+    r = rank(cx, cy)
+    assert sorted(r.ravel()) == list(range(16))
+    assert set(r[cx > 0]) == set(range(3, 15))
+    assert set(r[cy > 0]) == set(range(0, 12))
+    assert set(r[(cx > 0) & (cy > 0)]) == set(range(3, 12))
+    for w in range(2, 9):
+        o = np.arange(8)
+        assert np.array_equal(reach(o, w) > 0, (o + w - 1) >= 8)
+        # code 1 covers the lower half of the own block, 3 the upper half
+        # of the next one
+        assert np.array_equal(reach(o, w) == 1, ((o + w - 1) >= 8) & (o <= 3))
+        assert np.array_equal(reach(o, w) == 3, (o + w - 1 >= 12) & (o > 3))
 
 
 # ------------------------------------------------------------ validation --
