@@ -26,18 +26,19 @@
 //    point's row of the weight table, as pairs (w[a], w[a + 4]) over the
 //    block's 8 columns (zero elsewhere), and B = c w_z, already split into
 //    fp16 hi + lo, into four slot-major tables (re hi, re lo, im hi, im lo;
-//    [slot][point], zero elsewhere). It also notes which quadrants its
-//    footprint meets; one ballot per quadrant turns that into masks.
+//    [slot][point], zero elsewhere).
 //  * K-steps of 32 points: lane (li, lk) = (l % 16, l / 16) supplies
 //    A[li][8 lk + t] and B[8 lk + t][li] for t < 8: it reads its 8 points'
 //    weight pairs and its B column (one 16-byte read per table), and for
-//    every quadrant that one of the 32 points meets (a uniform branch on
-//    the masks) forms A = wx wy and splits it -- hi = the f32 product
+//    each quadrant forms A = wx wy and splits it -- hi = the f32 product
 //    rounded toward zero to fp16 (a truncation, identical on every
 //    conversion path), lo = fp16(fma(wx, wy, -hi)), which also keeps the f32
 //    product's rounding, so hi + lo carries the exact product to about
 //    2^-22 -- and accumulates hi*hi' + hi*lo' + lo*hi' into the quadrant's
-//    real and imaginary tiles (six MFMAs).
+//    real and imaginary tiles: 24 MFMAs per K-step, issued so that each
+//    of the 8 tiles recurs only every 8th instruction. (Skipping quadrants
+//    that none of a K-step's 32 points meets was measured: a K-step mixes
+//    so many classes that it spared 3 % of the MFMAs and was no faster.)
 // After a chunk, slots 0..7 are complete: lane (li < 8, lk) stores slot li
 // of cells (4 qx + lk, 4 qy + r) straight from the accumulators (four lanes
 // per column write one 64-byte run, aligned because segments and chunks
@@ -255,8 +256,8 @@ __device__ __forceinline__ int wave_max9(int v) {
 #endif
 template <int W, bool PRE>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(ZS_OCC))) void
-k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int nseg, float bl2e,
-                float ih, const int32_t *__restrict__ zstart, const uint32_t *__restrict__ perm,
+k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int nseg,
+                float bl2e, const int32_t *__restrict__ zstart, const uint32_t *__restrict__ perm,
                 const uint32_t *__restrict__ word, CF3s frs, const float2 *__restrict__ c,
                 const float2 *__restrict__ pre, float2 *__restrict__ grid) {
     static_assert(W >= 2 && W <= ZB && ZC + W - 1 <= 16, "footprint exceeds the 16 slots");
@@ -356,24 +357,26 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
             for (int i = lane; i < nb4; i += 64) bz[i] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
         __syncthreads();
-        int qm = 0;  // quadrants the point's footprint meets: bit 2 qx + qy
         if (valid) {
             // first tap relative to this block (minus 8 for points of the -x
             // / -y neighbour blocks) and its slot in the window
             const int ox = (int)((p.wd >> 23) & 7u) - ((p.r & 1) ? ZB : 0);
             const int oy = (int)((p.wd >> 26) & 7u) - ((p.r & 2) ? ZB : 0);
             const int sz = (int)(p.wd >> 29) + off;
-            const int hx0 = max(ox, 0) <= 3, hx1 = ox + W - 1 >= 4;
-            const int hy0 = max(oy, 0) <= 3, hy1 = oy + W - 1 >= 4;
-            qm = (hx0 & hy0) | ((hx0 & hy1) << 1) | ((hx1 & hy0) << 2) | ((hx1 & hy1) << 3);
             const float2 cb = make_float2(__builtin_amdgcn_ldexpf(cv.x, sexp),
                                           __builtin_amdgcn_ldexpf(cv.y, sexp));
             float *row = rows + lane * ROW;
+            float wx[W], wy[W], wz[W];
+            constexpr float ih = 2.0f / W;
 #pragma unroll
             for (int a = 0; a < W; ++a) {
-                const float wxa = es_weight_z(((float)a - p.fx) * ih, bl2e);
-                const float wya = es_weight_z(((float)a - p.fy) * ih, bl2e);
-                const float wza = es_weight_z(((float)a - p.fz) * ih, bl2e);
+                wx[a] = es_weight_z(((float)a - p.fx) * ih, bl2e);
+                wy[a] = es_weight_z(((float)a - p.fy) * ih, bl2e);
+                wz[a] = es_weight_z(((float)a - p.fz) * ih, bl2e);
+            }
+#pragma unroll
+            for (int a = 0; a < W; ++a) {
+                const float wxa = wx[a], wya = wy[a], wza = wz[a];
                 // taps outside the block go to the row's pad slot (no branch)
                 const int x = ox + a, y = oy + a;
                 const int ix = (unsigned)x < (unsigned)ZB ? 2 * (x & 3) + (x >> 2) : 16;
@@ -389,12 +392,6 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
                 btab[3 * kTab + o] = (_Float16)__builtin_fmaf(cb.y, wza, -(float)h[1]);
             }
         }
-#ifdef ZS_SKIPQ
-        const uint64_t mq0 = __ballot(qm & 1), mq1 = __ballot(qm & 2);
-        const uint64_t mq2 = __ballot(qm & 4), mq3 = __ballot(qm & 8);
-#else
-        (void)qm;
-#endif
         __syncthreads();
         // K-steps of 32 points; rows and B entries past the batch are zero
         for (int e0 = 0; e0 < p.nb; e0 += 32) {
@@ -414,23 +411,6 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
             const mh8 brl = *reinterpret_cast<const mh8 *>(btab + kTab + bo);
             const mh8 bih = *reinterpret_cast<const mh8 *>(btab + 2 * kTab + bo);
             const mh8 bil = *reinterpret_cast<const mh8 *>(btab + 3 * kTab + bo);
-#ifdef ZS_SKIPQ
-            const uint64_t sel = 0xffffffffull << e0;
-            const bool use[4] = {(mq0 & sel) != 0, (mq1 & sel) != 0, (mq2 & sel) != 0,
-                                 (mq3 & sel) != 0};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                if (!use[q]) continue;
-                mh8 ah, al;
-                split_prod8((q >> 1) ? wx1 : wx0, (q & 1) ? wy1 : wy0, ah, al);
-                are[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, brh, are[q], 0, 0, 0);
-                aim[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bih, aim[q], 0, 0, 0);
-                are[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, brl, are[q], 0, 0, 0);
-                aim[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bil, aim[q], 0, 0, 0);
-                are[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, brh, are[q], 0, 0, 0);
-                aim[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bih, aim[q], 0, 0, 0);
-            }
-#else
             mh8 ah[4], al[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q)
@@ -452,7 +432,6 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
                 are[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[q], brh, are[q], 0, 0, 0);
                 aim[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[q], bih, aim[q], 0, 0, 0);
             }
-#endif
         }
     };
 
@@ -529,14 +508,13 @@ struct ZLaunch {
             const int nzc = (n2 + ZC - 1) / ZC;
             const int64_t nw = (int64_t)nbx * nby * nseg;
             const float bl2e = (float)(a.beta * 1.4426950408889634);
-            const float ih = (float)(2.0 / W);
             if (a.pre)
                 k_spread_zsweep<W, true><<<(unsigned)nw, 64, 0, a.s>>>(
-                    n0, n1, n2, nbx, nby, nzc, a.zseg, nseg, bl2e, ih, a.zstart, a.perm, a.word,
+                    n0, n1, n2, nbx, nby, nzc, a.zseg, nseg, bl2e, a.zstart, a.perm, a.word,
                     a.frs, a.c, a.pre, a.grid);
             else
                 k_spread_zsweep<W, false><<<(unsigned)nw, 64, 0, a.s>>>(
-                    n0, n1, n2, nbx, nby, nzc, a.zseg, nseg, bl2e, ih, a.zstart, a.perm, a.word,
+                    n0, n1, n2, nbx, nby, nzc, a.zseg, nseg, bl2e, a.zstart, a.perm, a.word,
                     a.frs, a.c, a.pre, a.grid);
             MN_LAUNCH_CHECK("spread_zsweep");
             return MN_OK;
