@@ -20,7 +20,9 @@ One JSON line is printed:
   value      = M / (ms_per_step) in NU pts/s (end to end, device-resident)
   roofline   = the spread kernel (the metric's "spread HBM GB/s"): algorithmic
                bytes M*(8 + 8*3 + 4) + 8*512^3 per launch over its mean
-               HIP-event duration in the timed steps, against 8 TB/s
+               HIP-event duration in the timed steps, against 8 TB/s; traffic
+               from the committed rocprofv3 summary when it was measured on
+               the current kernel source (None otherwise)
   cpu_baseline = the same type-1 on the host cores (fp32 OpenMP spread +
                scipy.fft, the oracle's port; finufft is not installed)
 """
@@ -95,6 +97,30 @@ def cpu_baseline(x, c, N, eps):
             "sample": (f"full workload once (M={M:.0e}, N={N[0]}^3, eps={eps:g}, fp32 OpenMP "
                        f"spread + scipy.fft workers={threads}); {dt:.2f} s"),
             "seconds": {k: round(v, 4) for k, v in parts.items()}}
+
+
+def spread_traffic(kernel):
+    """HBM bytes per spread launch (FETCH_SIZE + WRITE_SIZE, calibrated) from
+    the committed rocprofv3 summary, with its provenance. The summary records
+    the kernel it measured and the SHA-256 of the kernel's source file at
+    the time; when either differs from what runs now, the figure is stale and
+    traffic is reported as None."""
+    import hashlib
+
+    tf = ROOT / "profiles" / "spread_zsweep_3d_t1_M2e7_N256_traffic.json"
+    src = ROOT / "mlx_nufft_amd" / "csrc" / "mn_zsweep.hip"
+    try:
+        d = json.loads(tf.read_text())
+        sha = hashlib.sha256(src.read_bytes()).hexdigest()
+    except (ValueError, OSError):
+        return None, {"file": str(tf.relative_to(ROOT)), "status": "missing"}
+    info = {"file": str(tf.relative_to(ROOT)), "kernel": d.get("kernel"),
+            "source_sha256": d.get("source_sha256"), "commit": d.get("commit")}
+    if d.get("kernel") != kernel or d.get("source_sha256") != sha:
+        info["status"] = "stale (kernel or source changed since the measurement)"
+        return None, info
+    info["status"] = "current"
+    return d.get("bytes_per_launch"), info
 
 
 # The reference's published type-3 execute times for this workload (M5 Max,
@@ -248,13 +274,6 @@ def main():
     spread_ms = stages.get("spread", float("nan"))
     alg_bytes = M * (8 + 8 * 3 + 4) + 8 * grid_cells
     achieved = alg_bytes / (spread_ms * 1e-3) / 1e9
-    traffic = None
-    tf = ROOT / "profiles" / "spread_zsweep_3d_t1_M2e7_N256_traffic.json"
-    if tf.exists():
-        try:
-            traffic = json.loads(tf.read_text()).get("bytes_per_launch")
-        except (ValueError, OSError):
-            traffic = None
     exec_ms = sum(stages.get(k, 0.0) for k in ("zero", "spread", "fft", "deconv"))
 
     # type-2 leg of the round trip: interp back at the
@@ -262,10 +281,9 @@ def main():
     fk = plan.execute(cd, return_np=False)
     plan_w, plan_bins = plan.w, [plan.bins.m[d] for d in range(3)]
     zsweep = plan.pts.kind == "zsweep"
-    valu_sweep = os.environ.get("MN_ZSWEEP_KERNEL") == "valu"
-    spread_kernel = ((f"k_spread_zsweep<{plan_w}>" if valu_sweep
-                      else f"k_spread_zsweep_mfma<{plan_w}, false>") if zsweep
+    spread_kernel = (f"k_spread_zsweep<{plan_w}, false, 1>" if zsweep
                      else f"k_spread_tiled<3,{plan_w},false>")
+    traffic, traffic_src = spread_traffic(spread_kernel)
     del plan
     p2 = mn.Type2PlanND(tuple(xd), N, eps=eps, isign=-1)
     for _ in range(max(1, args.warmup)):
@@ -296,14 +314,13 @@ def main():
         "config": {"workload": "3D type-1 M=2e7 N=256^3 eps=1e-5 (BASELINE.json configs[3])",
                    "M": M, "N": list(N), "eps": eps, "isign": 1, "w": plan_w,
                    "n_up": list(n_up),
-                   "spread": ((("z-sweep, 8x8 column blocks, "
-                                + ("per-lane register windows" if valu_sweep
-                                   else "MFMA accumulator windows")) if zsweep
-                               else f"LDS tiles {plan_bins}")),
+                   "spread": ("z-sweep, 8x8 column blocks, 8-cell z-chunks, MFMA windows"
+                              if zsweep else f"LDS tiles {plan_bins}"),
                    "step": ("execute only" if args.exec_only else
                             "set_sources + execute, device-resident")},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                     "traffic_source": traffic_src,
                      "kernel": spread_kernel, "alg_bytes_per_launch": alg_bytes,
                      "ms_per_launch": spread_ms},
         "step_ms": {"min": step_ms[0], "median": step_ms[len(step_ms) // 2],

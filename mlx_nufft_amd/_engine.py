@@ -325,6 +325,84 @@ class YSweepPoints:
         return _rows(self.frs, 2)
 
 
+class _Subset:
+    """Points [s, e) of a group-sorted copy of a point state: the attributes
+    the spread entry points read, as views of the copy's columns (frs and
+    i1s are lists of per-dimension rows)."""
+
+    def __init__(self, kind, bins, P, **views):
+        self.kind = kind
+        self.bins = bins
+        self.P = P
+        self.__dict__.update(views)
+
+    def fr_rows(self):
+        return list(self.frs)
+
+    def i1_rows(self):
+        return list(self.i1s)
+
+
+class GroupSplit:
+    """A point state partitioned by group label, for spreads of disjoint
+    point subsets that visit every point once in total.
+
+    glabel: int64 labels in caller order; labels outside [0, G) are left
+    out. One stable sort by label (carrying the spread's sorted columns)
+    keeps each group's points in the state's key order, so each group is a
+    contiguous, still key-sorted range. Iterating yields (g, subset) for the
+    non-empty groups and builds the subset's start table just before it is
+    used: z-/y-sweep key starts in one shared buffer (rebuilt in stream
+    order, after the previous group's spread has read it), or the tile
+    spread's subproblem table."""
+
+    def __init__(self, pts, glabel, G):
+        self.pts = pts
+        self.G = G
+        dim = pts.bins.dim
+        gs = glabel[pts.perm.long()]
+        gkey = torch.where((gs < 0) | (gs >= G), G, gs).to(torch.int32)
+        del gs
+        if pts.kind in ("zsweep", "ysweep"):
+            cols = [pts.word, pts.perm] + _rows(pts.frs, dim)
+        elif pts.kind == "tiles":
+            cols = [pts.skey, pts.perm] + _rows(pts.frs, dim) + _rows(pts.i1s, dim)
+        else:
+            raise ValueError(f"no disjoint spread for point state {pts.kind!r}")
+        skey, _, self.cols = sort_pairs(gkey, max(1, int(G).bit_length()), cols)
+        del gkey
+        bounds = torch.arange(G + 1, dtype=torch.int32, device=skey.device)
+        self.starts = torch.searchsorted(skey, bounds).cpu().tolist()
+        self._startbuf = None
+
+    def __iter__(self):
+        pts, dim, lib, c = self.pts, self.pts.bins.dim, L.lib(), self.cols
+        for g in range(self.G):
+            s, e = self.starts[g], self.starts[g + 1]
+            if e == s:
+                continue
+            frs = [r[s:e] for r in c[2:2 + dim]]
+            if pts.kind == "tiles":
+                sub = _Subset("tiles", pts.bins, e - s, perm=c[1][s:e], skey=c[0][s:e], frs=frs,
+                              i1s=[r[s:e] for r in c[2 + dim:2 + 2 * dim]])
+                sub.info, sub.nsub = build_subproblems(pts.bins, sub.skey)
+                yield g, sub
+                continue
+            if self._startbuf is None:
+                self._startbuf = torch.empty(pts.K + 1, dtype=torch.int32,
+                                             device=pts.perm.device)
+            sub = _Subset(pts.kind, pts.bins, e - s, perm=c[1][s:e], word=c[0][s:e], frs=frs,
+                          K=pts.K)
+            starts_fn = lib.mn_zsweep_starts if pts.kind == "zsweep" else lib.mn_ysweep_starts
+            L.check(starts_fn(ctypes.byref(pts.bins), sub.P, L.ptr(sub.word),
+                              L.ptr(self._startbuf), L.stream()), f"{pts.kind} starts")
+            if pts.kind == "zsweep":
+                sub.zstart = self._startbuf
+            else:
+                sub.ystart = self._startbuf
+            yield g, sub
+
+
 def ysweep_vectors_per_wave(B):
     """Vectors one y-sweep wavefront carries (the kernel's rule): the
     largest of 8, 4, 2, 1 not above B."""
@@ -371,6 +449,18 @@ def spread_zsweep(pts, beta, c, grid, pre=None, zseg=ZSEG, presorted=False):
                                      L.ptr(pts.zstart), None if presorted else L.ptr(pts.perm),
                                      L.ptr(pts.word), L.ptr3(pts.fr_rows()), L.ptr(c), L.ptr(pre),
                                      L.ptr(grid), L.stream()), "spread_zsweep")
+
+
+def spread_zsweep_batch(pts, beta, cs, grids, zseg=ZSEG, presorted=False):
+    """grids[b] = spread(cs[b]) for B vectors with the z-sweep, two vectors
+    per wave (overwrites grids)."""
+    B = cs.shape[0]
+    assert grids.shape[0] == B and cs.is_contiguous() and grids.is_contiguous()
+    L.check(L.lib().mn_spread_zsweep_batch(ctypes.byref(pts.bins), float(beta), pts.P, B,
+                                           int(zseg), L.ptr(pts.zstart),
+                                           None if presorted else L.ptr(pts.perm),
+                                           L.ptr(pts.word), L.ptr3(pts.fr_rows()), L.ptr(cs),
+                                           L.ptr(grids), L.stream()), "spread_zsweep_batch")
 
 
 def spread(pts, beta, c, grid, pre=None, accumulate=False):

@@ -78,6 +78,8 @@ _SIGS = [
     ("mn_zsweep_starts", c_int, [ctypes.POINTER(Bins), c_int64, c_vp, c_vp, c_vp]),
     ("mn_spread_zsweep", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int, c_vp, c_vp, c_vp,
                                  VP3, c_vp, c_vp, c_vp, c_vp]),
+    ("mn_spread_zsweep_batch", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int64, c_int,
+                                       c_vp, c_vp, c_vp, VP3, c_vp, c_vp, c_vp]),
     ("mn_permute_c64", c_int, [c_int64, c_vp, c_vp, c_vp, c_vp]),
     ("mn_ysweep_nkeys", c_int64, [ctypes.POINTER(Bins)]),
     ("mn_ysweep_setpts", c_int, [ctypes.POINTER(Bins), c_int64, ctypes.c_void_p * 2, c_int, c_vp,

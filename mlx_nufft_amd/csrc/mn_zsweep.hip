@@ -254,85 +254,102 @@ __device__ __forceinline__ int wave_max9(int v) {
 #ifndef ZS_OCC
 #define ZS_OCC 2
 #endif
-template <int W, bool PRE>
+template <int W, bool PRE, int VB>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(ZS_OCC))) void
 k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int nseg,
                 float bl2e, const int32_t *__restrict__ zstart, const uint32_t *__restrict__ perm,
                 const uint32_t *__restrict__ word, CF3s frs, const float2 *__restrict__ c,
-                const float2 *__restrict__ pre, float2 *__restrict__ grid) {
+                int64_t cstride, const float2 *__restrict__ pre, float2 *__restrict__ grid,
+                int64_t gstride) {
     static_assert(W >= 2 && W <= ZB && ZC + W - 1 <= 16, "footprint exceeds the 16 slots");
+    static_assert(VB == 1 || VB == 2, "one or two strength vectors per wave");
     constexpr float kAxisScale = 128.0f;
     __shared__ __align__(16) float rows[64 * ROW];
-    __shared__ __align__(16) _Float16 btab[4 * kTab];
+    __shared__ __align__(16) _Float16 btab[VB][4 * kTab];
     int bx, by, seg;
     zs_block(xcd_remap(blockIdx.x, (int64_t)nbx * nby * nseg), nbx, nby, bx, by, seg);
+    // this wave's strength vectors and grids
+    c += (int64_t)blockIdx.y * VB * cstride;
+    grid += (int64_t)blockIdx.y * VB * gstride;
     const int z0 = seg * zseg, zend = min(z0 + zseg, n2);
     const int lane = threadIdx.x, li = lane & 15, lk = lane >> 4;
     const int bxm = bx == 0 ? nbx - 1 : bx - 1, bym = by == 0 ? nby - 1 : by - 1;
     // the periodic chunks below z = 0 sit this far up when n2 is not a
     // multiple of 8 (their first-tap cells end at n2, not at 8 nzc)
     const int wrap_off = ZC * nzc - n2;
-    int sexp = INT32_MIN;  // unset until the first batch
-    mf4 are[4], aim[4];
+    int sexp[VB];  // INT32_MIN: unset until the first batch
+    mf4 are[VB][4], aim[VB][4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        are[q] = mf4{0.f, 0.f, 0.f, 0.f};
-        aim[q] = mf4{0.f, 0.f, 0.f, 0.f};
+    for (int v = 0; v < VB; ++v) {
+        sexp[v] = INT32_MIN;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            are[v][q] = mf4{0.f, 0.f, 0.f, 0.f};
+            aim[v][q] = mf4{0.f, 0.f, 0.f, 0.f};
+        }
     }
     int zb = z0 - ZC;  // z of slot 0
     // cell (4 qx + lk, 4 qy + r) of the block at z: a wave-uniform column
     // base per (q, r) plus the lane's offset lk n1 n2 + z (< 2^31: the key
     // space bounds n0 n1 n2 by 2^28)
-    float2 *const gblk = grid + ((int64_t)ZB * bx * n1 + ZB * by) * n2;
+    const int64_t gblk = ((int64_t)ZB * bx * n1 + ZB * by) * n2;
     const int loff = lk * n1 * n2;
 
     // Slots 0..7 are complete: store the owned ones, shift the window by 8.
-    auto advance = [&]() {
+    auto advance = [&]() __attribute__((always_inline)) {
         const int z = zb + li;
         if (li < ZC && z >= z0 && z < zend) {
+#pragma unroll
+            for (int v = 0; v < VB; ++v)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        float2 *gq = grid + v * gstride + gblk +
+                                     ((int64_t)(4 * (q >> 1)) * n1 + 4 * (q & 1) + r) * n2;
+                        gq[loff + z] =
+                            make_float2(__builtin_amdgcn_ldexpf(are[v][q][r], -14 - sexp[v]),
+                                        __builtin_amdgcn_ldexpf(aim[v][q][r], -14 - sexp[v]));
+                    }
+        }
+#pragma unroll
+        for (int v = 0; v < VB; ++v)
 #pragma unroll
             for (int q = 0; q < 4; ++q)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    float2 *gq = gblk + ((int64_t)(4 * (q >> 1)) * n1 + 4 * (q & 1) + r) * n2;
-                    gq[loff + z] = make_float2(__builtin_amdgcn_ldexpf(are[q][r], -14 - sexp),
-                                               __builtin_amdgcn_ldexpf(aim[q][r], -14 - sexp));
+                    are[v][q][r] = row_shl_zero<ZC>(are[v][q][r]);
+                    aim[v][q][r] = row_shl_zero<ZC>(aim[v][q][r]);
                 }
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                are[q][r] = row_shl_zero<ZC>(are[q][r]);
-                aim[q][r] = row_shl_zero<ZC>(aim[q][r]);
-            }
         zb += ZC;
     };
 
-    auto process = [&](const ZPoint &p, const float2 cp) __attribute__((always_inline)) {
+    auto process = [&](const ZPoint &p, const float2 (&cp)[VB]) __attribute__((always_inline)) {
         int wc, off;
         chunk_pos(p.c, wrap_off, wc, off);
         // points of chunk -2 below the reach of z = 0 take no part
         const bool valid = p.valid && (int)(p.wd >> 29) + off >= 0;
-        const float2 cv = valid ? make_float2(cp.x * p.pv.x - cp.y * p.pv.y,
-                                              cp.x * p.pv.y + cp.y * p.pv.x)
-                                : make_float2(0.f, 0.f);
-        // the batch's largest strength is below 2^(e - 126)
-        {
-            const float mx = fmaxf(fabsf(cv.x), fabsf(cv.y));
+        float2 cv[VB];
+#pragma unroll
+        for (int v = 0; v < VB; ++v) {
+            cv[v] = valid ? make_float2(cp[v].x * p.pv.x - cp[v].y * p.pv.y,
+                                        cp[v].x * p.pv.y + cp[v].y * p.pv.x)
+                          : make_float2(0.f, 0.f);
+            // the batch's largest strength is below 2^(e - 126)
+            const float mx = fmaxf(fabsf(cv[v].x), fabsf(cv[v].y));
             const int e = wave_max9((__float_as_int(mx) >> 23) & 0xff);
             const int want = min(140 - e, 139);
-            if (sexp == INT32_MIN || want < sexp) {
-                if (sexp != INT32_MIN) {
+            if (sexp[v] == INT32_MIN || want < sexp[v]) {
+                if (sexp[v] != INT32_MIN) {
 #pragma unroll
                     for (int q = 0; q < 4; ++q)
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
-                            are[q][r] = __builtin_amdgcn_ldexpf(are[q][r], want - sexp);
-                            aim[q][r] = __builtin_amdgcn_ldexpf(aim[q][r], want - sexp);
+                            are[v][q][r] = __builtin_amdgcn_ldexpf(are[v][q][r], want - sexp[v]);
+                            aim[v][q][r] = __builtin_amdgcn_ldexpf(aim[v][q][r], want - sexp[v]);
                         }
                 }
-                sexp = want;
+                sexp[v] = want;
             }
         }
         // the window moves up to the batch's chunk (the cursor is
@@ -351,8 +368,8 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
             float2 *rz = reinterpret_cast<float2 *>(rows + lane * ROW);
 #pragma unroll
             for (int i = 0; i < 8; ++i) rz[i] = make_float2(0.f, 0.f);
-            float4 *bz = reinterpret_cast<float4 *>(btab);
-            constexpr int nb4 = 4 * kTab / 8;  // float4 count of the four B tables
+            float4 *bz = reinterpret_cast<float4 *>(&btab[0][0]);
+            constexpr int nb4 = VB * 4 * kTab / 8;  // float4 count of the B tables
 #pragma unroll
             for (int i = lane; i < nb4; i += 64) bz[i] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
@@ -363,8 +380,11 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
             const int ox = (int)((p.wd >> 23) & 7u) - ((p.r & 1) ? ZB : 0);
             const int oy = (int)((p.wd >> 26) & 7u) - ((p.r & 2) ? ZB : 0);
             const int sz = (int)(p.wd >> 29) + off;
-            const float2 cb = make_float2(__builtin_amdgcn_ldexpf(cv.x, sexp),
-                                          __builtin_amdgcn_ldexpf(cv.y, sexp));
+            float2 cb[VB];
+#pragma unroll
+            for (int v = 0; v < VB; ++v)
+                cb[v] = make_float2(__builtin_amdgcn_ldexpf(cv[v].x, sexp[v]),
+                                    __builtin_amdgcn_ldexpf(cv[v].y, sexp[v]));
             float *row = rows + lane * ROW;
             float wx[W], wy[W], wz[W];
             constexpr float ih = 2.0f / W;
@@ -376,20 +396,21 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
             }
 #pragma unroll
             for (int a = 0; a < W; ++a) {
-                const float wxa = wx[a], wya = wy[a], wza = wz[a];
                 // taps outside the block go to the row's pad slot (no branch)
                 const int x = ox + a, y = oy + a;
                 const int ix = (unsigned)x < (unsigned)ZB ? 2 * (x & 3) + (x >> 2) : 16;
                 const int iy = (unsigned)y < (unsigned)ZB ? 8 + 2 * (y & 3) + (y >> 2) : 16;
-                row[ix] = wxa * kAxisScale;
-                row[iy] = wya * kAxisScale;
-                const float br = cb.x * wza, bi = cb.y * wza;
-                const auto h = __builtin_amdgcn_cvt_pkrtz(br, bi);
+                row[ix] = wx[a] * kAxisScale;
+                row[iy] = wy[a] * kAxisScale;
                 const int o = (sz + a) * BST + lane;
-                btab[o] = h[0];
-                btab[kTab + o] = (_Float16)__builtin_fmaf(cb.x, wza, -(float)h[0]);
-                btab[2 * kTab + o] = h[1];
-                btab[3 * kTab + o] = (_Float16)__builtin_fmaf(cb.y, wza, -(float)h[1]);
+#pragma unroll
+                for (int v = 0; v < VB; ++v) {
+                    const auto h = __builtin_amdgcn_cvt_pkrtz(cb[v].x * wz[a], cb[v].y * wz[a]);
+                    btab[v][o] = h[0];
+                    btab[v][kTab + o] = (_Float16)__builtin_fmaf(cb[v].x, wz[a], -(float)h[0]);
+                    btab[v][2 * kTab + o] = h[1];
+                    btab[v][3 * kTab + o] = (_Float16)__builtin_fmaf(cb[v].y, wz[a], -(float)h[1]);
+                }
             }
         }
         __syncthreads();
@@ -406,33 +427,42 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
                 wy0[t] = py.x;
                 wy1[t] = py.y;
             }
-            const int bo = li * BST + e0 + 8 * lk;
-            const mh8 brh = *reinterpret_cast<const mh8 *>(btab + bo);
-            const mh8 brl = *reinterpret_cast<const mh8 *>(btab + kTab + bo);
-            const mh8 bih = *reinterpret_cast<const mh8 *>(btab + 2 * kTab + bo);
-            const mh8 bil = *reinterpret_cast<const mh8 *>(btab + 3 * kTab + bo);
             mh8 ah[4], al[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q)
                 split_prod8((q >> 1) ? wx1 : wx0, (q & 1) ? wy1 : wy0, ah[q], al[q]);
-            // consecutive MFMAs go to different accumulators: each of the 8
-            // tiles is used again only 8 instructions later
+            const int bo = li * BST + e0 + 8 * lk;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                are[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], brh, are[q], 0, 0, 0);
-                aim[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], bih, aim[q], 0, 0, 0);
-            }
+            for (int v = 0; v < VB; ++v) {
+                const mh8 brh = *reinterpret_cast<const mh8 *>(&btab[v][bo]);
+                const mh8 brl = *reinterpret_cast<const mh8 *>(&btab[v][kTab + bo]);
+                const mh8 bih = *reinterpret_cast<const mh8 *>(&btab[v][2 * kTab + bo]);
+                const mh8 bil = *reinterpret_cast<const mh8 *>(&btab[v][3 * kTab + bo]);
+                // consecutive MFMAs go to different accumulators: each of
+                // the 8 tiles of a vector is used again only 8 instructions
+                // later
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                are[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], brl, are[q], 0, 0, 0);
-                aim[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], bil, aim[q], 0, 0, 0);
-            }
+                for (int q = 0; q < 4; ++q) {
+                    are[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], brh, are[v][q], 0, 0, 0);
+                    aim[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], bih, aim[v][q], 0, 0, 0);
+                }
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                are[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[q], brh, are[q], 0, 0, 0);
-                aim[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[q], bih, aim[q], 0, 0, 0);
+                for (int q = 0; q < 4; ++q) {
+                    are[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], brl, are[v][q], 0, 0, 0);
+                    aim[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], bil, aim[v][q], 0, 0, 0);
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    are[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[q], brh, are[v][q], 0, 0, 0);
+                    aim[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[q], bih, aim[v][q], 0, 0, 0);
+                }
             }
         }
+    };
+
+    auto strengths = [&](const ZPoint &p, float2 (&cv)[VB]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int v = 0; v < VB; ++v) cv[v] = c[v * cstride + p.src];
     };
 
     const int clast = (zend - 1) / ZC;  // the last chunk of the segment
@@ -442,25 +472,27 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
     cur.clast = clast;
     cur_load(cur, rg, (z0 == 0 && wrap_off > 0) ? -2 : z0 / ZC - 1, lane);
     ZPoint pa = zp_next<PRE>(cur, rg, lane, perm, word, frs, pre);
-    float2 ca = c[pa.src];  // idle lanes read c[perm[0]]: their rows stay zero
+    float2 ca[VB], cb[VB], cc[VB];
+    strengths(pa, ca);  // idle lanes read c[perm[0]]: their rows stay zero
     ZPoint pb = zp_next<PRE>(cur, rg, lane, perm, word, frs, pre);
     ZPoint pc;
-    float2 cb, cc;
     for (;;) {
         if (pa.nb == 0) break;
         pc = zp_next<PRE>(cur, rg, lane, perm, word, frs, pre);
-        cb = c[pb.src];
+        strengths(pb, cb);
         process(pa, ca);
         if (pb.nb == 0) break;
         pa = zp_next<PRE>(cur, rg, lane, perm, word, frs, pre);
-        cc = c[pc.src];
+        strengths(pc, cc);
         process(pb, cb);
         if (pc.nb == 0) break;
         pb = zp_next<PRE>(cur, rg, lane, perm, word, frs, pre);
-        ca = c[pa.src];
+        strengths(pa, ca);
         process(pc, cc);
     }
-    if (sexp == INT32_MIN) sexp = 0;  // no points at all: the window holds zeros
+#pragma unroll
+    for (int v = 0; v < VB; ++v)
+        if (sexp[v] == INT32_MIN) sexp[v] = 0;  // no points at all: the window holds zeros
     while (zb < zend) advance();
 }
 
@@ -493,6 +525,8 @@ struct ZArgs {
     CF3s frs;
     const float2 *c, *pre;
     float2 *grid;
+    int64_t B;  // strength vectors (c: B rows of P, grid: B grids)
+    int64_t P;
     hipStream_t s;
 };
 
@@ -508,15 +542,35 @@ struct ZLaunch {
             const int nzc = (n2 + ZC - 1) / ZC;
             const int64_t nw = (int64_t)nbx * nby * nseg;
             const float bl2e = (float)(a.beta * 1.4426950408889634);
-            if (a.pre)
-                k_spread_zsweep<W, true><<<(unsigned)nw, 64, 0, a.s>>>(
-                    n0, n1, n2, nbx, nby, nzc, a.zseg, nseg, bl2e, a.zstart, a.perm, a.word,
-                    a.frs, a.c, a.pre, a.grid);
-            else
-                k_spread_zsweep<W, false><<<(unsigned)nw, 64, 0, a.s>>>(
-                    n0, n1, n2, nbx, nby, nzc, a.zseg, nseg, bl2e, a.zstart, a.perm, a.word,
-                    a.frs, a.c, a.pre, a.grid);
-            MN_LAUNCH_CHECK("spread_zsweep");
+            const int64_t gs = (int64_t)n0 * n1 * n2;
+            // pairs of vectors share a wave (weights and A operands formed
+            // once); an odd last vector runs alone
+            const int64_t pairs = a.B / 2, rest = a.B % 2;
+            if (pairs) {
+                const dim3 gridp((unsigned)nw, (unsigned)pairs);
+                if (a.pre)
+                    k_spread_zsweep<W, true, 2><<<gridp, 64, 0, a.s>>>(
+                        n0, n1, n2, nbx, nby, nzc, a.zseg, nseg, bl2e, a.zstart, a.perm, a.word,
+                        a.frs, a.c, a.P, a.pre, a.grid, gs);
+                else
+                    k_spread_zsweep<W, false, 2><<<gridp, 64, 0, a.s>>>(
+                        n0, n1, n2, nbx, nby, nzc, a.zseg, nseg, bl2e, a.zstart, a.perm, a.word,
+                        a.frs, a.c, a.P, a.pre, a.grid, gs);
+                MN_LAUNCH_CHECK("spread_zsweep");
+            }
+            if (rest) {
+                const float2 *c1 = a.c + 2 * pairs * a.P;
+                float2 *g1 = a.grid + 2 * pairs * gs;
+                if (a.pre)
+                    k_spread_zsweep<W, true, 1><<<(unsigned)nw, 64, 0, a.s>>>(
+                        n0, n1, n2, nbx, nby, nzc, a.zseg, nseg, bl2e, a.zstart, a.perm, a.word,
+                        a.frs, c1, a.P, a.pre, g1, gs);
+                else
+                    k_spread_zsweep<W, false, 1><<<(unsigned)nw, 64, 0, a.s>>>(
+                        n0, n1, n2, nbx, nby, nzc, a.zseg, nseg, bl2e, a.zstart, a.perm, a.word,
+                        a.frs, c1, a.P, a.pre, g1, gs);
+                MN_LAUNCH_CHECK("spread_zsweep");
+            }
             return MN_OK;
         }
     }
@@ -544,14 +598,15 @@ int mn_zsweep_starts(const mn_bins *g, int64_t P, const uint32_t *sorted_word, i
     return key_starts(sorted_word, P, zsweep_nkeys(g), kZsKeyMask, zstart, as_stream(stream));
 }
 
-int mn_spread_zsweep(const mn_bins *g, float beta, int64_t P, int zseg, const int32_t *zstart,
-                     const uint32_t *perm, const uint32_t *sorted_word,
-                     const float *const frs[3], const void *c, const void *pre, void *grid,
-                     mn_stream_t stream) {
+static int zsweep_spread(const mn_bins *g, float beta, int64_t P, int64_t B, int zseg,
+                         const int32_t *zstart, const uint32_t *perm, const uint32_t *sorted_word,
+                         const float *const frs[3], const void *c, const void *pre, void *grid,
+                         mn_stream_t stream) {
     clear_error();
     int rc = zsweep_check(g);
     if (rc) return rc;
     MN_REQUIRE(P >= 1 && P < (int64_t(1) << 31), "zsweep spread: P must be in [1, 2^31)");
+    MN_REQUIRE(B >= 1 && B < 65536, "zsweep spread: B must be in [1, 65535]");
     MN_REQUIRE(zseg >= ZC && zseg % ZC == 0, "zsweep spread: zseg must be a positive multiple of 8");
     MN_REQUIRE(zstart && sorted_word && c && grid, "zsweep spread: NULL pointer");
     ZArgs a{};
@@ -568,8 +623,26 @@ int mn_spread_zsweep(const mn_bins *g, float beta, int64_t P, int zseg, const in
     a.c = static_cast<const float2 *>(c);
     a.pre = static_cast<const float2 *>(pre);
     a.grid = static_cast<float2 *>(grid);
+    a.B = B;
+    a.P = P;
     a.s = as_stream(stream);
     return select_dim_w<ZLaunch>(3, g->w, a);
+}
+
+int mn_spread_zsweep(const mn_bins *g, float beta, int64_t P, int zseg, const int32_t *zstart,
+                     const uint32_t *perm, const uint32_t *sorted_word,
+                     const float *const frs[3], const void *c, const void *pre, void *grid,
+                     mn_stream_t stream) {
+    return zsweep_spread(g, beta, P, 1, zseg, zstart, perm, sorted_word, frs, c, pre, grid,
+                         stream);
+}
+
+int mn_spread_zsweep_batch(const mn_bins *g, float beta, int64_t P, int64_t B, int zseg,
+                           const int32_t *zstart, const uint32_t *perm,
+                           const uint32_t *sorted_word, const float *const frs[3],
+                           const void *cs, void *grids, mn_stream_t stream) {
+    return zsweep_spread(g, beta, P, B, zseg, zstart, perm, sorted_word, frs, cs, nullptr, grids,
+                         stream);
 }
 
 }  // extern "C"

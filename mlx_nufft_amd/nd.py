@@ -263,20 +263,24 @@ class Type1PlanND(_PointsND):
         grid = self._fine_grid(1)
         fk = torch.empty(self.N, dtype=torch.complex64, device=self.device)
         tm = self._timer()
-        if self.pts.kind == "zsweep":
+        self._spread_one(self.pts, cd, grid, tm)
+        self._fft_crop(grid, fk, tm, 1)
+        self._finish_profile(tm)
+        return L.to_host(fk) if return_np else fk
+
+    def _spread_one(self, pts, cd, grid, tm):
+        """grid = spread of cd (caller order) over the points of pts."""
+        if pts.kind == "zsweep":
             with tm("spread"):
-                E.spread_zsweep(self.pts, self.beta, cd, grid)
-        elif self.pts.kind == "ysweep":
+                E.spread_zsweep(pts, self.beta, cd, grid)
+        elif pts.kind == "ysweep":
             with tm("spread"):
-                E.spread_ysweep(self.pts, self.beta, cd, grid)
+                E.spread_ysweep(pts, self.beta, cd, grid)
         else:
             with tm("zero"):
                 E.fill_zero(grid)
             with tm("spread"):
-                E.spread(self.pts, self.beta, cd, grid, accumulate=True)
-        self._fft_crop(grid, fk, tm, 1)
-        self._finish_profile(tm)
-        return L.to_host(fk) if return_np else fk
+                E.spread(pts, self.beta, cd, grid, accumulate=True)
 
     def _fft_crop(self, grid, fk, tm, batch):
         if self._pruned:
@@ -307,8 +311,7 @@ class Type1PlanND(_PointsND):
         tm = self._timer()
         with tm("spread"):
             if self.pts.kind == "zsweep":
-                for b in range(B):
-                    E.spread_zsweep(self.pts, self.beta, cd[b], grids[b])
+                E.spread_zsweep_batch(self.pts, self.beta, cd, grids)
             elif self.pts.kind == "ysweep":
                 E.spread_ysweep(self.pts, self.beta, cd, grids)
             else:
@@ -339,20 +342,32 @@ class Type1PlanND(_PointsND):
 
     def execute_disjoint(self, c, groups, return_np=True):
         """G independent transforms of disjoint point subsets of one plan:
-        out[g] = type-1 of c restricted to {j : groups[j] == g}; (G, *N).
-        ref: nd.py:796-855."""
-        groups = np.asarray(groups.cpu() if isinstance(groups, torch.Tensor) else groups)
-        if groups.shape != (self.P,):
+        out[g] = type-1 of c restricted to {j : groups[j] == g}, G =
+        max(groups) + 1, (G, *N); points with a negative label belong to no
+        subset and empty subsets give zeros. Every point is spread once in
+        total: the plan's sorted point state is partitioned by label with
+        one stable sort, each subset keeps the spread's key order, and the
+        subsets are spread one after another into one fine grid, each
+        followed by its own FFT and crop (ref: nd.py:796-855)."""
+        if isinstance(groups, torch.Tensor):
+            gl = groups.to(device=self.device, dtype=torch.int64)
+        else:
+            gl = torch.from_numpy(np.asarray(groups).astype(np.int64)).to(self.device)
+        if tuple(gl.shape) != (self.P,):
             raise ValueError(f"groups must have shape ({self.P},)")
         cd = self._strengths(c)
-        G = int(groups.max()) + 1 if groups.size else 0
-        if G == 0:
-            out = torch.zeros((0, *self.N), dtype=torch.complex64, device=self.device)
-            return L.to_host(out) if return_np else out
-        gd = torch.from_numpy(groups.astype(np.int64)).to(self.device)
-        sel = gd[None, :] == torch.arange(G, device=self.device)[:, None]
-        cs = torch.where(sel, cd[None, :], torch.zeros((), dtype=cd.dtype, device=self.device))
-        return self.execute_batch(cs.contiguous(), return_np=return_np)
+        G = int(gl.max()) + 1 if gl.numel() else 0
+        out = torch.zeros((max(G, 0), *self.N), dtype=torch.complex64, device=self.device)
+        if G > 0:
+            split = E.GroupSplit(self.pts, gl, G)
+            del gl
+            grid = self._fine_grid(1)
+            tm = self._timer()
+            for g, sub in split:
+                self._spread_one(sub, cd, grid, tm)
+                self._fft_crop(grid, out[g], tm, 1)
+            self._finish_profile(tm)
+        return L.to_host(out) if return_np else out
 
 
 class Type2PlanND(_PointsND):

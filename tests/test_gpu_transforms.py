@@ -356,20 +356,26 @@ def test_type2_3d_sparse_direct_gather(isign, oracle, mn):
     assert not pd._gather_direct()
 
 
-@pytest.mark.parametrize("dim,N", [(1, (200,)), (2, (64, 48)), (3, (32, 24, 20))])
-def test_execute_disjoint(dim, N, oracle, mn):
+@pytest.mark.parametrize("dim,N,method", [(1, (200,), "auto"), (2, (64, 48), "auto"),
+                                          (3, (32, 24, 20), "auto"), (3, (32, 24, 20), "gm"),
+                                          (2, (64, 48), "gm")])
+def test_execute_disjoint(dim, N, method, oracle, mn):
     """ref: nd.py:796-855. G transforms of disjoint point subsets of one plan
-    equal fresh plans of each subset (an empty group gives zeros) and the
-    direct sum, after a re-point that changes P."""
-    print(f"case execute_disjoint dim={dim}", flush=True)
+    equal fresh plans of each subset (an empty group gives zeros, label -1
+    belongs to no group) and the direct sum, after a re-point that changes
+    P; each point state kind (1D tiles, 2D y-sweep, 3D z-sweep, and the
+    tiles forced by "gm") is split by label."""
+    print(f"case execute_disjoint dim={dim} method={method}", flush=True)
     rng = np.random.default_rng(47 + dim)
     eps = 1e-5
-    p = mn.Type1PlanND(tuple(_pts(rng, dim, 9_000)), N, eps=eps)
+    p = mn.Type1PlanND(tuple(_pts(rng, dim, 9_000)), N, eps=eps, spread_method=method)
     M = 12_000
     x = _pts(rng, dim, M)
     p.set_sources(tuple(x))
+    kind = {1: "tiles", 2: "ysweep", 3: "zsweep"}[dim] if method == "auto" else "tiles"
+    assert p.pts.kind == kind
     c = _cplx(rng, M)
-    groups = rng.choice([0, 1, 3], M)          # group 2 stays empty
+    groups = rng.choice([0, 1, 3, -1], M)      # group 2 stays empty
     out = np.asarray(p.execute_disjoint(c, groups))
     assert out.shape == (4, *N)
     assert np.abs(out[2]).max() == 0.0
@@ -377,8 +383,15 @@ def test_execute_disjoint(dim, N, oracle, mn):
     for g in (0, 1, 3):
         sel = groups == g
         xs = [v[sel] for v in x]
-        fresh = mn.Type1PlanND(tuple(xs), N, eps=eps).execute(c[sel])
+        fresh = mn.Type1PlanND(tuple(xs), N, eps=eps, spread_method=method).execute(c[sel])
         assert oracle.rel_l2(out[g], fresh) < 1e-5
+        masked = p.execute(np.where(sel, c, 0))
+        assert oracle.rel_l2(out[g], masked) < 1e-6
         fe = oracle.dft_t1(xs, c[sel], modes, +1)
         ref_err = oracle.rel_l2(oracle.nufft_t1(xs, c[sel], N, eps, +1), fe)
         assert oracle.rel_l2(out[g], fe) <= max(eps, 2 * ref_err)
+    # torch labels on the device (the tile spreads add in atomic order, so
+    # repeats agree to rounding, not bit for bit), and no label at or above 0
+    tg = torch.from_numpy(groups).cuda()
+    assert oracle.rel_l2(np.asarray(p.execute_disjoint(c, tg)), out) < 1e-6
+    assert np.asarray(p.execute_disjoint(c, np.full(M, -1))).shape == (0, *N)

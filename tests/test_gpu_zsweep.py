@@ -210,3 +210,55 @@ def test_zsweep_mfma_strength_range(case, oracle, mn):
     err = oracle.rel_l2(g.cpu().numpy().astype(np.complex128), go)
     print(f"  vs oracle: {err:.2e}")
     assert err < 1e-5
+
+
+@pytest.mark.parametrize("B,presorted", [(1, False), (2, False), (3, True), (5, False)])
+def test_zsweep_batch(B, presorted, oracle, mn):
+    """The two-vector z-sweep equals the one-vector spread bit for bit for
+    every vector (same MFMA sequence per accumulator, same per-vector power
+    of two scale), whatever the vectors' magnitudes; vector 0 also against
+    the oracle."""
+    from mlx_nufft_amd import _engine as E
+
+    print(f"case zsweep batch B={B} presorted={presorted}", flush=True)
+    rng = np.random.default_rng(40 + B)
+    M, N = 30_000, (32, 40, 36)
+    x = [rng.uniform(-np.pi, np.pi, M) for _ in range(3)]
+    x[2][: M // 3] = rng.uniform(-0.2, 0.2, M // 3)   # a dense slab: full batches
+    p = mn.Type1PlanND(tuple(x), N, eps=1e-5)
+    assert p.pts.kind == "zsweep"
+    scales = [1.0, 1e-30, 1e30, 3e-3, 7.0]
+    cs = np.stack([(rng.standard_normal(M) + 1j * rng.standard_normal(M)) * scales[b]
+                   for b in range(B)]).astype(np.complex64)
+    cs[B - 1, ::7] = 0
+    cd = torch.from_numpy(cs).cuda()
+    if presorted:
+        cd = cd[:, p.pts.perm.long()].contiguous()
+    grids = torch.full((B, *p.n_up), float("nan"), dtype=torch.complex64, device="cuda")
+    E.spread_zsweep_batch(p.pts, p.beta, cd, grids, presorted=presorted)
+    one = torch.empty(p.n_up, dtype=torch.complex64, device="cuda")
+    for b in range(B):
+        one.fill_(float("nan"))
+        E.spread_zsweep(p.pts, p.beta, cd[b].contiguous(), one, presorted=presorted)
+        assert torch.equal(grids[b].view(torch.int64), one.view(torch.int64)), b
+    i1o, fro = oracle.setpts_t12(x, p.n_up, p.w)
+    go = oracle.spread(i1o, fro, cs[0], p.n_up, p.w, p.beta)
+    assert oracle.rel_l2(grids[0].cpu().numpy(), go) < 1e-5
+
+
+def test_execute_batch_3d(oracle, mn):
+    """Type-1 execute_batch in 3D against execute per vector and the direct
+    sum (ref: nd.py:744-794)."""
+    print("case execute_batch 3D", flush=True)
+    rng = np.random.default_rng(47)
+    M, N, B, eps = 8000, (16, 20, 12), 3, 1e-6
+    x = [rng.uniform(-np.pi, np.pi, M) for _ in range(3)]
+    cs = (rng.standard_normal((B, M)) + 1j * rng.standard_normal((B, M))).astype(np.complex64)
+    p = mn.Type1PlanND(tuple(x), N, eps=eps)
+    assert p.pts.kind == "zsweep"
+    fb = p.execute_batch(cs)
+    assert fb.shape == (B, *N)
+    modes = [np.arange(-(n // 2), n - n // 2) for n in N]
+    for b in range(B):
+        assert oracle.rel_l2(fb[b], p.execute(cs[b])) < 1e-6
+        assert oracle.rel_l2(fb[b], oracle.dft_t1(x, cs[b], modes, +1)) < 1e-5
