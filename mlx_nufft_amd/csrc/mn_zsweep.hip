@@ -3,7 +3,9 @@
 //
 // Layout. The grid is cut into 8x8 (x, y) column blocks; one wavefront owns
 // a block over a z-segment (a multiple of 8 cells) and sweeps it upwards in
-// z-chunks of 8 cells. Each 4x4 column quadrant of the block keeps its
+// z-chunks of 8 cells. The block's columns form four 4x4 "quadrants" by
+// parity (x = 2i + qx, y = 2j + qy for i, j < 4), so that a lane's two x
+// (and two y) columns are adjacent in memory; each quadrant keeps its
 // z-window in two matrix-core accumulators (v_mfma_f32_16x16x32_f16 tiles:
 // rows are the quadrant's 16 cells, columns 16 consecutive z-slots), one for
 // the real and one for the imaginary part. The window spans the chunk being
@@ -23,13 +25,14 @@
 // Per batch (up to 64 points of one chunk, a lane per point):
 //  * prologue: the lane evaluates the W ES weights of each axis once (3W
 //    evaluations) and writes them at their cells: x- and y-weights into the
-//    point's row of the weight table, as pairs (w[a], w[a + 4]) over the
-//    block's 8 columns (zero elsewhere), and B = c w_z, already split into
-//    fp16 hi + lo, into four slot-major tables (re hi, re lo, im hi, im lo;
-//    [slot][point], zero elsewhere).
+//    point's row of the weight table (the block's 8 columns in order, zero
+//    elsewhere; taps off the block land in unread padding), and B = c w_z,
+//    already split into fp16 hi + lo, into four slot-major tables (re hi,
+//    re lo, im hi, im lo; [slot][point], zero elsewhere).
 //  * K-steps of 32 points: lane (li, lk) = (l % 16, l / 16) supplies
 //    A[li][8 lk + t] and B[8 lk + t][li] for t < 8: it reads its 8 points'
-//    weight pairs and its B column (one 16-byte read per table), and for
+//    weight pairs (columns 2 (li / 4) + {0, 1} and rows 2 (li % 4) + {0, 1},
+//    one 8-byte read each) and its B column (one 16-byte read per table), and for
 //    each quadrant forms A = wx wy and splits it -- hi = the f32 product
 //    rounded toward zero to fp16 (a truncation, identical on every
 //    conversion path), lo = fp16(fma(wx, wy, -hi)), which also keeps the f32
@@ -40,10 +43,10 @@
 //    that none of a K-step's 32 points meets was measured: a K-step mixes
 //    so many classes that it spared 3 % of the MFMAs and was no faster.)
 // After a chunk, slots 0..7 are complete: lane (li < 8, lk) stores slot li
-// of cells (4 qx + lk, 4 qy + r) straight from the accumulators (four lanes
+// of cells (2 lk + qx, 2 r + qy) straight from the accumulators (four lanes
 // per column write one 64-byte run, aligned because segments and chunks
-// start at multiples of 8 cells), and DPP row_shl:8 shifts every
-// accumulator down by 8 slots, filling zeros.
+// start at multiples of 8 cells) with non-temporal stores, and DPP
+// row_shl:8 shifts every accumulator down by 8 slots, filling zeros.
 //
 // Scale. A is stored times 2^14 (2^7 per axis) and B times 2^s, a per-wave
 // power of two with |B| < 2^14: set by the first batch and lowered (the
@@ -72,15 +75,21 @@ namespace {
 constexpr int ZB = kZsBlock;  // block size along x and y
 constexpr int ZC = kZsChunk;  // z-steps per chunk
 constexpr int NR = 4;         // key ranges per chunk: own, -x, -y, -xy
-// floats per weight-table row: wx pairs [8], wy pairs [8], pad. The K-step's
-// four lane groups read rows 8 apart: 144 dwords, 16 banks apart.
-constexpr int ROW = 18;
+// Weight-table row (floats): the x-weight of block column X at XO + X and
+// the y-weight of row Y at YO + Y, X, Y in [0, 8). A point writes its W taps
+// at XO + ox + a (ox in [1 - W, 8)): the taps off the block land in the
+// slots around the two data runs, which are never read, so a tap's slot is
+// a constant offset from the point's base and needs no index arithmetic.
+// The K-step's four lane groups read rows 8 apart: 336 dwords, 16 banks
+// apart.
+constexpr int XO = 8, YO = 24, ROW = 42;
 // halves per B-table slot row: 64 points + pad. 36 dwords: the 16 slots of a
 // quarter-wave's 16-byte reads start 4 (9 li mod 16) banks in, all apart.
 constexpr int BST = 72;
 constexpr int kTab = 16 * BST;  // halves per B table
 
 typedef float mf4 __attribute__((ext_vector_type(4)));
+typedef float mf2 __attribute__((ext_vector_type(2)));
 typedef _Float16 mh8 __attribute__((ext_vector_type(8)));
 
 template <int SH>
@@ -240,6 +249,15 @@ __device__ __forceinline__ void split_prod8(const float (&x)[8], const float (&y
     for (int t = 0; t < 8; ++t) lo[t] = (_Float16)__builtin_fmaf(x[t], y[t], -(float)hi[t]);
 }
 
+// ES weight exp(beta (sqrt(1 - z^2) - 1)) at the scaled distance z, as
+// exp2(bl2e sqrt|1 - z^2| - bl2e): |z| <= 1 for every tap up to rounding,
+// and the absolute value (a free source modifier) stands in for a clamp.
+__device__ __forceinline__ float zs_es(float z, float bl2e) {
+    const float t = __builtin_fmaf(-z, z, 1.0f);
+    return __builtin_amdgcn_exp2f(
+        __builtin_fmaf(bl2e, __builtin_amdgcn_sqrtf(__builtin_fabsf(t)), -bl2e));
+}
+
 // Wave-wide maximum of a small non-negative integer (< 512), by ballots.
 __device__ __forceinline__ int wave_max9(int v) {
     int m = 0;
@@ -289,11 +307,11 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
         }
     }
     int zb = z0 - ZC;  // z of slot 0
-    // cell (4 qx + lk, 4 qy + r) of the block at z: a wave-uniform column
-    // base per (q, r) plus the lane's offset lk n1 n2 + z (< 2^31: the key
+    // cell (2 lk + qx, 2 r + qy) of the block at z: a wave-uniform column
+    // base per (q, r) plus the lane's offset 2 lk n1 n2 + z (< 2^31: the key
     // space bounds n0 n1 n2 by 2^28)
     const int64_t gblk = ((int64_t)ZB * bx * n1 + ZB * by) * n2;
-    const int loff = lk * n1 * n2;
+    const int loff = 2 * lk * n1 * n2;
 
     // Slots 0..7 are complete: store the owned ones, shift the window by 8.
     auto advance = [&]() __attribute__((always_inline)) {
@@ -306,10 +324,14 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         float2 *gq = grid + v * gstride + gblk +
-                                     ((int64_t)(4 * (q >> 1)) * n1 + 4 * (q & 1) + r) * n2;
-                        gq[loff + z] =
-                            make_float2(__builtin_amdgcn_ldexpf(are[v][q][r], -14 - sexp[v]),
-                                        __builtin_amdgcn_ldexpf(aim[v][q][r], -14 - sexp[v]));
+                                     ((int64_t)(q >> 1) * n1 + (q & 1) + 2 * r) * n2;
+                        // streaming store: each cell is written once and
+                        // next read by the FFT; kept out of the caches it
+                        // leaves them to the point and strength reads
+                        // (measured 0.1-0.16 ms less per 512^3 spread)
+                        const mf2 val = {__builtin_amdgcn_ldexpf(are[v][q][r], -14 - sexp[v]),
+                                         __builtin_amdgcn_ldexpf(aim[v][q][r], -14 - sexp[v])};
+                        __builtin_nontemporal_store(val, reinterpret_cast<mf2 *>(gq + loff + z));
                     }
         }
 #pragma unroll
@@ -335,11 +357,12 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
             cv[v] = valid ? make_float2(cp[v].x * p.pv.x - cp[v].y * p.pv.y,
                                         cp[v].x * p.pv.y + cp[v].y * p.pv.x)
                           : make_float2(0.f, 0.f);
-            // the batch's largest strength is below 2^(e - 126)
+            // the scale is lowered when a strength reaches 2^(141 - sexp - 127);
+            // then the batch's largest strength is below 2^(e - 126)
             const float mx = fmaxf(fabsf(cv[v].x), fabsf(cv[v].y));
-            const int e = wave_max9((__float_as_int(mx) >> 23) & 0xff);
-            const int want = min(140 - e, 139);
-            if (sexp[v] == INT32_MIN || want < sexp[v]) {
+            const int eb = (__float_as_int(mx) >> 23) & 0xff;
+            if (sexp[v] == INT32_MIN || __ballot(eb > 140 - sexp[v])) {
+                const int want = min(140 - wave_max9(eb), 139);
                 if (sexp[v] != INT32_MIN) {
 #pragma unroll
                     for (int q = 0; q < 4; ++q)
@@ -349,7 +372,7 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
                             aim[v][q][r] = __builtin_amdgcn_ldexpf(aim[v][q][r], want - sexp[v]);
                         }
                 }
-                sexp[v] = want;
+                sexp[v] = want;  // below the old scale whenever one was set
             }
         }
         // the window moves up to the batch's chunk (the cursor is
@@ -365,9 +388,13 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
         }
         __syncthreads();  // the previous batch's K-steps are done with the tables
         {
-            float2 *rz = reinterpret_cast<float2 *>(rows + lane * ROW);
+            float2 *rzx = reinterpret_cast<float2 *>(rows + lane * ROW + XO);
+            float2 *rzy = reinterpret_cast<float2 *>(rows + lane * ROW + YO);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) rz[i] = make_float2(0.f, 0.f);
+            for (int i = 0; i < 4; ++i) {
+                rzx[i] = make_float2(0.f, 0.f);
+                rzy[i] = make_float2(0.f, 0.f);
+            }
             float4 *bz = reinterpret_cast<float4 *>(&btab[0][0]);
             constexpr int nb4 = VB * 4 * kTab / 8;  // float4 count of the B tables
 #pragma unroll
@@ -385,31 +412,27 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
             for (int v = 0; v < VB; ++v)
                 cb[v] = make_float2(__builtin_amdgcn_ldexpf(cv[v].x, sexp[v]),
                                     __builtin_amdgcn_ldexpf(cv[v].y, sexp[v]));
-            float *row = rows + lane * ROW;
-            float wx[W], wy[W], wz[W];
+            // tap a of each axis goes to a constant offset from the point's
+            // base (taps off the block land in unread slots)
+            float *rx = rows + lane * ROW + XO + ox;
+            float *ry = rows + lane * ROW + YO + oy;
+            _Float16 *bt = &btab[0][0] + sz * BST + lane;
             constexpr float ih = 2.0f / W;
 #pragma unroll
             for (int a = 0; a < W; ++a) {
-                wx[a] = es_weight_z(((float)a - p.fx) * ih, bl2e);
-                wy[a] = es_weight_z(((float)a - p.fy) * ih, bl2e);
-                wz[a] = es_weight_z(((float)a - p.fz) * ih, bl2e);
-            }
-#pragma unroll
-            for (int a = 0; a < W; ++a) {
-                // taps outside the block go to the row's pad slot (no branch)
-                const int x = ox + a, y = oy + a;
-                const int ix = (unsigned)x < (unsigned)ZB ? 2 * (x & 3) + (x >> 2) : 16;
-                const int iy = (unsigned)y < (unsigned)ZB ? 8 + 2 * (y & 3) + (y >> 2) : 16;
-                row[ix] = wx[a] * kAxisScale;
-                row[iy] = wy[a] * kAxisScale;
-                const int o = (sz + a) * BST + lane;
+                // scaled distance (a - f) 2/w of tap a, one fma
+                const float ca = (float)a * ih;
+                rx[a] = zs_es(__builtin_fmaf(-p.fx, ih, ca), bl2e) * kAxisScale;
+                ry[a] = zs_es(__builtin_fmaf(-p.fy, ih, ca), bl2e) * kAxisScale;
+                const float wz = zs_es(__builtin_fmaf(-p.fz, ih, ca), bl2e);
 #pragma unroll
                 for (int v = 0; v < VB; ++v) {
-                    const auto h = __builtin_amdgcn_cvt_pkrtz(cb[v].x * wz[a], cb[v].y * wz[a]);
-                    btab[v][o] = h[0];
-                    btab[v][kTab + o] = (_Float16)__builtin_fmaf(cb[v].x, wz[a], -(float)h[0]);
-                    btab[v][2 * kTab + o] = h[1];
-                    btab[v][3 * kTab + o] = (_Float16)__builtin_fmaf(cb[v].y, wz[a], -(float)h[1]);
+                    _Float16 *o = bt + v * 4 * kTab + a * BST;
+                    const auto h = __builtin_amdgcn_cvt_pkrtz(cb[v].x * wz, cb[v].y * wz);
+                    o[0] = h[0];
+                    o[kTab] = (_Float16)__builtin_fmaf(cb[v].x, wz, -(float)h[0]);
+                    o[2 * kTab] = h[1];
+                    o[3 * kTab] = (_Float16)__builtin_fmaf(cb[v].y, wz, -(float)h[1]);
                 }
             }
         }
@@ -420,8 +443,8 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
                 const float *rr = rows + (e0 + 8 * lk + t) * ROW;
-                const float2 px = *reinterpret_cast<const float2 *>(rr + 2 * (li >> 2));
-                const float2 py = *reinterpret_cast<const float2 *>(rr + 8 + 2 * (li & 3));
+                const float2 px = *reinterpret_cast<const float2 *>(rr + XO + 2 * (li >> 2));
+                const float2 py = *reinterpret_cast<const float2 *>(rr + YO + 2 * (li & 3));
                 wx0[t] = px.x;
                 wx1[t] = px.y;
                 wy0[t] = py.x;
