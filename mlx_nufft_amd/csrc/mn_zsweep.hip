@@ -75,14 +75,22 @@ namespace {
 constexpr int ZB = kZsBlock;  // block size along x and y
 constexpr int ZC = kZsChunk;  // z-steps per chunk
 constexpr int NR = 4;         // key ranges per chunk: own, -x, -y, -xy
-// Weight-table row (floats): the x-weight of block column X at XO + X and
-// the y-weight of row Y at YO + Y, X, Y in [0, 8). A point writes its W taps
-// at XO + ox + a (ox in [1 - W, 8)): the taps off the block land in the
-// slots around the two data runs, which are never read, so a tap's slot is
-// a constant offset from the point's base and needs no index arithmetic.
-// The K-step's four lane groups read rows 8 apart: 336 dwords, 16 banks
-// apart.
-constexpr int XO = 8, YO = 24, ROW = 42;
+// Weight-table row (floats) for width W: the x-weight of block column X at
+// XO + X and the y-weight of row Y at YO + Y, X, Y in [0, 8). A point writes
+// its W taps at XO + ox + a (ox in [1 - W, 8)): the taps off the block land
+// in the slots around the two data runs, which are never read, so a tap's
+// slot is a constant offset from the point's base and needs no index
+// arithmetic. XO and YO are even (8-byte pair reads); ROW is 2 mod 4, so the
+// K-step's four lane groups, which read rows 8 apart, start 16 banks apart.
+template <int W>
+struct RowLayout {
+    static constexpr int XO = (W - 1 + 1) & ~1;
+    static constexpr int YO = (XO + W + 7 + 1) & ~1;
+    static constexpr int ROW = ((YO + W + 7) + 3) / 4 * 4 + 2;
+};
+// rows and B entries of point positions 64..71 stay zero: K-step lanes past
+// a batch part read this group
+constexpr int kZeroGroup = 8;
 // halves per B-table slot row: 64 points + pad. 36 dwords: the 16 slots of a
 // quarter-wave's 16-byte reads start 4 (9 li mod 16) banks in, all apart.
 constexpr int BST = 72;
@@ -192,14 +200,17 @@ __device__ __forceinline__ void cur_load(Cursor &k, const Ranges &rg, int c, int
 }
 
 // One lane's point of a batch, its loads issued (the strength, which needs
-// src, is loaded one batch later).
+// src, is loaded one batch later). A batch takes up to 64 points from the
+// current chunk (part A, lanes [0, nA)) and, when that chunk ends first, the
+// head of the next chunk (part B, lanes [oB, oB + nB) from the next multiple
+// of 8), so that the prologue runs on full batches across chunk ends.
 struct ZPoint {
-    int c, nb;        // the batch's chunk and size (uniform; nb = 0: done)
-    bool valid;
-    int r;            // the point's range (source block)
-    uint32_t wd, src; // sorted word; index of its strength in c
+    int cA, nA, cB, oB, nB;  // uniform; nA = 0: done
+    bool valid, inB;
+    int r;                   // the point's range (source block)
+    uint32_t wd, src;        // sorted word; index of its strength in c
     float fx, fy, fz;
-    float2 pv;        // prephase (1 if none)
+    float2 pv;               // prephase (1 if none)
 };
 
 template <bool PRE>
@@ -213,12 +224,30 @@ __device__ __forceinline__ ZPoint zp_next(Cursor &k, const Ranges &rg, int lane,
         while (k.bat >= k.tot && k.c <= k.clast) cur_load(k, rg, k.c + 1, lane);
     }
     ZPoint q;
-    q.c = k.c;
-    q.nb = k.c <= k.clast ? min(64, k.tot - k.bat) : 0;
-    q.valid = lane < q.nb;
-    const int e = k.bat + lane;
-    const int r = (e >= k.p1 ? 1 : 0) + (e >= k.p2 ? 1 : 0) + (e >= k.p3 ? 1 : 0);
-    const int dj = r == 0 ? k.dj0 : (r == 1 ? k.dj1 : (r == 2 ? k.dj2 : k.dj3));
+    q.cA = k.c;
+    q.nA = k.c <= k.clast ? min(64, k.tot - k.bat) : 0;
+    q.cB = k.c + 1;
+    q.oB = (q.nA + 7) & ~7;
+    q.nB = 0;
+    // part A: elements bat + lane of the current chunk
+    const int eA = k.bat + lane;
+    int r = (eA >= k.p1 ? 1 : 0) + (eA >= k.p2 ? 1 : 0) + (eA >= k.p3 ? 1 : 0);
+    int dj = r == 0 ? k.dj0 : (r == 1 ? k.dj1 : (r == 2 ? k.dj2 : k.dj3));
+    int e = eA;
+    k.bat += q.nA;
+    if (q.nA > 0 && q.oB < 64 && k.c + 1 <= k.clast) {
+        // part B: the head of the next chunk, whose bounds were prefetched
+        cur_load(k, rg, k.c + 1, lane);
+        q.nB = min(64 - q.oB, k.tot);
+        k.bat = q.nB;
+        if (lane >= q.oB) {
+            e = lane - q.oB;
+            r = (e >= k.p1 ? 1 : 0) + (e >= k.p2 ? 1 : 0) + (e >= k.p3 ? 1 : 0);
+            dj = r == 0 ? k.dj0 : (r == 1 ? k.dj1 : (r == 2 ? k.dj2 : k.dj3));
+        }
+    }
+    q.inB = lane >= q.oB;
+    q.valid = lane < q.nA || (q.inB && lane < q.oB + q.nB);
     const uint32_t j = q.valid ? (uint32_t)(e + dj) : 0u;
     q.r = r;
     q.wd = word[j];
@@ -231,7 +260,6 @@ __device__ __forceinline__ ZPoint zp_next(Cursor &k, const Ranges &rg, int lane,
         q.pv = pre[j];
     else
         q.pv = make_float2(1.f, 0.f);
-    k.bat += 64;
     return q;
 }
 
@@ -282,7 +310,8 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
     static_assert(W >= 2 && W <= ZB && ZC + W - 1 <= 16, "footprint exceeds the 16 slots");
     static_assert(VB == 1 || VB == 2, "one or two strength vectors per wave");
     constexpr float kAxisScale = 128.0f;
-    __shared__ __align__(16) float rows[64 * ROW];
+    constexpr int XO = RowLayout<W>::XO, YO = RowLayout<W>::YO, ROW = RowLayout<W>::ROW;
+    __shared__ __align__(16) float rows[(8 * kZeroGroup + 8) * ROW];
     __shared__ __align__(16) _Float16 btab[VB][4 * kTab];
     int bx, by, seg;
     zs_block(xcd_remap(blockIdx.x, (int64_t)nbx * nby * nseg), nbx, nby, bx, by, seg);
@@ -346,9 +375,74 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
         zb += ZC;
     };
 
+    // the window moves up to chunk c (the cursor is chunk-major): usually
+    // one step, straight-line code (a loop that stores makes the compiler
+    // wait for every outstanding load before it)
+    auto window_to = [&](int c) __attribute__((always_inline)) {
+        const int zt = ZC * (c < -1 ? -1 : c);
+        if (zb < zt) {
+            advance();
+            if (zb < zt) {
+                advance();
+                while (zb < zt) advance();
+            }
+        }
+    };
+
+    // K-steps of 32 points over the 8-point groups [g0, g1) of the tables;
+    // lanes past g1 read the zero group
+    auto ksteps = [&](int g0, int g1) __attribute__((always_inline)) {
+        for (int gs = g0; gs < g1; gs += 4) {
+            const int pos = 8 * (gs + lk < g1 ? gs + lk : kZeroGroup);
+            float wx0[8], wx1[8], wy0[8], wy1[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const float *rr = rows + (pos + t) * ROW;
+                const float2 px = *reinterpret_cast<const float2 *>(rr + XO + 2 * (li >> 2));
+                const float2 py = *reinterpret_cast<const float2 *>(rr + YO + 2 * (li & 3));
+                wx0[t] = px.x;
+                wx1[t] = px.y;
+                wy0[t] = py.x;
+                wy1[t] = py.y;
+            }
+            mh8 ah[4], al[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                split_prod8((q >> 1) ? wx1 : wx0, (q & 1) ? wy1 : wy0, ah[q], al[q]);
+            const int bo = li * BST + pos;
+#pragma unroll
+            for (int v = 0; v < VB; ++v) {
+                const mh8 brh = *reinterpret_cast<const mh8 *>(&btab[v][bo]);
+                const mh8 brl = *reinterpret_cast<const mh8 *>(&btab[v][kTab + bo]);
+                const mh8 bih = *reinterpret_cast<const mh8 *>(&btab[v][2 * kTab + bo]);
+                const mh8 bil = *reinterpret_cast<const mh8 *>(&btab[v][3 * kTab + bo]);
+                // consecutive MFMAs go to different accumulators: each of
+                // the 8 tiles of a vector is used again only 8 instructions
+                // later
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    are[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], brh, are[v][q], 0, 0, 0);
+                    aim[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], bih, aim[v][q], 0, 0, 0);
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    are[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], brl, are[v][q], 0, 0, 0);
+                    aim[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], bil, aim[v][q], 0, 0, 0);
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    are[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[q], brh, are[v][q], 0, 0, 0);
+                    aim[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[q], bih, aim[v][q], 0, 0, 0);
+                }
+            }
+        }
+    };
+
     auto process = [&](const ZPoint &p, const float2 (&cp)[VB]) __attribute__((always_inline)) {
-        int wc, off;
-        chunk_pos(p.c, wrap_off, wc, off);
+        int wcA, offA, wcB, offB;
+        chunk_pos(p.cA, wrap_off, wcA, offA);
+        chunk_pos(p.cB, wrap_off, wcB, offB);
+        const int off = p.inB ? offB : offA;
         // points of chunk -2 below the reach of z = 0 take no part
         const bool valid = p.valid && (int)(p.wd >> 29) + off >= 0;
         float2 cv[VB];
@@ -375,17 +469,7 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
                 sexp[v] = want;  // below the old scale whenever one was set
             }
         }
-        // the window moves up to the batch's chunk (the cursor is
-        // chunk-major): usually one step, straight-line code (a loop that
-        // stores makes the compiler wait for every outstanding load before it)
-        const int zt = ZC * wc;
-        if (zb < zt) {
-            advance();
-            if (zb < zt) {
-                advance();
-                while (zb < zt) advance();
-            }
-        }
+        window_to(p.cA);
         __syncthreads();  // the previous batch's K-steps are done with the tables
         {
             float2 *rzx = reinterpret_cast<float2 *>(rows + lane * ROW + XO);
@@ -403,7 +487,7 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
         __syncthreads();
         if (valid) {
             // first tap relative to this block (minus 8 for points of the -x
-            // / -y neighbour blocks) and its slot in the window
+            // / -y neighbour blocks) and its slot in its chunk's window
             const int ox = (int)((p.wd >> 23) & 7u) - ((p.r & 1) ? ZB : 0);
             const int oy = (int)((p.wd >> 26) & 7u) - ((p.r & 2) ? ZB : 0);
             const int sz = (int)(p.wd >> 29) + off;
@@ -437,49 +521,11 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
             }
         }
         __syncthreads();
-        // K-steps of 32 points; rows and B entries past the batch are zero
-        for (int e0 = 0; e0 < p.nb; e0 += 32) {
-            float wx0[8], wx1[8], wy0[8], wy1[8];
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                const float *rr = rows + (e0 + 8 * lk + t) * ROW;
-                const float2 px = *reinterpret_cast<const float2 *>(rr + XO + 2 * (li >> 2));
-                const float2 py = *reinterpret_cast<const float2 *>(rr + YO + 2 * (li & 3));
-                wx0[t] = px.x;
-                wx1[t] = px.y;
-                wy0[t] = py.x;
-                wy1[t] = py.y;
-            }
-            mh8 ah[4], al[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-                split_prod8((q >> 1) ? wx1 : wx0, (q & 1) ? wy1 : wy0, ah[q], al[q]);
-            const int bo = li * BST + e0 + 8 * lk;
-#pragma unroll
-            for (int v = 0; v < VB; ++v) {
-                const mh8 brh = *reinterpret_cast<const mh8 *>(&btab[v][bo]);
-                const mh8 brl = *reinterpret_cast<const mh8 *>(&btab[v][kTab + bo]);
-                const mh8 bih = *reinterpret_cast<const mh8 *>(&btab[v][2 * kTab + bo]);
-                const mh8 bil = *reinterpret_cast<const mh8 *>(&btab[v][3 * kTab + bo]);
-                // consecutive MFMAs go to different accumulators: each of
-                // the 8 tiles of a vector is used again only 8 instructions
-                // later
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    are[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], brh, are[v][q], 0, 0, 0);
-                    aim[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], bih, aim[v][q], 0, 0, 0);
-                }
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    are[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], brl, are[v][q], 0, 0, 0);
-                    aim[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], bil, aim[v][q], 0, 0, 0);
-                }
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    are[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[q], brh, are[v][q], 0, 0, 0);
-                    aim[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[q], bih, aim[v][q], 0, 0, 0);
-                }
-            }
+        // part A in its chunk's window, then part B in the next chunk's
+        ksteps(0, (p.nA + 7) >> 3);
+        if (p.nB > 0) {
+            window_to(p.cB);
+            ksteps(p.oB >> 3, (p.oB + p.nB + 7) >> 3);
         }
     };
 
@@ -488,6 +534,8 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
         for (int v = 0; v < VB; ++v) cv[v] = c[v * cstride + p.src];
     };
 
+    // the zero group's rows (the B tables are cleared with every batch)
+    for (int i = lane; i < 8 * ROW; i += 64) rows[8 * kZeroGroup * ROW + i] = 0.f;
     const int clast = (zend - 1) / ZC;  // the last chunk of the segment
     const Ranges rg{bx, by, bxm - bx, bym - by, nby, nzc, clast, zstart};
     Cursor cur;
@@ -500,15 +548,15 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
     ZPoint pb = zp_next<PRE>(cur, rg, lane, perm, word, frs, pre);
     ZPoint pc;
     for (;;) {
-        if (pa.nb == 0) break;
+        if (pa.nA == 0) break;
         pc = zp_next<PRE>(cur, rg, lane, perm, word, frs, pre);
         strengths(pb, cb);
         process(pa, ca);
-        if (pb.nb == 0) break;
+        if (pb.nA == 0) break;
         pa = zp_next<PRE>(cur, rg, lane, perm, word, frs, pre);
         strengths(pc, cc);
         process(pb, cb);
-        if (pc.nb == 0) break;
+        if (pc.nA == 0) break;
         pb = zp_next<PRE>(cur, rg, lane, perm, word, frs, pre);
         strengths(pa, ca);
         process(pc, cc);
