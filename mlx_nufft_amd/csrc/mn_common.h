@@ -120,6 +120,20 @@ __device__ __forceinline__ float es_weight(float d, float bl2e, float inv_hw) {
     return __builtin_amdgcn_exp2f(bl2e * (__builtin_amdgcn_sqrtf(t) - 1.0f));
 }
 
+// The same kernel with the exponent written -bl2e z^2 / (1 + sqrt(1 - z^2)),
+// equal to bl2e (sqrt(1 - z^2) - 1) in exact arithmetic but free of its
+// cancellation near z = 0, where the fp32 rounding of the square root would
+// enter the weight multiplied by beta (about 1e-6 relative at beta = 16).
+// Used where the grid's error is amplified afterwards (the type-3 spread,
+// whose inner grid is deconvolved twice).
+__device__ __forceinline__ float es_weight_stable(float d, float bl2e, float inv_hw) {
+    const float z = d * inv_hw;
+    const float z2 = z * z;
+    const float t = fmaxf(1.0f - z2, 0.0f);
+    return __builtin_amdgcn_exp2f(-bl2e * z2 *
+                                  __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_sqrtf(t)));
+}
+
 // The same kernel at the scaled distance z = 2d/w: the exp2 argument
 // bl2e*(sqrt(t) - 1) is one fma. For |z| > 1 it returns e^-beta (t clamped
 // to 0); callers mask those taps.

@@ -53,8 +53,9 @@ __device__ __forceinline__ int local_cell(int i1, int hw, int n, int b, int m) {
 
 // F64: the strength times its prephase and every tap product are formed in
 // fp64 and the grid is complex128 (flushed with fp64 atomics), so the grid
-// carries no white fp32 rounding noise; the ES weights stay fp32 (their
-// error is a smooth function of the fraction).
+// carries no white fp32 rounding noise; the ES weights stay fp32, evaluated
+// without the cancellation of sqrt(1 - z^2) - 1 (es_weight_stable: at eps
+// 1e-6 the plain fp32 exponent alone doubled the type-3 error).
 template <int DIM, int W, bool BATCH, bool F64>
 __global__ __launch_bounds__(256) void k_spread_tiled(Geom g, float bl2e, float inv_hw,
                                                       int64_t nsub, const int32_t *__restrict__ info,
@@ -94,7 +95,9 @@ __global__ __launch_bounds__(256) void k_spread_tiled(Geom g, float bl2e, float 
             ok = ok && loc[d] >= 0;
             const float f = frs.p[d][j];
 #pragma unroll
-            for (int a = 0; a < W; ++a) wt[d][a] = es_weight((float)a - f, bl2e, inv_hw);
+            for (int a = 0; a < W; ++a)
+                wt[d][a] = F64 ? es_weight_stable((float)a - f, bl2e, inv_hw)
+                               : es_weight((float)a - f, bl2e, inv_hw);
         }
         if (!ok) continue;  // cannot happen for keys built by setpts
         float2 pv = make_float2(1.0f, 0.0f);
@@ -309,7 +312,8 @@ __global__ __launch_bounds__(OWN_THREADS) void k_spread_owner(
             const float f = frs.p[d][j];
 #pragma unroll
             for (int a = 0; a < W; ++a)
-                wt[d - 1][a] = loc[d - 1][a] < cnt[d] ? es_weight((float)a - f, bl2e, inv_hw) : 0.0f;
+                wt[d - 1][a] =
+                    loc[d - 1][a] < cnt[d] ? es_weight_stable((float)a - f, bl2e, inv_hw) : 0.0f;
         }
         const float f0 = frs.p[0][j];
         const float2 c0 = c[perm[j]];
@@ -325,7 +329,7 @@ __global__ __launch_bounds__(OWN_THREADS) void k_spread_owner(
             int v0 = a0 - a00;
             v0 += v0 < 0 ? g.n[0] : 0;
             if (v0 >= cnt[0]) continue;
-            const double w0 = (double)es_weight((float)a0 - f0, bl2e, inv_hw);
+            const double w0 = (double)es_weight_stable((float)a0 - f0, bl2e, inv_hw);
             const double r0 = cvx * w0, i0 = cvy * w0;
 #pragma unroll
             for (int a1 = 0; a1 < W; ++a1) {

@@ -109,12 +109,32 @@ int or_stable_sort(int64_t P, const uint32_t *key, int64_t nkeys, uint32_t *perm
     return 0;
 }
 
+/* Weight precision of taps(): 0 = fp64 ES kernel; 1 = the fp32 evaluation
+ * exp2(beta log2(e) (sqrt(max(1 - z^2, 0)) - 1)) with z = (a - fr) (2/w),
+ * every step rounded to fp32 (a CPU emulation: the GPU's hardware exp2/sqrt
+ * carry about 1 ulp of their own); 2 = the same in fp32 with the exponent
+ * written -beta log2(e) z^2 / (1 + sqrt(1 - z^2)). Products and sums stay
+ * fp64 either way. Test infrastructure, set per process. */
+static int g_weights_f32 = 0;
+
+void or_set_weights_f32(int mode) { g_weights_f32 = mode; }
+
+static double es_f32(float d, double beta, int w) {
+    const float z = d * (2.0f / (float)w);
+    const float t = fmaxf(1.0f - z * z, 0.0f);
+    const float bl2e = (float)(beta * 1.4426950408889634);
+    if (g_weights_f32 == 2)  /* sqrt(t) - 1 = -z^2 / (1 + sqrt(t)): no cancellation */
+        return (double)exp2f(-bl2e * (z * z) / (1.0f + sqrtf(t)));
+    return (double)exp2f(bl2e * (sqrtf(t) - 1.0f));
+}
+
 /* Taps of one point along one dim: wrapped cell indices and ES weights. */
 static void taps(int32_t i1, float fr, int64_t n, int w, double beta, int64_t *cell,
                  double *wt) {
     for (int a = 0; a < w; ++a) {
         cell[a] = pmod64((int64_t)i1 + a, n);
-        wt[a] = es((double)a - (double)fr, beta, w);
+        wt[a] = g_weights_f32 ? es_f32((float)a - fr, beta, w)
+                              : es((double)a - (double)fr, beta, w);
     }
 }
 

@@ -63,6 +63,7 @@ def lib():
         L.or_dft_t1.argtypes = [ctypes.c_int, i64, vp, vp, vp, vp, ctypes.c_int, vp]
         L.or_dft_t2.argtypes = [ctypes.c_int, vp, vp, vp, ctypes.c_int, i64, vp, vp]
         L.or_dft_t3.argtypes = [i64, vp, vp, vp, ctypes.c_int, i64, vp, vp]
+        L.or_set_weights_f32.argtypes = [ctypes.c_int]
         _lib = L
     return _lib
 
@@ -188,26 +189,47 @@ def stable_sort(key, nkeys):
 
 # --------------------------------------------------------- spread/interp ---
 
-def spread(i1, fr, c, n, w, beta):
-    """fp64 spread onto the periodic grid n (complex128 array of shape n)."""
+class _weights_f32:
+    """Within the block the oracle's spread and interp evaluate the ES
+    weights in fp32 (products and sums stay fp64): True or "f32" as the
+    GPU's type-1/2 kernels do, "f32-stable" with the exponent rewritten
+    without cancellation, as the GPU's type-3 spread does."""
+
+    def __init__(self, mode):
+        self.mode = {False: 0, True: 1, "f32": 1, "f32-stable": 2}[mode]
+
+    def __enter__(self):
+        lib().or_set_weights_f32(self.mode)
+
+    def __exit__(self, *exc):
+        lib().or_set_weights_f32(0)
+
+
+def spread(i1, fr, c, n, w, beta, weights_f32=False):
+    """fp64 spread onto the periodic grid n (complex128 array of shape n);
+    weights_f32 evaluates the ES weights in fp32 (the GPU's formula)."""
     dim, P = i1.shape
     grid = np.zeros(tuple(n), np.complex128)
     cc = np.ascontiguousarray(np.asarray(c, dtype=np.complex128).ravel())
     nn = np.asarray(list(n) + [1] * (3 - dim), np.int64)
     i1c = [np.ascontiguousarray(i1[d]) for d in range(dim)]
     frc = [np.ascontiguousarray(fr[d]) for d in range(dim)]
-    lib().or_spread(dim, P, _pa(i1c), _pa(frc), _p(cc), _p(nn), int(w), float(beta), _p(grid))
+    with _weights_f32(weights_f32):
+        lib().or_spread(dim, P, _pa(i1c), _pa(frc), _p(cc), _p(nn), int(w), float(beta),
+                        _p(grid))
     return grid
 
 
-def interp(i1, fr, grid, w, beta):
+def interp(i1, fr, grid, w, beta, weights_f32=False):
     dim, P = i1.shape
     g = np.ascontiguousarray(grid, dtype=np.complex128)
     nn = np.asarray(list(g.shape) + [1] * (3 - dim), np.int64)
     out = np.empty(P, np.complex128)
     i1c = [np.ascontiguousarray(i1[d]) for d in range(dim)]
     frc = [np.ascontiguousarray(fr[d]) for d in range(dim)]
-    lib().or_interp(dim, P, _pa(i1c), _pa(frc), _p(g), _p(nn), int(w), float(beta), _p(out))
+    with _weights_f32(weights_f32):
+        lib().or_interp(dim, P, _pa(i1c), _pa(frc), _p(g), _p(nn), int(w), float(beta),
+                        _p(out))
     return out
 
 
@@ -332,16 +354,20 @@ def t3_setup(x, s, eps=1e-5, isign=+1, upsampfac=1.25, prec="crit64"):
     return out
 
 
-def nufft_t3(x, c, s, eps=1e-5, isign=+1, upsampfac=1.25, spread64=True):
+def nufft_t3(x, c, s, eps=1e-5, isign=+1, upsampfac=1.25, spread64=True,
+             weights_f32=(False, False)):
     """CPU type-3 (3D), following ref_t3.py:48-221 with the crit64 setup of
     t3_setup: all stages fp64, or with the spread stage in fp32
     (spread64=False, the reference's most precision-sensitive fp32 stage,
-    ref: harness/diagnose_ref.py:21-41)."""
+    ref: harness/diagnose_ref.py:21-41). weights_f32 = (spread, interp)
+    evaluates the ES weights of that fp64 stage in fp32 as the GPU does."""
     st = t3_setup(x, s, eps, isign, upsampfac, "crit64")
     w, beta, nf, n_up = st["w"], st["beta"], st["nf"], st["n_up"]
-    b = (spread if spread64 else spread_f32)(st["i1"], st["fr"],
-                                             np.asarray(c, np.complex128) * st["pre"], nf, w,
-                                             beta)
+    cp = np.asarray(c, np.complex128) * st["pre"]
+    if spread64:
+        b = spread(st["i1"], st["fr"], cp, nf, w, beta, weights_f32=weights_f32[0])
+    else:
+        b = spread_f32(st["i1"], st["fr"], cp, nf, w, beta)
     decs = []
     for d in range(3):
         q = np.arange(-nf[d] // 2, nf[d] // 2, dtype=np.float64)
@@ -350,7 +376,7 @@ def nufft_t3(x, c, s, eps=1e-5, isign=+1, upsampfac=1.25, spread64=True):
     H[np.ix_(*[np.arange(-nf[d] // 2, nf[d] // 2) % n_up[d] for d in range(3)])] = \
         b * _outer(decs)
     v = _fftn(H, isign)
-    return interp(st["t_i1"], st["t_fr"], v, w, beta) * st["post"]
+    return interp(st["t_i1"], st["t_fr"], v, w, beta, weights_f32=weights_f32[1]) * st["post"]
 
 
 # ----------------------------------------------------------- direct sums ---

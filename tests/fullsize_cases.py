@@ -24,6 +24,18 @@ def _mode_sample(N, per_dim):
             for n in N]
 
 
+def _mode_sample_edges(N, per_dim):
+    """per_dim distinct modes per axis (sorted): both ends of the modeord-0
+    box, -(n // 2) and n - n // 2 - 1, plus per_dim - 2 drawn from between."""
+    rng = np.random.default_rng(100)
+    out = []
+    for n in N:
+        lo, hi = -(n // 2), n - n // 2 - 1
+        mid = rng.choice(np.arange(lo + 1, hi), per_dim - 2, replace=False)
+        out.append(np.sort(np.concatenate([[lo, hi], mid])))
+    return out
+
+
 def _point_sample(P, count):
     rng = np.random.default_rng(100)
     return np.sort(rng.choice(P, count, replace=False))
@@ -66,15 +78,16 @@ def cfg2_2d_t2_radial():
 
 
 def cfg3_3d_t1():
-    """3D type-1: M = 2e7, N = 256^3, eps 1e-5, isign +1; a 4 x 4 x 4
-    sub-grid of modes is sampled (the type-2 round trip samples 64 points)."""
+    """3D type-1: M = 2e7, N = 256^3, eps 1e-5, isign +1; an 8 x 8 x 8
+    sub-grid of modes, including both ends of every axis, is sampled (the
+    type-2 round trip samples 512 points)."""
     rng = np.random.default_rng(0)
     M = 20_000_000
     x = [rng.uniform(-PI, PI, M) for _ in range(3)]
     c = _cplx(rng, M)
     N = (256, 256, 256)
-    return {"x": x, "c": c, "N": N, "eps": 1e-5, "isign": +1, "modes": _mode_sample(N, 4),
-            "points": _point_sample(M, 64)}
+    return {"x": x, "c": c, "N": N, "eps": 1e-5, "isign": +1,
+            "modes": _mode_sample_edges(N, 8), "points": _point_sample(M, 512)}
 
 
 def cfg4_3d_t3():

@@ -119,10 +119,12 @@ def test_t3_small_anisotropic_precisions(prec, oracle, mn):
     The contract bound is max(eps, 2 x the reference's own error); that
     pipeline spreads in fp32 (ref_t3.py:168), whose error the oracle's
     spread64=False restatement gives (2.5e-5 here at eps 1e-6). This engine
-    is also held within 3x the all-fp64 restatement's error: at eps 1e-6 it
-    sits at about 2.3x (7.6e-6 against 3.3e-6). A complex128 inner grid
-    leaves that unchanged, so the grid's complex64 rounding is not the
-    cause."""
+    is also held to the all-fp64 restatement's error: within 1.2x with fp64
+    coordinates and phases (3.49e-6 against 3.33e-6 at eps 1e-6), within
+    1.5x when the phases are fp32 (4.6e-6, the mode's own rounding). The
+    spread's fp32 ES weights are evaluated without the cancellation of
+    sqrt(1 - z^2) - 1; in the plain form they alone put the error at 7.6e-6
+    (the oracle's fp32-weight emulation gives 7.2e-6)."""
     print(f"case t3 small anisotropic prec={prec}", flush=True)
     x, c, s = gen_anisotropic(64, 2000, 0.02)
     fd = oracle.dft_t3(x, c, s, +1)
@@ -134,7 +136,7 @@ def test_t3_small_anisotropic_precisions(prec, oracle, mn):
         print(f"  eps={eps:.0e} err={err:.3e} fp64 restatement {ref64:.3e} "
               f"fp32-spread restatement {ref32:.3e}", flush=True)
         assert err <= max(eps, 2 * ref32)
-        assert err <= max(eps, 3 * ref64)
+        assert err <= max(eps, (1.2 if prec in ("crit64", "coords64") else 1.5) * ref64)
     if prec == "crit64":
         ones = np.ones(s[0].size)
         fa = mn.Type3Plan(s, x, eps=1e-5, isign=-1).execute(ones.astype(np.complex64))

@@ -146,6 +146,36 @@ def test_zsweep_matches_tiles(mn, monkeypatch):
     assert torch.equal(gp, gz)
 
 
+def test_zsweep_matches_tiles_bench_grid(mn, monkeypatch):
+    """The bench's grid (3D type-1, M = 2e7 uniform points, N = 256^3,
+    eps 1e-5: a 512^3 fine grid, w = 6): the z-sweep's split-fp16 MFMA
+    products against the tile spread's fp32 products accumulated in fp64,
+    over the whole grid. Gate 1e-6 relative l2 (fp32 rounding of the weight
+    products and of the stored grid is about 1e-7)."""
+    from mlx_nufft_amd import _engine as E
+
+    print("case zsweep vs tiles at 512^3, M=2e7", flush=True)
+    rng = np.random.default_rng(0)
+    M = 20_000_000
+    x = tuple(torch.from_numpy(rng.uniform(-np.pi, np.pi, M)).cuda() for _ in range(3))
+    c = torch.from_numpy((rng.standard_normal(M) + 1j * rng.standard_normal(M))
+                         .astype(np.complex64)).cuda()
+    pz = mn.Type1PlanND(x, (256, 256, 256), eps=1e-5)
+    assert pz.pts.kind == "zsweep" and pz.w == 6 and list(pz.n_up) == [512] * 3
+    gz = torch.empty(pz.n_up, dtype=torch.complex64, device="cuda")
+    E.spread_zsweep(pz.pts, pz.beta, c, gz)
+    del pz
+    monkeypatch.setenv("MN_SPREAD", "tiles")
+    pt = mn.Type1PlanND(x, (256, 256, 256), eps=1e-5)
+    assert pt.pts.kind == "tiles"
+    gt = torch.empty(pt.n_up, dtype=torch.complex64, device="cuda")
+    E.spread(pt.pts, pt.beta, c, gt)
+    rel = float((gz - gt).abs().norm() / gt.abs().norm())
+    worst = float((gz - gt).abs().max() / gt.abs().max())
+    print(f"  rel l2 {rel:.3e}, max |diff| / max |grid| {worst:.3e}")
+    assert rel < 1e-6
+
+
 @pytest.mark.parametrize("N,eps", [((64, 64, 48), 1e-5), ((32, 48, 40), 1e-7), ((48, 32, 64), 1e-2)])
 def test_zsweep_segments(N, eps, oracle, mn):
     """Segments of 8, 16, 128 and 256 cells (8 and 16 put a segment edge in

@@ -299,3 +299,29 @@ def test_type3_setup_modes(oracle, prec):
             assert not np.array_equal(st["fr"], ref["fr"])
         if p32:
             assert not np.array_equal(st["pre"], ref["pre"])
+
+
+def test_f32_weight_emulation_modes(oracle):
+    """The oracle's fp32 ES-weight emulations, used to locate the type-3
+    error at eps 1e-6: on a 3D spread at sigma 1.25 (beta 16.5 and 18.3) the
+    plain fp32 exponent beta (sqrt(1 - z^2) - 1) is off the fp64 grid by
+    about beta x 3e-8 (the square root's rounding, multiplied by beta where
+    the exponent cancels), while -beta z^2 / (1 + sqrt(1 - z^2)) in fp32 is
+    off by about one fp32 rounding. A dropped term or a wrong sign in either
+    form would move its grid far outside these bands."""
+    for eps in (1e-5, 1e-6):
+        w, beta = oracle.kernel_params(eps, 1.25)
+        rng = np.random.default_rng(3)
+        P, n = 4000, (48, 40, 36)
+        x = [rng.uniform(-np.pi, np.pi, P) for _ in range(3)]
+        c = rng.standard_normal(P) + 1j * rng.standard_normal(P)
+        i1, fr = oracle.setpts_t12(x, n, w)
+        g64 = oracle.spread(i1, fr, c, n, w, beta)
+        e_plain = oracle.rel_l2(oracle.spread(i1, fr, c, n, w, beta, weights_f32="f32"), g64)
+        e_stable = oracle.rel_l2(
+            oracle.spread(i1, fr, c, n, w, beta, weights_f32="f32-stable"), g64)
+        assert 2e-7 < e_plain < 2e-6, (eps, e_plain)
+        assert 1e-8 < e_stable < 2e-7, (eps, e_stable)
+        assert e_stable < e_plain / 4
+        # the default restores fp64 weights
+        assert oracle.rel_l2(oracle.spread(i1, fr, c, n, w, beta), g64) == 0.0
