@@ -53,10 +53,12 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--exec-only", action="store_true",
                     help="time execute() only (plan built once), for profiling")
-    ap.add_argument("--workload", choices=["t1", "t3-generic"], default="t1",
+    ap.add_argument("--workload", choices=["t1", "t3-generic", "t1-1d", "t3"], default="t1",
                     help="t1: the north-star line (default). t3-generic: the reference's "
                          "type-3 Table I case (generic geometry, 1e6 sources on a 640^3 "
-                         "grid, M = N^2 targets), execute() only")
+                         "grid, M = N^2 targets), execute() only. t1-1d and t3: "
+                         "BASELINE.json configs[0] (1D type-1) and configs[4] (3D type-3), "
+                         "execute() only, for profiling their spread paths")
     ap.add_argument("--t3-N", type=int, default=1024, choices=[512, 1024, 2048],
                     help="t3-generic: targets M = N^2")
     ap.add_argument("--copy-calibration", type=float, default=0.0, metavar="GIB",
@@ -191,6 +193,45 @@ def bench_t3(args):
     print(json.dumps(out))
 
 
+def bench_other(args):
+    """execute() of BASELINE.json configs[0] (1D type-1: M = 1e5, N = 4096,
+    eps 1e-6) or configs[4] (3D type-3: 1e6 sources in [-1, 1]^3, 1e6
+    targets in [-200, 200]^3, eps 1e-5), the plan built once and the
+    strengths resident in HBM; one JSON line with the time per execute."""
+    import numpy as np
+    import torch
+
+    import mlx_nufft_amd as mn
+    from mlx_nufft_amd import _lib
+
+    _lib.require_gpu()
+    rng = np.random.default_rng(0)
+    if args.workload == "t1-1d":
+        M = 100_000
+        x = (rng.uniform(-np.pi, np.pi, M),)
+        plan = mn.Type1PlanND(x, (4096,), eps=1e-6, isign=+1)
+        cfg = {"workload": "1D type-1 M=1e5 N=4096 eps=1e-6 (BASELINE.json configs[0])"}
+    else:
+        M = 1_000_000
+        x = tuple(rng.uniform(-1.0, 1.0, M) for _ in range(3))
+        s = tuple(rng.uniform(-200.0, 200.0, M) for _ in range(3))
+        plan = mn.Type3Plan(x, s, eps=1e-5, isign=+1)
+        cfg = {"workload": "3D type-3 1e6 x 1e6 eps=1e-5 (BASELINE.json configs[4])"}
+    c = (rng.standard_normal(M) + 1j * rng.standard_normal(M)).astype(np.complex64)
+    cd = torch.from_numpy(c).cuda()
+    for _ in range(args.warmup):
+        plan.execute(cd, return_np=False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        plan.execute(cd, return_np=False)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    print(json.dumps({"metric": "execute time", "value": ms, "unit": "ms", "n_gpus": 1,
+                      "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+                      "higher_is_better": False, "config": cfg}))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -202,6 +243,9 @@ def main():
         return
     if args.workload == "t3-generic":
         bench_t3(args)
+        return
+    if args.workload in ("t1-1d", "t3"):
+        bench_other(args)
         return
     import numpy as np
     import torch
