@@ -265,6 +265,32 @@ int mn_spread_zsweep_batch(const mn_bins *g, float beta, int64_t P, int64_t B, i
                            const void *cs, void *grids, mn_stream_t stream);
 
 /*
+ * Z-gather interpolation, the fast path for 3D type-2 on z-sweep geometries
+ * (same checks as mn_spread_zsweep). Point state: mn_zgather_setpts writes
+ * the z-sweep word with the key ((bx*(n1/8) + by)*ceil(n2/8) + z/8)*16 +
+ * 2*(x cell of the first tap in its block) -- the points of a block and
+ * z-chunk ordered by that x cell; bits 23-31 as for the spread -- and the
+ * fractions; sort and build zstart exactly as for the spread
+ * (mn_zsweep_nkeys, mn_sort_pairs, mn_zsweep_starts). Each
+ * wavefront owns an 8x8 column block over a z-segment of zseg cells (a
+ * positive multiple of 8), holds the (8 + w - 1)^2 window columns x 16
+ * z-slots of the grid as fp16 hi/lo MFMA operands (v_mfma_f32_16x16x32_f16,
+ * three products per term, about 2^-22 relative, f32 accumulation, a
+ * power-of-two scale per 8 z-slots so any finite grid magnitude is handled)
+ * and interpolates every point whose first tap lies in the block exactly
+ * once; a tile of 16 points runs the matrix cores only over the x columns
+ * its footprints cover. grids: B fine grids of n0*n1*n2 complex64; outs: B
+ * rows of P complex64, written in caller order (outs[b][perm[j]]).
+ * ref: nd.py:974-1073 (output-driven gather), nd.py:298-372 (bin sort).
+ */
+int mn_zgather_setpts(const mn_bins *g, int64_t P, const double *const x[3], int prec64,
+                      uint32_t *word, float *const fr[3], mn_stream_t stream);
+int mn_interp_zgather(const mn_bins *g, float beta, int64_t P, int64_t B, int zseg,
+                      const int32_t *zstart, const uint32_t *perm, const uint32_t *sorted_word,
+                      const float *const frs[3], const void *grids, void *outs,
+                      mn_stream_t stream);
+
+/*
  * Owner-computes 2D spread ("y-sweep"), the fast path for 2D type-1 grids
  * with n0 a multiple of 64 (>= 128), w <= 8 and (n0/64)*n1*2 <= 2^26 keys.
  * Each wavefront owns 64 consecutive x-columns over a y-segment of yseg

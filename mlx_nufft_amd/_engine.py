@@ -232,17 +232,19 @@ def zsweep_eligible(dim, w, n_up):
 
 
 class ZSweepPoints:
-    """Point state for the z-sweep spread: packed point words and fractions
-    (setpts), stably sorted together by the z-sweep key, and the key start
+    """Point state for the z-sweep spread (gather=False, kind "zsweep") or
+    the z-gather interpolation (gather=True, kind "zgather"): packed point
+    words and fractions (setpts), stably sorted together by the z-sweep key
+    (points of a block and z-chunk grouped by class for the spread, ordered
+    by the x cell of their first tap for the gather), and the key start
     table. Given the previous point set of the same plan (prev) with the
     same P and geometry, its device buffers are reused, so re-pointing
     allocates nothing; prev's contents are overwritten in stream order."""
 
-    kind = "zsweep"
-
-    def __init__(self, bins, x64, prec64, prev=None):
+    def __init__(self, bins, x64, prec64, prev=None, gather=False):
         lib = L.lib()
         dev = x64[0].device
+        self.kind = "zgather" if gather else "zsweep"
         self.bins = bins
         self.P = P = x64[0].numel()
         self.K = K = int(lib.mn_zsweep_nkeys(ctypes.byref(bins)))
@@ -257,9 +259,9 @@ class ZSweepPoints:
 
         word = buf("word_in", P, torch.int32)
         fr = buf("fr_in", (3, P), torch.float32)
-        L.check(lib.mn_zsweep_setpts(ctypes.byref(bins), P, L.ptr3(x64), int(bool(prec64)),
-                                     L.ptr(word), L.ptr3(_rows(fr, 3)), L.stream()),
-                "zsweep setpts")
+        setpts = lib.mn_zgather_setpts if gather else lib.mn_zsweep_setpts
+        L.check(setpts(ctypes.byref(bins), P, L.ptr3(x64), int(bool(prec64)), L.ptr(word),
+                       L.ptr3(_rows(fr, 3)), L.stream()), f"{self.kind} setpts")
         self.frs = buf("frs", (3, P), torch.float32)
         ws_bytes = int(lib.mn_sort_pairs_workspace_bytes(P, 3))
         self.word, self.perm, _ = sort_pairs(
@@ -538,6 +540,29 @@ def interp_direct_preferred(pts, w, n_up):
     else:
         staged = float(pts.nsub) * float(np.prod([pts.bins.m[d] + w - 1 for d in range(3)]))
     return direct < 5.0 * staged
+
+
+def zgather_preferred(P, w, n_up):
+    """True when the z-gather interpolation should beat the direct gather for
+    P points on the 3D fine grid n_up: the direct gather reads P w^3 taps,
+    the z-gather (8 + w - 1)^2 columns of 8 new z-cells for every 8x8-column
+    block and z-chunk that holds points (16 after a skipped chunk), expected
+    over uniform points. The factor 5 is the crossover measured between the
+    direct and the staged-tile gathers (interp_direct_preferred)."""
+    nchunks = (n_up[0] / 8.0) * (n_up[1] / 8.0) * -(-n_up[2] // 8)
+    lam = float(P) / nchunks
+    busy = nchunks * -np.expm1(-lam)
+    staged = (8 + w - 1) ** 2 * 8.0 * busy * (1.0 + np.exp(-lam))
+    return float(P) * w ** 3 >= 5.0 * staged
+
+
+def interp_zgather(pts, beta, grids, outs, B=1, zseg=ZSEG):
+    """3D interpolation over the z-sweep point state: B grids (B x n_up)
+    into B output vectors of P values in caller order (outs: B x P)."""
+    L.check(L.lib().mn_interp_zgather(ctypes.byref(pts.bins), float(beta), pts.P, int(B),
+                                      int(zseg), L.ptr(pts.zstart), L.ptr(pts.perm),
+                                      L.ptr(pts.word), L.ptr3(pts.fr_rows()), L.ptr(grids),
+                                      L.ptr(outs), L.stream()), "interp_zgather")
 
 
 def interp(pts, beta, grid, out, post=None):

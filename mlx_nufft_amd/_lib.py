@@ -80,6 +80,9 @@ _SIGS = [
                                  VP3, c_vp, c_vp, c_vp, c_vp]),
     ("mn_spread_zsweep_batch", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int64, c_int,
                                        c_vp, c_vp, c_vp, VP3, c_vp, c_vp, c_vp]),
+    ("mn_zgather_setpts", c_int, [ctypes.POINTER(Bins), c_int64, VP3, c_int, c_vp, VP3, c_vp]),
+    ("mn_interp_zgather", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int64, c_int, c_vp,
+                                  c_vp, c_vp, VP3, c_vp, c_vp, c_vp]),
     ("mn_permute_c64", c_int, [c_int64, c_vp, c_vp, c_vp, c_vp]),
     ("mn_ysweep_nkeys", c_int64, [ctypes.POINTER(Bins)]),
     ("mn_ysweep_setpts", c_int, [ctypes.POINTER(Bins), c_int64, ctypes.c_void_p * 2, c_int, c_vp,

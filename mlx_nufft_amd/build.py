@@ -39,9 +39,17 @@ def _run(cmd):
     return p
 
 
+# Per-source additions. The z-gather reads its MFMA results with VALU code
+# right away: in the VGPR form of the MFMAs they need no copy out of the
+# accumulation registers (one v_accvgpr_read per result element otherwise).
+EXTRA_FLAGS = {
+    "mn_zgather.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: pathlib.Path) -> pathlib.Path:
     obj = BUILD / (src.stem + ".o")
-    _run([HIPCC, *CFLAGS, "-c", str(src), "-o", str(obj)])
+    _run([HIPCC, *CFLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)])
     return obj
 
 

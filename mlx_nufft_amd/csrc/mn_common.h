@@ -216,6 +216,18 @@ __device__ __forceinline__ uint32_t zs_word(int x, int y, int z, int n1, int nzc
     return key | ((uint32_t)lx << 23) | ((uint32_t)ly << 26) | ((uint32_t)lz << 29);
 }
 
+// The z-gather interpolation sorts the same word with a key that orders
+// the points of a (block, chunk) by the x cell of their first tap instead of
+// by class: key = ((bx*nby + by)*nzc + zc)*16 + 2*lx, so the key space, the
+// chunk starts (zstart at multiples of 16) and the word's upper bits are
+// those of zs_word.
+__device__ __forceinline__ uint32_t zg_word(int x, int y, int z, int n1, int nzc) {
+    const int lx = x & (kZsBlock - 1), ly = y & (kZsBlock - 1), lz = z & (kZsChunk - 1);
+    const uint32_t blk = (uint32_t)((x / kZsBlock) * (n1 / kZsBlock) + y / kZsBlock);
+    const uint32_t key = (blk * (uint32_t)nzc + (uint32_t)(z / kZsChunk)) * 16u + 2u * (uint32_t)lx;
+    return key | ((uint32_t)lx << 23) | ((uint32_t)ly << 26) | ((uint32_t)lz << 29);
+}
+
 // Validate a z-sweep geometry (3D, 2 <= w <= 8, n0 and n1 multiples of 8 and
 // >= 16, key space within kZsKeyBits); number of keys
 // K = nbx*nby*ceil(n2/8)*16.

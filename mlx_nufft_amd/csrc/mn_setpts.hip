@@ -76,8 +76,10 @@ __global__ void k_setpts_t12(int64_t P, D3 x, Geom g, double h0, double h1, doub
     key[j] = k;
 }
 
-// 3D type-1 setup for the z-sweep spread: the same cells and fractions, and
-// the packed point word (zs_word) instead of a bin key.
+// 3D setup for the z-sweep spread (GATHER false) and the z-gather
+// interpolation (GATHER true): the same cells and fractions, and the packed
+// point word (zs_word, zg_word) instead of a bin key.
+template <bool GATHER>
 __global__ void k_zs_setpts(int64_t P, D3 x, int n0, int n1, int n2, int w, double h0, double h1,
                             double h2, int prec64, uint32_t *__restrict__ word, F3 fro) {
     int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -88,8 +90,11 @@ __global__ void k_zs_setpts(int64_t P, D3 x, int n0, int n1, int n2, int w, doub
     cell_t12(x.p[0][j], h0, halfw, prec64, ix, fx);
     cell_t12(x.p[1][j], h1, halfw, prec64, iy, fy);
     cell_t12(x.p[2][j], h2, halfw, prec64, iz, fz);
-    word[j] = zs_word(pmod(ix, n0), pmod(iy, n1), pmod(iz, n2), n1, (n2 + kZsChunk - 1) / kZsChunk,
-                      w);
+    const int nzc = (n2 + kZsChunk - 1) / kZsChunk;
+    if constexpr (GATHER)
+        word[j] = zg_word(pmod(ix, n0), pmod(iy, n1), pmod(iz, n2), n1, nzc);
+    else
+        word[j] = zs_word(pmod(ix, n0), pmod(iy, n1), pmod(iz, n2), n1, nzc, w);
     fro.p[0][j] = fx;
     fro.p[1][j] = fy;
     fro.p[2][j] = fz;
@@ -275,8 +280,8 @@ int mn_setpts_t12(const mn_bins *g, int64_t P, const double *const x[3], int pre
     return MN_OK;
 }
 
-int mn_zsweep_setpts(const mn_bins *g, int64_t P, const double *const x[3], int prec64,
-                     uint32_t *word, float *const fr[3], mn_stream_t stream) {
+static int zs_setpts(bool gather, const mn_bins *g, int64_t P, const double *const x[3],
+                     int prec64, uint32_t *word, float *const fr[3], mn_stream_t stream) {
     clear_error();
     int rc = zsweep_check(g);
     if (rc) return rc;
@@ -291,10 +296,21 @@ int mn_zsweep_setpts(const mn_bins *g, int64_t P, const double *const x[3], int 
         fo.p[d] = fr[d];
         h[d] = kTwoPi / (double)g->n[d];
     }
-    k_zs_setpts<<<blocks_for(P, 256), 256, 0, as_stream(stream)>>>(
+    auto kern = gather ? k_zs_setpts<true> : k_zs_setpts<false>;
+    kern<<<blocks_for(P, 256), 256, 0, as_stream(stream)>>>(
         P, xs, (int)g->n[0], (int)g->n[1], (int)g->n[2], g->w, h[0], h[1], h[2], prec64, word, fo);
     MN_LAUNCH_CHECK("zsweep_setpts");
     return MN_OK;
+}
+
+int mn_zsweep_setpts(const mn_bins *g, int64_t P, const double *const x[3], int prec64,
+                     uint32_t *word, float *const fr[3], mn_stream_t stream) {
+    return zs_setpts(false, g, P, x, prec64, word, fr, stream);
+}
+
+int mn_zgather_setpts(const mn_bins *g, int64_t P, const double *const x[3], int prec64,
+                      uint32_t *word, float *const fr[3], mn_stream_t stream) {
+    return zs_setpts(true, g, P, x, prec64, word, fr, stream);
 }
 
 int mn_ysweep_setpts(const mn_bins *g, int64_t P, const double *const x[2], int prec64,

@@ -68,6 +68,7 @@
 #include <cstring>
 
 #include "mn_common.h"
+#include "mn_zsweep.h"
 
 namespace mn {
 namespace {
@@ -104,27 +105,6 @@ template <int SH>
 __device__ __forceinline__ float row_shl_zero(float v) {
     return __int_as_float(
         __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + SH, 0xf, 0xf, true));
-}
-
-// Workgroup index -> (column block bx, by; z-segment seg). The segment
-// varies slowest; within a segment the blocks go in bands of ZS_BAND
-// consecutive bx rows, bx fastest inside a band. The -x, -y and -xy
-// neighbours of a block, which read the same reaching points, are then
-// dispatched at most ZS_BAND + 1 workgroups earlier (except across a band
-// edge) and run on the same XCD at about the same z. Measured on MI355X with
-// 2e7 uniform points on a 512^3 grid: 18 % less HBM fetch than the
-// segment-fastest order.
-constexpr int ZS_BAND = 16;
-__device__ __forceinline__ void zs_block(int64_t wid, int nbx, int nby, int &bx, int &by,
-                                         int &seg) {
-    const int64_t plane = (int64_t)nbx * nby;
-    seg = (int)(wid / plane);
-    const int64_t r = wid % plane, bandc = (int64_t)ZS_BAND * nby;
-    const int b0 = (int)(r / bandc) * ZS_BAND;
-    const int tx = min(ZS_BAND, nbx - b0);
-    const int local = (int)(r % bandc);
-    by = local / tx;
-    bx = b0 + local % tx;
 }
 
 // The four key ranges of a chunk: range r = source block (bit 0: the -x
@@ -275,26 +255,6 @@ __device__ __forceinline__ void split_prod8(const float (&x)[8], const float (&y
     }
 #pragma unroll
     for (int t = 0; t < 8; ++t) lo[t] = (_Float16)__builtin_fmaf(x[t], y[t], -(float)hi[t]);
-}
-
-// ES weight exp(beta (sqrt(1 - z^2) - 1)) at the scaled distance z, as
-// exp2(bl2e sqrt|1 - z^2| - bl2e): |z| <= 1 for every tap up to rounding,
-// and the absolute value (a free source modifier) stands in for a clamp.
-__device__ __forceinline__ float zs_es(float z, float bl2e) {
-    const float t = __builtin_fmaf(-z, z, 1.0f);
-    return __builtin_amdgcn_exp2f(
-        __builtin_fmaf(bl2e, __builtin_amdgcn_sqrtf(__builtin_fabsf(t)), -bl2e));
-}
-
-// Wave-wide maximum of a small non-negative integer (< 512), by ballots.
-__device__ __forceinline__ int wave_max9(int v) {
-    int m = 0;
-#pragma unroll
-    for (int b = 8; b >= 0; --b) {
-        const int cand = m | (1 << b);
-        if (__ballot(v >= cand)) m = cand;
-    }
-    return m;
 }
 
 #ifndef ZS_OCC

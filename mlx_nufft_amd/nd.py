@@ -16,6 +16,8 @@ grids, else rocFFT + crop). Type 2 runs the adjoint chain: deconvolve +
 zero-pad + FFT -> LDS-tiled interpolation written straight to caller order.
 """
 
+import os
+
 import numpy as np
 import torch
 
@@ -104,7 +106,7 @@ class _PointsND:
             self.bins = E.make_bins(3, self.w, self.n_up, m=E.ZSTREAM_M)
         else:
             self.bins = E.make_bins(self.dim, self.w, self.n_up, cell_bytes=self._cell_bytes)
-        self._zsweep = self._use_zsweep and E.zsweep_eligible(self.dim, self.w, self.n_up)
+        self._zsweep = E.zsweep_eligible(self.dim, self.w, self.n_up) and self._zsweep_wanted()
         if self._zsweep:
             self._zbins = E.make_bins(3, self.w, self.n_up, m=(8, 8, 1))
         self._ysweep = self._use_zsweep and E.ysweep_eligible(self.dim, self.w, self.n_up)
@@ -124,6 +126,13 @@ class _PointsND:
         self._grid = None
         self._pruned = E.fftp_supported(self.n_up)
         self._work = None
+
+    # the z-sweep point state is built in the spread's key order unless set
+    _zgather_points = False
+
+    def _zsweep_wanted(self):
+        """Whether the point state should be the z-sweep's (3D, eligible grids)."""
+        return self._use_zsweep
 
     # -- point state -------------------------------------------------------
 
@@ -155,8 +164,11 @@ class _PointsND:
         if self._zsweep:
             with tm("setpts+sort+tables"):
                 prev = getattr(self, "pts", None)
+                gather = self._zgather_points
+                kind = "zgather" if gather else "zsweep"
+                same = isinstance(prev, E.ZSweepPoints) and prev.kind == kind
                 self.pts = E.ZSweepPoints(self._zbins, x64, self.prec == "crit64",
-                                          prev=prev if isinstance(prev, E.ZSweepPoints) else None)
+                                          prev=prev if same else None, gather=gather)
                 del prev
         elif self._ysweep:
             with tm("setpts+sort+tables"):
@@ -379,6 +391,7 @@ class Type2PlanND(_PointsND):
     _cell_bytes = E.INTERP_CELL_BYTES
     _use_zsweep = False
     _use_zstream = True
+    _zgather_points = True
 
     def __init__(self, x, n_modes, eps=1e-6, isign=-1, upsampfac=2.0, prec="crit64",
                  sort_points=False, spread_method="auto"):
@@ -417,12 +430,24 @@ class Type2PlanND(_PointsND):
             with tm("fft"):
                 E.fft(grid, self.n_up, self.isign)
         with tm("interp"):
-            if self._gather_direct():
+            if self.pts.kind == "zgather":
+                E.interp_zgather(self.pts, self.beta, grid, out)
+            elif self._gather_direct():
                 E.interp_direct(self.pts, self.beta, grid, out)
             else:
                 E.interp(self.pts, self.beta, grid, out)
         self._finish_profile(tm)
         return L.to_host(out) if return_np else out
+
+    def _zsweep_wanted(self):
+        """The z-gather interpolation (over the z-sweep point state) serves
+        "auto" and "od" plans whose points are dense enough on their grid
+        (E.zgather_preferred); MN_INTERP=tiles or zstream keeps those gathers."""
+        if self.dim != 3 or self.spread_method not in ("auto", "od"):
+            return False
+        if os.environ.get("MN_INTERP", "") in ("tiles", "zstream"):
+            return False
+        return E.zgather_preferred(self.P, self.w, self.n_up)
 
     def _gather_direct(self):
         """3D points sparse on the fine grid read their taps directly (no
@@ -430,7 +455,9 @@ class Type2PlanND(_PointsND):
         pts = self.pts
         if getattr(self, "_gd_pts", None) is not pts:
             self._gd_pts = pts
-            if self.spread_method == "gm":
+            if pts.kind == "zgather":
+                self._gd = False
+            elif self.spread_method == "gm":
                 self._gd = self.dim == 3
             else:
                 self._gd = E.interp_direct_preferred(pts, self.w, self.n_up)

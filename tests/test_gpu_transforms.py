@@ -96,14 +96,18 @@ def test_spread_grid_vs_oracle(dim, N, path, oracle, mn, monkeypatch):
 
 
 @pytest.mark.parametrize("dim,N", [(1, (300,)), (2, (64, 48)), (3, (32, 24, 20))])
-def test_interp_vs_oracle(dim, N, oracle, mn):
+def test_interp_vs_oracle(dim, N, oracle, mn, monkeypatch):
+    """The staged-tile interpolation (the 3D z-gather, which dense 3D plans
+    use instead, has its own tests in test_gpu_zgather.py)."""
     from mlx_nufft_amd import _engine as E
 
     print(f"case interp dim={dim} N={N}", flush=True)
     rng = np.random.default_rng(10)
     M = 30_000
     x = _pts(rng, dim, M)
+    monkeypatch.setenv("MN_INTERP", "tiles")
     p = mn.Type2PlanND(tuple(x), N, eps=1e-6)
+    assert p.pts.kind == "tiles"
     g = _cplx(rng, tuple(p.n_up))
     out = torch.empty(M, dtype=torch.complex64, device="cuda")
     E.interp(p.pts, p.beta, torch.from_numpy(g).cuda(), out)
@@ -337,7 +341,7 @@ def test_interp_zstream_vs_tiles(N, eps, cluster, mn, monkeypatch):
 @pytest.mark.parametrize("isign", [+1, -1])
 def test_type2_3d_sparse_direct_gather(isign, oracle, mn):
     """A 3D type-2 with few points on a large grid gathers directly (no
-    staged tiles) and matches the direct sum; a dense one keeps the tiles."""
+    staged tiles) and matches the direct sum; a dense one takes the z-gather."""
     print(f"case t2 sparse direct gather isign={isign}", flush=True)
     rng = np.random.default_rng(41)
     N, M, eps = (96, 80, 64), 3_000, 1e-6
@@ -353,7 +357,7 @@ def test_type2_3d_sparse_direct_gather(isign, oracle, mn):
     print(f"  err={err:.3e} ref_err={ref_err:.3e}")
     assert err <= max(eps, 2 * ref_err)
     pd = mn.Type2PlanND(tuple(_pts(rng, 3, 600_000)), (32, 32, 32), eps=1e-5, isign=isign)
-    assert not pd._gather_direct()
+    assert pd.pts.kind == "zgather" and not pd._gather_direct()
 
 
 @pytest.mark.parametrize("dim,N,method", [(1, (200,), "auto"), (2, (64, 48), "auto"),
