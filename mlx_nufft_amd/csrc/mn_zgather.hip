@@ -29,8 +29,9 @@
 // product exact in f32: four MFMAs per X for the real and imaginary parts.
 // The wx sum runs on the accumulator layout (lane (n, g) holds rows 4g + i
 // of column n), the wz weights and the scales multiply it, and a
-// reduce-scatter over the 16 lanes of a row leaves each of the tile's 8
-// results (4 points x re, im) in two lanes, one of which stores it.
+// reduce-scatter over each 8 lanes of a row (then a sum of the two halves)
+// leaves each of the tile's 8 results (4 points x re, im) in two lanes, one
+// of which stores it.
 //
 // Batches. Up to 64 points (a lane per point): the prologue evaluates the
 // point's 3w ES weights once and writes the tables the tiles read -- its A
@@ -49,6 +50,8 @@
 // and its next writes.
 // ref: nd.py:974-1073 (the reference's output-driven gather this replaces),
 // nd.py:298-372 (its bin sort).
+#include <type_traits>
+
 #include "mn_common.h"
 #include "mn_zsweep.h"
 
@@ -88,6 +91,19 @@ __device__ __forceinline__ uint32_t split_lo(float a, float b, uint32_t hi) {
         : "=&v"(lo)
         : "v"(a), "v"(hi), "v"(b));
     return lo;
+}
+
+// 32-bit LDS address of a __shared__ object
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// v = 16 bytes of LDS at address a + OFF, written in place (lanes the exec
+// mask leaves out keep v); the caller waits (lgkmcnt) before using v
+template <typename T>
+__device__ __forceinline__ void ds_read_b128_into(T &v, uint32_t a, const int off) {
+    static_assert(sizeof(T) == 16, "16-byte operand");
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "+v"(v) : "v"(a), "i"(off) : "memory");
 }
 
 // The uniform description of a batch and one lane's loads for it.
@@ -151,7 +167,7 @@ __global__ __launch_bounds__(64) void k_interp_zgather(
         int y0 = ZB * by + 2 * ya, y1 = y0 + 1;
         if (y0 >= n1) y0 -= n1;
         if (y1 >= n1) y1 -= n1;
-        const bool on0 = yp < NYP, on1 = yp < NYP && 2 * yp + 1 < NX;
+        const bool on0 = yp < NYP;
         const int o0 = y0 * n2 + z, o1 = y1 * n2 + z;
         const int64_t plane = (int64_t)n1 * n2;
         float2 v0[NX], v1[NX];
@@ -159,18 +175,21 @@ __global__ __launch_bounds__(64) void k_interp_zgather(
         for (int X = 0; X < NX; ++X) {
             int x = ZB * bx + X;
             if (x >= n0) x -= n0;
-            const float2 *col = grid + x * plane;
-            v0[X] = col[o0];
-            v1[X] = col[o1];
+            // a uniform column base and 32-bit lane offsets (one address add
+            // per load in the memory unit, none on the VALU)
+            const char *col = reinterpret_cast<const char *>(grid + x * plane);
+            v0[X] = *reinterpret_cast<const float2 *>(col + (uint32_t)o0 * 8u);
+            v1[X] = *reinterpret_cast<const float2 *>(col + (uint32_t)o1 * 8u);
         }
+        // (idle lanes and, for odd NX, the pair's second column Y = NX, which
+        // meets only zero A entries, stage real grid values: finite grids
+        // need no zeroing)
         float mx = 0.f;
 #pragma unroll
-        for (int X = 0; X < NX; ++X) {
-            if (!on0) v0[X] = make_float2(0.f, 0.f);
-            if (!on1) v1[X] = make_float2(0.f, 0.f);
+        for (int X = 0; X < NX; ++X)
             mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v0[X].x), fabsf(v0[X].y)),
                                  fmaxf(fabsf(v1[X].x), fabsf(v1[X].y))));
-        }
+        if (!on0) mx = 0.f;
         // the half's largest magnitude is below 2^(e - 126): scaled by
         // 2^(141 - e) every value is below 2^15
         const int s = 141 - wave_max9((__float_as_int(mx) >> 23) & 0xff);
@@ -196,14 +215,18 @@ __global__ __launch_bounds__(64) void k_interp_zgather(
                 }
             }
             if ((n >> 3) == h) {
+                // read straight into the window registers of this half's
+                // lanes (a plain load and masked merge costs a copy per
+                // register); the reads are waited for here
+                const uint32_t a = lds_addr(stg) + ((g * 8 + (n & 7)) * 8) * 2;
 #pragma unroll
                 for (int X = 0; X < NX; ++X) {
-                    const gh8 v = *reinterpret_cast<const gh8 *>(stg + ((X * 4 + g) * 8 + (n & 7)) * 8);
                     if (part)
-                        bim[X] = v;
+                        ds_read_b128_into(bim[X], a, X * 4 * 8 * 8 * 2);
                     else
-                        bre[X] = v;
+                        ds_read_b128_into(bre[X], a, X * 4 * 8 * 8 * 2);
                 }
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             }
         }
     };
@@ -268,9 +291,37 @@ __global__ __launch_bounds__(64) void k_interp_zgather(
     };
 
     // tiles [t0, t1) of the batch; rows [pb, pe) hold points
+    // The x sums of one tile over the window columns [XS, XS + LEN), as
+    // straight-line code: with no branch between columns the compiler
+    // overlaps each column's MFMA chain and weight read with the next ones
+    // (a branch per column left every step waiting on its own latencies).
+    auto xrun = [&](auto XS, auto LEN, const gh8 &a1, const gh8 &a2, int t, float(&accr)[4],
+                    float(&acci)[4]) __attribute__((always_inline)) {
+        constexpr int xs = decltype(XS)::value, len = decltype(LEN)::value;
+#pragma unroll
+        for (int k = 0; k < len; ++k) {
+            const int X = xs + k;
+            gf4 cr = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bre[X], gf4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            gf4 ci = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bim[X], gf4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            cr = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, bre[X], cr, 0, 0, 0);
+            ci = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, bim[X], ci, 0, 0, 0);
+            const gf4 wv = *reinterpret_cast<const gf4 *>(wxt + X * TROW + 16 * t + 4 * g);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                accr[i] = __builtin_fmaf(wv[i], cr[i], accr[i]);
+                acci[i] = __builtin_fmaf(wv[i], ci[i], acci[i]);
+            }
+        }
+    };
+    // a tile's columns fit a window of XL = w + 2 (x cells of its first and
+    // last rows at most 2 apart, the usual case) or take all NX
+    constexpr int XL = W + 2;
+    using XLc = std::integral_constant<int, XL>;
+
+    // tiles [t0, t1) of the batch; rows [pb, pe) hold points
     auto tiles = [&](int t0, int t1, int pb, int pe) __attribute__((always_inline)) {
         const int esc = -((n >> 3) ? se1 : se0) - 14;
-        const bool b3 = n & 8, b2 = n & 4, b1 = n & 2;
+        const bool b2 = n & 4, b1 = n & 2, b0 = n & 1;
         for (int t = t0; t < t1; ++t) {
             // the tile's rows are in x-cell order: its footprints cover the
             // columns [ox of the first row, ox of the last row + w)
@@ -281,43 +332,44 @@ __global__ __launch_bounds__(64) void k_interp_zgather(
             gh8 a2 = *reinterpret_cast<const gh8 *>(ar + 16);
             if (g >= 2) a2 = gh8{0, 0, 0, 0, 0, 0, 0, 0};
             float accr[4] = {0.f, 0.f, 0.f, 0.f}, acci[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int X = 0; X < NX; ++X) {
-                if (X < xlo || X >= xhi) continue;
-                gf4 cr = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bre[X], gf4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                gf4 ci = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bim[X], gf4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                cr = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, bre[X], cr, 0, 0, 0);
-                ci = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, bim[X], ci, 0, 0, 0);
-                const gf4 wv = *reinterpret_cast<const gf4 *>(wxt + X * TROW + 16 * t + 4 * g);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    accr[i] = __builtin_fmaf(wv[i], cr[i], accr[i]);
-                    acci[i] = __builtin_fmaf(wv[i], ci[i], acci[i]);
-                }
+            if (xhi - xlo <= XL) {
+                const int xs = min(xlo, NX - XL);
+                auto pick = [&](auto... I) __attribute__((always_inline)) {
+                    ((xs == decltype(I)::value ? xrun(I, XLc{}, a1, a2, t, accr, acci) : void()), ...);
+                };
+                static_assert(NX - XL == 5, "six window offsets");
+                pick(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{},
+                     std::integral_constant<int, 2>{}, std::integral_constant<int, 3>{},
+                     std::integral_constant<int, 4>{}, std::integral_constant<int, 5>{});
+            } else {
+                xrun(std::integral_constant<int, 0>{}, std::integral_constant<int, NX>{}, a1, a2, t,
+                     accr, acci);
             }
             const gf4 wz = *reinterpret_cast<const gf4 *>(wzt + n * TROW + 16 * t + 4 * g);
             float v[8];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                v[2 * i] = __builtin_amdgcn_ldexpf(accr[i] * wz[i], esc);
-                v[2 * i + 1] = __builtin_amdgcn_ldexpf(acci[i] * wz[i], esc);
+                v[2 * i] = accr[i] * wz[i];
+                v[2 * i + 1] = acci[i] * wz[i];
             }
-            // reduce-scatter over the row's 16 lanes: lane n ends with the
-            // sum of value n >> 1 (point 4g + (n >> 2), part (n >> 1) & 1)
+            // reduce-scatter over each half row of 8 lanes (one slot scale),
+            // leaving lane n with value n & 7 (point 4g + ((n & 7) >> 1), part
+            // n & 1); unscale; add the two halves
             float u[4], w2[2];
 #pragma unroll
             for (int k = 0; k < 4; ++k)
-                u[k] = (b3 ? v[k + 4] : v[k]) + dpp_f<kDppRowRor8>(b3 ? v[k] : v[k + 4]);
+                u[k] = (b2 ? v[k + 4] : v[k]) + dpp_f<kDppRowHalfMirror>(b2 ? v[k] : v[k + 4]);
 #pragma unroll
             for (int k = 0; k < 2; ++k)
-                w2[k] = (b2 ? u[k + 2] : u[k]) + dpp_f<kDppRowHalfMirror>(b2 ? u[k] : u[k + 2]);
-            float r = (b1 ? w2[1] : w2[0]) + dpp_f<kDppQuadMirror>(b1 ? w2[0] : w2[1]);
-            r += dpp_f<kDppQuadSwap>(r);
+                w2[k] = (b1 ? u[k + 2] : u[k]) + dpp_f<kDppQuadMirror>(b1 ? u[k] : u[k + 2]);
+            float r = (b0 ? w2[1] : w2[0]) + dpp_f<kDppQuadSwap>(b0 ? w2[0] : w2[1]);
+            r = __builtin_amdgcn_ldexpf(r, esc);
+            r += dpp_f<kDppRowRor8>(r);
             // (stores of the results straight from the tile measured 0.15 ms
             // faster than staging a batch's results in LDS for one store)
-            const int p = 16 * t + 4 * g + (n >> 2);
-            if (!(n & 1) && p >= pb && p < pe)
-                reinterpret_cast<float *>(out)[2 * (int64_t)pmt[p] + ((n >> 1) & 1)] = r;
+            const int p = 16 * t + 4 * g + ((n & 7) >> 1);
+            if (n < 8 && p >= pb && p < pe)
+                reinterpret_cast<float *>(out)[2 * (int64_t)pmt[p] + (n & 1)] = r;
         }
     };
 
@@ -352,30 +404,23 @@ __global__ __launch_bounds__(64) void k_interp_zgather(
     // window loads of the next batch go out before this batch's stores:
     // waiting for them then does not wait for the scattered stores, which
     // complete while the next batch is built and swept.
-    // The batch loop is unrolled twice so that the two batches in flight
-    // keep their registers (a copy of a value still loading would wait).
-    auto process = [&](const ZgBatch &cur, const ZgPoint &pc, const ZgBatch &nxt)
-                       __attribute__((always_inline)) {
-        prologue(cur, pc);
-        tiles(0, (cur.nA + 15) >> 4, 0, cur.nA);
-        if (cur.nB > 0) {
-            window_to(cur.cB);
-            tiles(cur.oB >> 4, (cur.oB + cur.nB + 15) >> 4, cur.oB, cur.oB + cur.nB);
-        }
-        if (nxt.nA > 0) window_to(nxt.cA);
-    };
-    ZgBatch b0 = next_batch(), b1;
-    ZgPoint p0 = load_points(b0), p1;
-    window_to(b0.cA);
+    ZgBatch cur = next_batch();
+    ZgPoint pc = load_points(cur);
     for (;;) {
-        b1 = next_batch();
-        p1 = load_points(b1);
-        process(b0, p0, b1);
-        if (b1.nA == 0) break;
-        b0 = next_batch();
-        p0 = load_points(b0);
-        process(b1, p1, b0);
-        if (b0.nA == 0) break;
+        const ZgBatch nxt = next_batch();
+        const ZgPoint pn = load_points(nxt);
+        prologue(cur, pc);
+        // parts A and B through one copy of the window and tile code
+#pragma nounroll
+        for (int part = 0; part < 2; ++part) {
+            if (part == 1 && cur.nB == 0) break;
+            const int p0 = part ? cur.oB : 0, p1 = part ? cur.oB + cur.nB : cur.nA;
+            window_to(part ? cur.cB : cur.cA);
+            tiles(p0 >> 4, (p1 + 15) >> 4, p0, p1);
+        }
+        if (nxt.nA == 0) break;
+        cur = nxt;
+        pc = pn;
     }
 }
 
