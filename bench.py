@@ -104,16 +104,18 @@ def cpu_baseline(x, c, N, eps):
 def spread_traffic(kernel):
     """HBM bytes per spread launch (FETCH_SIZE + WRITE_SIZE, calibrated) from
     the committed rocprofv3 summary, with its provenance. The summary records
-    the kernel it measured and the SHA-256 of the kernel's source file at
-    the time; when either differs from what runs now, the figure is stale and
-    traffic is reported as None."""
+    the kernel it measured and the SHA-256 of the kernel's sources at the
+    time (mn_zsweep.hip followed by the mn_zsweep.h it includes); when either
+    differs from what runs now, the figure is stale and traffic is reported
+    as None."""
     import hashlib
 
     tf = ROOT / "profiles" / "spread_zsweep_3d_t1_M2e7_N256_traffic.json"
-    src = ROOT / "mlx_nufft_amd" / "csrc" / "mn_zsweep.hip"
+    csrc = ROOT / "mlx_nufft_amd" / "csrc"
     try:
         d = json.loads(tf.read_text())
-        sha = hashlib.sha256(src.read_bytes()).hexdigest()
+        sha = hashlib.sha256(b"".join((csrc / f).read_bytes()
+                                      for f in ("mn_zsweep.hip", "mn_zsweep.h"))).hexdigest()
     except (ValueError, OSError):
         return None, {"file": str(tf.relative_to(ROOT)), "status": "missing"}
     info = {"file": str(tf.relative_to(ROOT)), "kernel": d.get("kernel"),
