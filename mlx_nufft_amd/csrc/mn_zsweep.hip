@@ -114,7 +114,10 @@ struct Ranges {
     int bx, by, dbx, dby, nby, nzc, clast;
     const int32_t *zstart;
     // (st, en) of range `lane` (lanes 0..3) of chunk c (c = -1 is the last
-    // chunk, periodically); (0, 0) for other lanes and for chunks past clast
+    // chunk, periodically); an empty range (both zstart[0]) for other lanes
+    // and for chunks past clast. The loaded values are returned as they are
+    // (a select on them here would make the wave wait for every load in
+    // flight, the prefetched point data included, as soon as they issue).
     __device__ __forceinline__ int2 fetch(int c, int lane) const {
         const int r = lane & 3;
         const bool ok = lane < NR && c <= clast;
@@ -123,8 +126,7 @@ struct Ranges {
         const int lo = (r & 1) ? 3 : 0;
         const int hi = r == 0 ? 16 : (r == 1 ? 15 : 12);
         const int64_t kb = ok ? ((int64_t)blk * nzc + cc) * 16 : 0;
-        const int st = zstart[kb + (ok ? lo : 0)], en = zstart[kb + (ok ? hi : 0)];
-        return make_int2(ok ? st : 0, ok ? en : 0);
+        return make_int2(zstart[kb + (ok ? lo : 0)], zstart[kb + (ok ? hi : 0)]);
     }
 };
 
@@ -244,17 +246,28 @@ __device__ __forceinline__ ZPoint zp_next(Cursor &k, const Ranges &rg, int lane,
 }
 
 // hi/lo fp16 halves of the products x[t] y[t] (t = 0..7): hi is the f32
-// product rounded toward zero to fp16, lo = fp16(fma(x, y, -hi)).
+// product rounded toward zero to fp16, lo = fp16(fma(x, y, -hi)), each lo
+// one mixed-precision fma that reads hi as fp16 (v_fma_mix{lo,hi}_f16, two
+// per pair, against a conversion, an fma and a conversion per value).
 __device__ __forceinline__ void split_prod8(const float (&x)[8], const float (&y)[8], mh8 &hi,
                                             mh8 &lo) {
+    typedef _Float16 mh2 __attribute__((ext_vector_type(2)));
 #pragma unroll
     for (int t = 0; t < 8; t += 2) {
         const auto h = __builtin_amdgcn_cvt_pkrtz(x[t] * y[t], x[t + 1] * y[t + 1]);
         hi[t] = h[0];
         hi[t + 1] = h[1];
+        uint32_t hb, lb;
+        __builtin_memcpy(&hb, &h, 4);
+        asm("v_fma_mixlo_f16 %0, %1, %2, -%3 op_sel_hi:[0,0,1]\n\t"
+            "v_fma_mixhi_f16 %0, %4, %5, -%3 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+            : "=&v"(lb)
+            : "v"(x[t]), "v"(y[t]), "v"(hb), "v"(x[t + 1]), "v"(y[t + 1]));
+        mh2 l;
+        __builtin_memcpy(&l, &lb, 4);
+        lo[t] = l[0];
+        lo[t + 1] = l[1];
     }
-#pragma unroll
-    for (int t = 0; t < 8; ++t) lo[t] = (_Float16)__builtin_fmaf(x[t], y[t], -(float)hi[t]);
 }
 
 #ifndef ZS_OCC
