@@ -17,10 +17,13 @@ pytestmark = pytest.mark.gpu
 
 # (mode box, eps -> w, clustered at the periodic corner, points): fine grids
 # 64x48x40 (w 7), 16^3 (the smallest, w 7), 80x72x150 (w 4, a partial last
-# z-chunk), 48^3 (w 2), 64x40x30 (w 8, a partial last z-chunk), 32x32x64 (w 6)
+# z-chunk), 48^3 (w 2), 64x40x30 (w 8, a partial last z-chunk), 32x32x64 (w 6),
+# 32x32x12 (w 6: two z-chunks, the second partial, so the 16-slot ring holds
+# every z cell more than once), 32x48x12 (w 3)
 CASES = [((32, 24, 20), 1e-6, False, 30_000), ((8, 8, 8), 1e-6, True, 20_000),
          ((40, 36, 75), 1e-3, False, 200_000), ((24, 24, 24), 1e-1, False, 120_000),
-         ((32, 20, 13), 1e-7, True, 60_000), ((16, 16, 32), 1e-5, False, 50_000)]
+         ((32, 20, 13), 1e-7, True, 60_000), ((16, 16, 32), 1e-5, False, 50_000),
+         ((16, 16, 4), 1e-5, True, 40_000), ((16, 24, 6), 1e-2, False, 30_000)]
 
 
 def _pts(rng, M, cluster):
