@@ -316,27 +316,31 @@ int launch_axis_ti(bool prune_out, int isign, const float2 *in, float2 *out, con
 }
 
 // Lines per workgroup: fp_ti(LOGN) fills 64 KB of LDS. Measured on MI355X
-// at 512^3, a quarter of that for contiguous lines (the last axis) and half
-// for strided ones run fastest: more resident workgroups per CU keep more
-// loads in flight. MN_FFT_TI_SHIFT / MN_FFT_TI_SHIFT_STRIDED override the
-// shifts (tuning).
-int fp_ti_shift(bool contig) {
+// at 512^3, a quarter of that for contiguous lines (the last axis) runs
+// fastest, and for strided ones half when the pass crops its output (type
+// 1: 0.597 ms for the three passes, against 0.625 with a quarter and 0.655
+// with all) and a quarter when it pads its input (type 2: 0.693 ms, against
+// 0.731 with half): more resident workgroups per CU keep more loads in
+// flight. MN_FFT_TI_SHIFT / MN_FFT_TI_SHIFT_STRIDED override the shifts
+// (tuning).
+int fp_ti_shift(bool contig, bool prune_out) {
     static const int vc = [] {
         const char *e = getenv("MN_FFT_TI_SHIFT");
         return e ? atoi(e) : 2;
     }();
     static const int vs = [] {
         const char *e = getenv("MN_FFT_TI_SHIFT_STRIDED");
-        return e ? atoi(e) : 1;
+        return e ? atoi(e) : -1;
     }();
-    return contig ? vc : vs;
+    if (contig) return vc;
+    return vs >= 0 ? vs : (prune_out ? 1 : 2);
 }
 
 template <int LOGN>
 int launch_axis(bool prune_out, int isign, const float2 *in, float2 *out, const AxisArgs &a,
                 hipStream_t s) {
     constexpr int TI = fp_ti(LOGN);
-    const int shift = fp_ti_shift(a.inner == 1);
+    const int shift = fp_ti_shift(a.inner == 1, prune_out);
     if constexpr (TI >= 8) {
         if (shift >= 3) return launch_axis_ti<LOGN, TI / 8>(prune_out, isign, in, out, a, s);
     }
