@@ -409,7 +409,12 @@ __global__ __launch_bounds__(64) void k_interp_zgather(
     for (;;) {
         const ZgBatch nxt = next_batch();
         const ZgPoint pn = load_points(nxt);
+        // compiler-only fences keep the tables' program order (written as
+        // scalars, read as vectors; the wave's LDS operations complete in
+        // issue order, so no wait is needed)
+        asm volatile("" ::: "memory");
         prologue(cur, pc);
+        asm volatile("" ::: "memory");
         // parts A and B through one copy of the window and tile code
 #pragma nounroll
         for (int part = 0; part < 2; ++part) {
