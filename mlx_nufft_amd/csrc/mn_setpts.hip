@@ -79,25 +79,43 @@ __global__ void k_setpts_t12(int64_t P, D3 x, Geom g, double h0, double h1, doub
 // 3D setup for the z-sweep spread (GATHER false) and the z-gather
 // interpolation (GATHER true): the same cells and fractions, and the packed
 // point word (zs_word, zg_word) instead of a bin key.
+// A thread takes ZP_ITEMS points ZP_THREADS apart (coalesced), their
+// coordinate loads all issued before the arithmetic: with one point per
+// thread the kernel waited on memory latency.
+constexpr int ZP_THREADS = 256;
+constexpr int ZP_ITEMS = 4;
 template <bool GATHER>
-__global__ void k_zs_setpts(int64_t P, D3 x, int n0, int n1, int n2, int w, double h0, double h1,
-                            double h2, int prec64, uint32_t *__restrict__ word, F3 fro) {
-    int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= P) return;
+__global__ __launch_bounds__(ZP_THREADS) void k_zs_setpts(int64_t P, D3 x, int n0, int n1, int n2,
+                                                          int w, double h0, double h1, double h2,
+                                                          int prec64, uint32_t *__restrict__ word,
+                                                          F3 fro) {
+    const int64_t j0 = (int64_t)blockIdx.x * (ZP_THREADS * ZP_ITEMS) + threadIdx.x;
     const double halfw = 0.5 * (double)w;
-    int ix, iy, iz;
-    float fx, fy, fz;
-    cell_t12(x.p[0][j], h0, halfw, prec64, ix, fx);
-    cell_t12(x.p[1][j], h1, halfw, prec64, iy, fy);
-    cell_t12(x.p[2][j], h2, halfw, prec64, iz, fz);
     const int nzc = (n2 + kZsChunk - 1) / kZsChunk;
-    if constexpr (GATHER)
-        word[j] = zg_word(pmod(ix, n0), pmod(iy, n1), pmod(iz, n2), n1, nzc);
-    else
-        word[j] = zs_word(pmod(ix, n0), pmod(iy, n1), pmod(iz, n2), n1, nzc, w);
-    fro.p[0][j] = fx;
-    fro.p[1][j] = fy;
-    fro.p[2][j] = fz;
+    double xv[ZP_ITEMS][3];
+#pragma unroll
+    for (int i = 0; i < ZP_ITEMS; ++i) {
+        const int64_t j = j0 + (int64_t)i * ZP_THREADS;
+#pragma unroll
+        for (int d = 0; d < 3; ++d) xv[i][d] = j < P ? x.p[d][j] : 0.0;
+    }
+#pragma unroll
+    for (int i = 0; i < ZP_ITEMS; ++i) {
+        const int64_t j = j0 + (int64_t)i * ZP_THREADS;
+        if (j >= P) break;
+        int ix, iy, iz;
+        float fx, fy, fz;
+        cell_t12(xv[i][0], h0, halfw, prec64, ix, fx);
+        cell_t12(xv[i][1], h1, halfw, prec64, iy, fy);
+        cell_t12(xv[i][2], h2, halfw, prec64, iz, fz);
+        if constexpr (GATHER)
+            word[j] = zg_word(pmod(ix, n0), pmod(iy, n1), pmod(iz, n2), n1, nzc);
+        else
+            word[j] = zs_word(pmod(ix, n0), pmod(iy, n1), pmod(iz, n2), n1, nzc, w);
+        fro.p[0][j] = fx;
+        fro.p[1][j] = fy;
+        fro.p[2][j] = fz;
+    }
 }
 
 // 2D type-1 setup for the y-sweep spread: the same cells and fractions, and
@@ -297,7 +315,7 @@ static int zs_setpts(bool gather, const mn_bins *g, int64_t P, const double *con
         h[d] = kTwoPi / (double)g->n[d];
     }
     auto kern = gather ? k_zs_setpts<true> : k_zs_setpts<false>;
-    kern<<<blocks_for(P, 256), 256, 0, as_stream(stream)>>>(
+    kern<<<blocks_for(P, ZP_THREADS * ZP_ITEMS), ZP_THREADS, 0, as_stream(stream)>>>(
         P, xs, (int)g->n[0], (int)g->n[1], (int)g->n[2], g->w, h[0], h[1], h[2], prec64, word, fo);
     MN_LAUNCH_CHECK("zsweep_setpts");
     return MN_OK;
