@@ -23,8 +23,10 @@
 // chunk, so the sweep needs no cell indices.
 //
 // Per batch (up to 64 points of one chunk, a lane per point):
-//  * prologue: the lane evaluates the W ES weights of each axis once (3W
-//    evaluations) and writes them at their cells: x- and y-weights into the
+//  * the lane's W ES weights of each axis (3W evaluations) are computed in
+//    the block of the previous batch's first K-step, where their VALU work
+//    overlaps its MFMAs (measured 1.5-3 % faster than in the prologue);
+//  * prologue: the lane writes the weights at their cells: x- and y-weights into the
 //    point's row of the weight table (the block's 8 columns in order, zero
 //    elsewhere; taps off the block land in unread padding), and B = c w_z,
 //    already split into fp16 hi + lo, into four slot-major tables (re hi,
@@ -362,56 +364,77 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
         }
     };
 
-    // K-steps of 32 points over the 8-point groups [g0, g1) of the tables;
-    // lanes past g1 read the zero group
-    auto ksteps = [&](int g0, int g1) __attribute__((always_inline)) {
-        for (int gs = g0; gs < g1; gs += 4) {
-            const int pos = 8 * (gs + lk < g1 ? gs + lk : kZeroGroup);
-            float wx0[8], wx1[8], wy0[8], wy1[8];
+    // the K-step of 32 points over the 8-point groups [gs, min(gs + 4, g1))
+    // of the tables; lanes past g1 read the zero group
+    auto kstep = [&](int gs, int g1) __attribute__((always_inline)) {
+        const int pos = 8 * (gs + lk < g1 ? gs + lk : kZeroGroup);
+        float wx0[8], wx1[8], wy0[8], wy1[8];
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                const float *rr = rows + (pos + t) * ROW;
-                const float2 px = *reinterpret_cast<const float2 *>(rr + XO + 2 * (li >> 2));
-                const float2 py = *reinterpret_cast<const float2 *>(rr + YO + 2 * (li & 3));
-                wx0[t] = px.x;
-                wx1[t] = px.y;
-                wy0[t] = py.x;
-                wy1[t] = py.y;
+        for (int t = 0; t < 8; ++t) {
+            const float *rr = rows + (pos + t) * ROW;
+            const float2 px = *reinterpret_cast<const float2 *>(rr + XO + 2 * (li >> 2));
+            const float2 py = *reinterpret_cast<const float2 *>(rr + YO + 2 * (li & 3));
+            wx0[t] = px.x;
+            wx1[t] = px.y;
+            wy0[t] = py.x;
+            wy1[t] = py.y;
+        }
+        mh8 ah[4], al[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            split_prod8((q >> 1) ? wx1 : wx0, (q & 1) ? wy1 : wy0, ah[q], al[q]);
+        const int bo = li * BST + pos;
+#pragma unroll
+        for (int v = 0; v < VB; ++v) {
+            const mh8 brh = *reinterpret_cast<const mh8 *>(&btab[v][bo]);
+            const mh8 brl = *reinterpret_cast<const mh8 *>(&btab[v][kTab + bo]);
+            const mh8 bih = *reinterpret_cast<const mh8 *>(&btab[v][2 * kTab + bo]);
+            const mh8 bil = *reinterpret_cast<const mh8 *>(&btab[v][3 * kTab + bo]);
+            // consecutive MFMAs go to different accumulators: each of
+            // the 8 tiles of a vector is used again only 8 instructions
+            // later
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                are[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], brh, are[v][q], 0, 0, 0);
+                aim[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], bih, aim[v][q], 0, 0, 0);
             }
-            mh8 ah[4], al[4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                split_prod8((q >> 1) ? wx1 : wx0, (q & 1) ? wy1 : wy0, ah[q], al[q]);
-            const int bo = li * BST + pos;
+            for (int q = 0; q < 4; ++q) {
+                are[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], brl, are[v][q], 0, 0, 0);
+                aim[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], bil, aim[v][q], 0, 0, 0);
+            }
 #pragma unroll
-            for (int v = 0; v < VB; ++v) {
-                const mh8 brh = *reinterpret_cast<const mh8 *>(&btab[v][bo]);
-                const mh8 brl = *reinterpret_cast<const mh8 *>(&btab[v][kTab + bo]);
-                const mh8 bih = *reinterpret_cast<const mh8 *>(&btab[v][2 * kTab + bo]);
-                const mh8 bil = *reinterpret_cast<const mh8 *>(&btab[v][3 * kTab + bo]);
-                // consecutive MFMAs go to different accumulators: each of
-                // the 8 tiles of a vector is used again only 8 instructions
-                // later
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    are[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], brh, are[v][q], 0, 0, 0);
-                    aim[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], bih, aim[v][q], 0, 0, 0);
-                }
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    are[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], brl, are[v][q], 0, 0, 0);
-                    aim[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], bil, aim[v][q], 0, 0, 0);
-                }
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    are[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[q], brh, are[v][q], 0, 0, 0);
-                    aim[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[q], bih, aim[v][q], 0, 0, 0);
-                }
+            for (int q = 0; q < 4; ++q) {
+                are[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[q], brh, are[v][q], 0, 0, 0);
+                aim[v][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[q], bih, aim[v][q], 0, 0, 0);
             }
         }
     };
+    // K-steps of 32 points over the 8-point groups [g0, g1) (g0 < g1); extra()
+    // runs in the block of the first one, whose MFMAs it can overlap
+    auto ksteps = [&](int g0, int g1, auto extra) __attribute__((always_inline)) {
+        kstep(g0, g1);
+        extra();
+        for (int gs = g0 + 4; gs < g1; gs += 4) kstep(gs, g1);
+    };
 
-    auto process = [&](const ZPoint &p, const float2 (&cp)[VB]) __attribute__((always_inline)) {
+    // the 3W ES weights of a point (x and y scaled by kAxisScale); the scaled
+    // distance (a - f) 2/w of tap a is one fma
+    auto es_eval = [&](const ZPoint &p, float (&ew)[3][W]) __attribute__((always_inline)) {
+        constexpr float ih = 2.0f / W;
+#pragma unroll
+        for (int a = 0; a < W; ++a) {
+            const float ca = (float)a * ih;
+            ew[0][a] = zs_es(__builtin_fmaf(-p.fx, ih, ca), bl2e) * kAxisScale;
+            ew[1][a] = zs_es(__builtin_fmaf(-p.fy, ih, ca), bl2e) * kAxisScale;
+            ew[2][a] = zs_es(__builtin_fmaf(-p.fz, ih, ca), bl2e);
+        }
+    };
+
+    // batch p with its strengths cp and weights ew; computes ewn for the next
+    // batch pn
+    auto process = [&](const ZPoint &p, const float2 (&cp)[VB], const float (&ew)[3][W],
+                       const ZPoint &pn, float (&ewn)[3][W]) __attribute__((always_inline)) {
         int wcA, offA, wcB, offB;
         chunk_pos(p.cA, wrap_off, wcA, offA);
         chunk_pos(p.cB, wrap_off, wcB, offB);
@@ -474,14 +497,11 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
             float *rx = rows + lane * ROW + XO + ox;
             float *ry = rows + lane * ROW + YO + oy;
             _Float16 *bt = &btab[0][0] + sz * BST + lane;
-            constexpr float ih = 2.0f / W;
 #pragma unroll
             for (int a = 0; a < W; ++a) {
-                // scaled distance (a - f) 2/w of tap a, one fma
-                const float ca = (float)a * ih;
-                rx[a] = zs_es(__builtin_fmaf(-p.fx, ih, ca), bl2e) * kAxisScale;
-                ry[a] = zs_es(__builtin_fmaf(-p.fy, ih, ca), bl2e) * kAxisScale;
-                const float wz = zs_es(__builtin_fmaf(-p.fz, ih, ca), bl2e);
+                rx[a] = ew[0][a];
+                ry[a] = ew[1][a];
+                const float wz = ew[2][a];
 #pragma unroll
                 for (int v = 0; v < VB; ++v) {
                     _Float16 *o = bt + v * 4 * kTab + a * BST;
@@ -495,10 +515,10 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
         }
         __syncthreads();
         // part A in its chunk's window, then part B in the next chunk's
-        ksteps(0, (p.nA + 7) >> 3);
+        ksteps(0, (p.nA + 7) >> 3, [&]() __attribute__((always_inline)) { es_eval(pn, ewn); });
         if (p.nB > 0) {
             window_to(p.cB);
-            ksteps(p.oB >> 3, (p.oB + p.nB + 7) >> 3);
+            ksteps(p.oB >> 3, (p.oB + p.nB + 7) >> 3, []() {});
         }
     };
 
@@ -517,22 +537,24 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
     cur_load(cur, rg, (z0 == 0 && wrap_off > 0) ? -2 : z0 / ZC - 1, lane);
     ZPoint pa = zp_next<PRE>(cur, rg, lane, perm, word, frs, pre);
     float2 ca[VB], cb[VB], cc[VB];
+    float ewa[3][W], ewb[3][W], ewc[3][W];
     strengths(pa, ca);  // idle lanes read c[perm[0]]: their rows stay zero
+    es_eval(pa, ewa);
     ZPoint pb = zp_next<PRE>(cur, rg, lane, perm, word, frs, pre);
     ZPoint pc;
     for (;;) {
         if (pa.nA == 0) break;
         pc = zp_next<PRE>(cur, rg, lane, perm, word, frs, pre);
         strengths(pb, cb);
-        process(pa, ca);
+        process(pa, ca, ewa, pb, ewb);
         if (pb.nA == 0) break;
         pa = zp_next<PRE>(cur, rg, lane, perm, word, frs, pre);
         strengths(pc, cc);
-        process(pb, cb);
+        process(pb, cb, ewb, pc, ewc);
         if (pc.nA == 0) break;
         pb = zp_next<PRE>(cur, rg, lane, perm, word, frs, pre);
         strengths(pa, ca);
-        process(pc, cc);
+        process(pc, cc, ewc, pa, ewa);
     }
 #pragma unroll
     for (int v = 0; v < VB; ++v)
