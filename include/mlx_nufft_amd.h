@@ -324,6 +324,40 @@ int mn_spread_ysweep(const mn_bins *g, float beta, int64_t P, int64_t B, int yse
                      const float *const frs[2], const void *c, void *grid, mn_stream_t stream);
 
 /*
+ * 2D owner-computes spread on the matrix cores ("y-window MFMA sweep"):
+ * grids[b] (n0 x n1 complex64, fully overwritten) = spread of strength
+ * vector b for B vectors (c: B rows of P). For 2D geometries with
+ * 2 <= w <= 8, n0 a multiple of 16 (>= 32) and n1 a multiple of 8 (>= 16).
+ * One wavefront owns 16 consecutive x-columns over a y-segment of yseg
+ * cells (a multiple of 8) and keeps each vector's 16 x 16-slot y-window in
+ * matrix-core accumulators: A = the x-weights, B = the strength times the
+ * y-weights, both split into fp16 hi + lo (three products, f32
+ * accumulation).
+ * Point word (one uint32 per point, from mn_ymfma_setpts):
+ *   bits 0-24  key = ((x/16)*(n1/8) + y/8)*2 + reach   (sorted on)
+ *   bits 25-28 x mod 16 of the first tap; bits 29-31 y mod 8
+ * (reach = the footprint crosses into the next 16-column block).
+ * mn_ymfma_setpts computes the words and fr exactly as mn_setpts_t12 does
+ * i1 and fr; sort the words with mn_sort_pairs (key_bits = bit length of
+ * mn_ymfma_nkeys() - 1, fr as payload) and build ystart
+ * (mn_ymfma_nkeys() + 1 int32) with mn_ymfma_starts. Strengths are
+ * c[perm[j]], or c[j] when perm is NULL; c holds B rows of P values, or P
+ * rows of B values when point_major is nonzero (then a point's strengths
+ * are one contiguous run, the faster layout for B > 1).
+ * ref: nd.py:152-165 (cells), nd.py:492-579 and nd.py:683-742 (output-driven
+ * and batched spread), nd.py:298-372 (bin sort).
+ */
+int64_t mn_ymfma_nkeys(const mn_bins *g);
+int mn_ymfma_setpts(const mn_bins *g, int64_t P, const double *const x[2], int prec64,
+                    uint32_t *word, float *const fr[2], mn_stream_t stream);
+int mn_ymfma_starts(const mn_bins *g, int64_t P, const uint32_t *sorted_word, int32_t *ystart,
+                    mn_stream_t stream);
+int mn_spread_ymfma(const mn_bins *g, float beta, int64_t P, int64_t B, int yseg,
+                    const int32_t *ystart, const uint32_t *perm, const uint32_t *sorted_word,
+                    const float *const frs[2], const void *c, int point_major, void *grid,
+                    mn_stream_t stream);
+
+/*
  * out[j] = in[perm[j]] for P complex64 values (a strength vector into
  * sorted order). ref: nd.py:603 (mx.take of c by perm, GM spread).
  */

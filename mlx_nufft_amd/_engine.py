@@ -286,21 +286,37 @@ def ysweep_eligible(dim, w, n_up):
             and n_up[1] >= w and (n_up[0] // 64) * n_up[1] * 2 <= 1 << 26)
 
 
+def ymfma_eligible(dim, w, n_up):
+    """True when the 2D spread on the matrix cores (y-window MFMA sweep)
+    applies: 2D, w <= 8, n0 a multiple of 16 (>= 32), n1 a multiple of 8
+    (>= 16) and at most 2^25 sort keys ((n0/16)*(n1/8)*2). MN_SPREAD=tiles
+    forces the LDS-tile spread, MN_SPREAD=ysweep the VALU y-sweep."""
+    if os.environ.get("MN_SPREAD", "") in ("tiles", "ysweep"):
+        return False
+    return (dim == 2 and 2 <= w <= 8 and n_up[0] % 16 == 0 and n_up[0] >= 32
+            and n_up[1] % 8 == 0 and 16 <= n_up[1] < 1 << 24
+            and (n_up[0] // 16) * (n_up[1] // 8) * 2 <= 1 << 25)
+
+
 class YSweepPoints:
-    """Point state for the 2D y-sweep spread: packed point words and
-    fractions, stably sorted together by the y-sweep key, and the key start
-    table. Buffers of the previous point set of the same plan (prev, same P
-    and geometry) are reused, as in ZSweepPoints."""
+    """Point state for the 2D y-sweep spread (mfma=False, kind "ysweep") or
+    the y-window MFMA sweep (mfma=True, kind "ymfma"): packed point words and
+    fractions, stably sorted together by the sweep's key, and the key start
+    table. Buffers of the previous point set of the same plan (prev, same
+    kind, P and geometry) are reused, as in ZSweepPoints."""
 
-    kind = "ysweep"
-
-    def __init__(self, bins, x64, prec64, prev=None):
+    def __init__(self, bins, x64, prec64, prev=None, mfma=False):
         lib = L.lib()
         dev = x64[0].device
+        self.kind = "ymfma" if mfma else "ysweep"
+        nkeys, setpts, starts = ((lib.mn_ymfma_nkeys, lib.mn_ymfma_setpts, lib.mn_ymfma_starts)
+                                 if mfma else
+                                 (lib.mn_ysweep_nkeys, lib.mn_ysweep_setpts, lib.mn_ysweep_starts))
         self.bins = bins
         self.P = P = x64[0].numel()
-        self.K = K = int(lib.mn_ysweep_nkeys(ctypes.byref(bins)))
-        same = (prev is not None and prev.P == P and prev.K == K and prev.dev == dev)
+        self.K = K = int(nkeys(ctypes.byref(bins)))
+        same = (prev is not None and prev.kind == self.kind and prev.P == P and prev.K == K
+                and prev.dev == dev)
         self.dev = dev
         self._bufs = bufs = prev._bufs if same else {}
 
@@ -312,10 +328,9 @@ class YSweepPoints:
         V2 = ctypes.c_void_p * 2
         word = buf("word_in", P, torch.int32)
         fr = buf("fr_in", (2, P), torch.float32)
-        L.check(lib.mn_ysweep_setpts(ctypes.byref(bins), P, V2(x64[0].data_ptr(), x64[1].data_ptr()),
-                                     int(bool(prec64)), L.ptr(word),
-                                     V2(fr[0].data_ptr(), fr[1].data_ptr()), L.stream()),
-                "ysweep setpts")
+        L.check(setpts(ctypes.byref(bins), P, V2(x64[0].data_ptr(), x64[1].data_ptr()),
+                       int(bool(prec64)), L.ptr(word), V2(fr[0].data_ptr(), fr[1].data_ptr()),
+                       L.stream()), f"{self.kind} setpts")
         self.frs = buf("frs", (2, P), torch.float32)
         ws_bytes = int(lib.mn_sort_pairs_workspace_bytes(P, 2))
         self.word, self.perm, _ = sort_pairs(
@@ -323,8 +338,8 @@ class YSweepPoints:
             skey=buf("word", P, torch.int32), perm=buf("perm", P, torch.int32),
             ws=buf("ws", ws_bytes, torch.uint8))
         self.ystart = buf("ystart", K + 1, torch.int32)
-        L.check(lib.mn_ysweep_starts(ctypes.byref(bins), P, L.ptr(self.word), L.ptr(self.ystart),
-                                     L.stream()), "ysweep starts")
+        L.check(starts(ctypes.byref(bins), P, L.ptr(self.word), L.ptr(self.ystart), L.stream()),
+                f"{self.kind} starts")
 
     def fr_rows(self):
         return _rows(self.frs, 2)
@@ -368,7 +383,7 @@ class GroupSplit:
         gs = glabel[pts.perm.long()]
         gkey = torch.where((gs < 0) | (gs >= G), G, gs).to(torch.int32)
         del gs
-        if pts.kind in ("zsweep", "ysweep"):
+        if pts.kind in ("zsweep", "ysweep", "ymfma"):
             cols = [pts.word, pts.perm] + _rows(pts.frs, dim)
         elif pts.kind == "tiles":
             cols = [pts.skey, pts.perm] + _rows(pts.frs, dim) + _rows(pts.i1s, dim)
@@ -398,7 +413,8 @@ class GroupSplit:
                                              device=pts.perm.device)
             sub = _Subset(pts.kind, pts.bins, e - s, perm=c[1][s:e], word=c[0][s:e], frs=frs,
                           K=pts.K)
-            starts_fn = lib.mn_zsweep_starts if pts.kind == "zsweep" else lib.mn_ysweep_starts
+            starts_fn = {"zsweep": lib.mn_zsweep_starts, "ysweep": lib.mn_ysweep_starts,
+                         "ymfma": lib.mn_ymfma_starts}[pts.kind]
             L.check(starts_fn(ctypes.byref(pts.bins), sub.P, L.ptr(sub.word),
                               L.ptr(self._startbuf), L.stream()), f"{pts.kind} starts")
             if pts.kind == "zsweep":
@@ -439,6 +455,38 @@ def spread_ysweep(pts, beta, cs, grids):
                                      ysweep_segment(n_up, B), L.ptr(pts.ystart), L.ptr(pts.perm),
                                      L.ptr(pts.word), V2(pts.frs[0].data_ptr(), pts.frs[1].data_ptr()),
                                      L.ptr(cs), L.ptr(grids), L.stream()), "spread_ysweep")
+
+
+def ymfma_segment(n_up, B):
+    """y-segment per wavefront of the y-window MFMA sweep: the longest power
+    of two (<= 256, >= 32) that still gives at least 4096 wavefronts (each
+    segment also sweeps the chunk below it)."""
+    vb = ysweep_vectors_per_wave(B)
+    groups = -(-B // vb)
+    nbx = n_up[0] // 16
+    yseg = 256
+    while yseg > 32 and nbx * (-(-n_up[1] // yseg)) * groups < 4096:
+        yseg //= 2
+    return yseg
+
+
+def spread_ymfma(pts, beta, cs, grids):
+    """grids[b] = spread(cs[b]) for B vectors (cs: (B, P) or (P,), caller
+    order) with the y-window MFMA sweep; grids are fully overwritten. Several
+    vectors are first transposed to point-major (P, B), so that a point
+    visit gathers its strengths in one run rather than one sector per
+    vector."""
+    B = 1 if cs.dim() == 1 else int(cs.shape[0])
+    n_up = [int(pts.bins.n[0]), int(pts.bins.n[1])]
+    V2 = ctypes.c_void_p * 2
+    pm = 0
+    if B > 1:
+        cs = cs.t().contiguous()
+        pm = 1
+    L.check(L.lib().mn_spread_ymfma(ctypes.byref(pts.bins), float(beta), pts.P, B,
+                                    ymfma_segment(n_up, B), L.ptr(pts.ystart), L.ptr(pts.perm),
+                                    L.ptr(pts.word), V2(pts.frs[0].data_ptr(), pts.frs[1].data_ptr()),
+                                    L.ptr(cs), pm, L.ptr(grids), L.stream()), "spread_ymfma")
 
 
 def permute_c64(perm, c, out):

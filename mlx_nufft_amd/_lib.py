@@ -90,6 +90,12 @@ _SIGS = [
     ("mn_ysweep_starts", c_int, [ctypes.POINTER(Bins), c_int64, c_vp, c_vp, c_vp]),
     ("mn_spread_ysweep", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int64, c_int, c_vp,
                                  c_vp, c_vp, ctypes.c_void_p * 2, c_vp, c_vp, c_vp]),
+    ("mn_ymfma_nkeys", c_int64, [ctypes.POINTER(Bins)]),
+    ("mn_ymfma_setpts", c_int, [ctypes.POINTER(Bins), c_int64, ctypes.c_void_p * 2, c_int, c_vp,
+                                ctypes.c_void_p * 2, c_vp]),
+    ("mn_ymfma_starts", c_int, [ctypes.POINTER(Bins), c_int64, c_vp, c_vp, c_vp]),
+    ("mn_spread_ymfma", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int64, c_int, c_vp,
+                                c_vp, c_vp, ctypes.c_void_p * 2, c_vp, c_int, c_vp, c_vp]),
     ("mn_spread_batch", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int64, c_vp, c_vp, VP3,
                                 VP3, c_int64, c_vp, c_vp, c_vp]),
     ("mn_interp", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int64, c_vp, c_vp, VP3, VP3,

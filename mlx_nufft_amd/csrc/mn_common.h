@@ -256,6 +256,35 @@ __device__ __forceinline__ uint32_t ys_word(int x, int y, int n1, int w) {
 int ysweep_check(const mn_bins *g);
 int64_t ysweep_nkeys(const mn_bins *g);
 
+// ---- y-window MFMA sweep point word (2D) ------------------------------------
+// The 2D spread on the matrix cores (mn_ymfma.hip) sorts one 32-bit word per
+// point:
+//   bits  0-24  key = (bx*nyc + yc)*2 + reach (sorted on)
+//   bits 25-28  x cell of the first tap within its 16-column block
+//   bits 29-31  y cell of the first tap within its 8-cell y-chunk
+// where bx is the 16-column block of the first tap x, yc = y / 8 its y-chunk
+// (nyc = n1 / 8 chunks) and reach says whether the footprint crosses into
+// the next block. Inside a (block, chunk) the order of the points does not
+// matter to the spread (its y-window spans the whole chunk).
+constexpr int kYmBlock = 16;
+constexpr int kYmChunk = 8;
+constexpr int kYmKeyBits = 25;
+constexpr uint32_t kYmKeyMask = (1u << kYmKeyBits) - 1u;
+
+__device__ __forceinline__ uint32_t ym_word(int x, int y, int nyc, int w) {
+    const int lx = x & (kYmBlock - 1), ly = y & (kYmChunk - 1);
+    const uint32_t reach = (lx + w - 1 >= kYmBlock) ? 1u : 0u;
+    const uint32_t key =
+        ((uint32_t)(x / kYmBlock) * (uint32_t)nyc + (uint32_t)(y / kYmChunk)) * 2u + reach;
+    return key | ((uint32_t)lx << kYmKeyBits) | ((uint32_t)ly << 29);
+}
+
+// Validate a y-window MFMA sweep geometry (2D, 2 <= w <= 8, n0 a multiple
+// of 16 and >= 32, n1 a multiple of 8 and >= 16, key space within
+// kYmKeyBits); number of keys K = (n0/16)*(n1/8)*2.
+int ymfma_check(const mn_bins *g);
+int64_t ymfma_nkeys(const mn_bins *g);
+
 // Validate the point/subproblem arguments shared by spread and interp.
 int check_points(const mn_bins *g, int64_t P, int64_t nsub, const int32_t *info,
                  const uint32_t *perm, const int32_t *const i1s[3], const float *const frs[3],

@@ -134,6 +134,22 @@ __global__ void k_ys_setpts(int64_t P, D3 x, int n0, int n1, int w, double h0, d
     fro.p[1][j] = fy;
 }
 
+// 2D setup for the y-window MFMA sweep: the same cells and fractions, and
+// the packed point word (ym_word).
+__global__ void k_ym_setpts(int64_t P, D3 x, int n0, int n1, int w, double h0, double h1,
+                            int prec64, uint32_t *__restrict__ word, F3 fro) {
+    int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= P) return;
+    const double halfw = 0.5 * (double)w;
+    int ix, iy;
+    float fx, fy;
+    cell_t12(x.p[0][j], h0, halfw, prec64, ix, fx);
+    cell_t12(x.p[1][j], h1, halfw, prec64, iy, fy);
+    word[j] = ym_word(pmod(ix, n0), pmod(iy, n1), n1 / kYmChunk, w);
+    fro.p[0][j] = fx;
+    fro.p[1][j] = fy;
+}
+
 struct T3Src {
     double C[3], gam[3], hd[3], D[3], nf2[3];
 };
@@ -349,6 +365,27 @@ int mn_ysweep_setpts(const mn_bins *g, int64_t P, const double *const x[2], int 
         P, xs, (int)g->n[0], (int)g->n[1], g->w, kTwoPi / (double)g->n[0],
         kTwoPi / (double)g->n[1], prec64, word, fo);
     MN_LAUNCH_CHECK("ysweep_setpts");
+    return MN_OK;
+}
+
+int mn_ymfma_setpts(const mn_bins *g, int64_t P, const double *const x[2], int prec64,
+                    uint32_t *word, float *const fr[2], mn_stream_t stream) {
+    clear_error();
+    int rc = ymfma_check(g);
+    if (rc) return rc;
+    MN_REQUIRE(P >= 1 && P < (int64_t(1) << 31), "ymfma setpts: P must be in [1, 2^31)");
+    MN_REQUIRE(x && fr && word, "ymfma setpts: NULL pointer");
+    D3 xs{};
+    F3 fo{};
+    for (int d = 0; d < 2; ++d) {
+        MN_REQUIRE(x[d] && fr[d], "ymfma setpts: NULL coordinate/output pointer");
+        xs.p[d] = x[d];
+        fo.p[d] = fr[d];
+    }
+    k_ym_setpts<<<blocks_for(P, 256), 256, 0, as_stream(stream)>>>(
+        P, xs, (int)g->n[0], (int)g->n[1], g->w, kTwoPi / (double)g->n[0],
+        kTwoPi / (double)g->n[1], prec64, word, fo);
+    MN_LAUNCH_CHECK("ymfma_setpts");
     return MN_OK;
 }
 

@@ -109,9 +109,13 @@ class _PointsND:
         self._zsweep = E.zsweep_eligible(self.dim, self.w, self.n_up) and self._zsweep_wanted()
         if self._zsweep:
             self._zbins = E.make_bins(3, self.w, self.n_up, m=(8, 8, 1))
-        self._ysweep = self._use_zsweep and E.ysweep_eligible(self.dim, self.w, self.n_up)
+        # 2D: the y-window MFMA sweep where its geometry applies, else the
+        # VALU y-sweep
+        self._ymfma = self._use_zsweep and E.ymfma_eligible(self.dim, self.w, self.n_up)
+        self._ysweep = self._use_zsweep and (self._ymfma or
+                                             E.ysweep_eligible(self.dim, self.w, self.n_up))
         if self._ysweep:
-            self._ybins = E.make_bins(2, self.w, self.n_up, m=(64, 1))
+            self._ybins = E.make_bins(2, self.w, self.n_up, m=(16 if self._ymfma else 64, 1))
         self._set_points(x64)
 
         # Mode deconvolution 1/phihat(2 pi k / n_up) on the uncentred fine grid
@@ -174,7 +178,8 @@ class _PointsND:
             with tm("setpts+sort+tables"):
                 prev = getattr(self, "pts", None)
                 self.pts = E.YSweepPoints(self._ybins, x64, self.prec == "crit64",
-                                          prev=prev if isinstance(prev, E.YSweepPoints) else None)
+                                          prev=prev if isinstance(prev, E.YSweepPoints) else None,
+                                          mfma=self._ymfma)
                 del prev
         else:
             with tm("setpts"):
@@ -288,6 +293,9 @@ class Type1PlanND(_PointsND):
         elif pts.kind == "ysweep":
             with tm("spread"):
                 E.spread_ysweep(pts, self.beta, cd, grid)
+        elif pts.kind == "ymfma":
+            with tm("spread"):
+                E.spread_ymfma(pts, self.beta, cd, grid)
         else:
             with tm("zero"):
                 E.fill_zero(grid)
@@ -326,6 +334,8 @@ class Type1PlanND(_PointsND):
                 E.spread_zsweep_batch(self.pts, self.beta, cd, grids)
             elif self.pts.kind == "ysweep":
                 E.spread_ysweep(self.pts, self.beta, cd, grids)
+            elif self.pts.kind == "ymfma":
+                E.spread_ymfma(self.pts, self.beta, cd, grids)
             else:
                 E.spread_batch(self.pts, self.beta, cd, grids)
         self._fft_crop(grids, fk, tm, B)

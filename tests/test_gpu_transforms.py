@@ -367,8 +367,8 @@ def test_execute_disjoint(dim, N, method, oracle, mn):
     """ref: nd.py:796-855. G transforms of disjoint point subsets of one plan
     equal fresh plans of each subset (an empty group gives zeros, label -1
     belongs to no group) and the direct sum, after a re-point that changes
-    P; each point state kind (1D tiles, 2D y-sweep, 3D z-sweep, and the
-    tiles forced by "gm") is split by label."""
+    P; each point state kind (1D tiles, 2D y-window MFMA sweep, 3D z-sweep,
+    and the tiles forced by "gm") is split by label."""
     print(f"case execute_disjoint dim={dim} method={method}", flush=True)
     rng = np.random.default_rng(47 + dim)
     eps = 1e-5
@@ -376,7 +376,7 @@ def test_execute_disjoint(dim, N, method, oracle, mn):
     M = 12_000
     x = _pts(rng, dim, M)
     p.set_sources(tuple(x))
-    kind = {1: "tiles", 2: "ysweep", 3: "zsweep"}[dim] if method == "auto" else "tiles"
+    kind = {1: "tiles", 2: "ymfma", 3: "zsweep"}[dim] if method == "auto" else "tiles"
     assert p.pts.kind == kind
     c = _cplx(rng, M)
     groups = rng.choice([0, 1, 3, -1], M)      # group 2 stays empty
