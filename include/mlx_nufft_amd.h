@@ -254,9 +254,9 @@ int mn_spread_zsweep(const mn_bins *g, float beta, int64_t P, int zseg, const in
 /*
  * B strength vectors over one sorted point set: cs holds B rows of P
  * (caller order, or sorted order when perm is NULL), grids B fine grids of
- * n0*n1*n2 complex64, each fully overwritten. A wave carries two vectors:
- * the ES weights, the cursor walk and the MFMA A operands are formed once
- * for both. Each grid equals mn_spread_zsweep's for its vector bit for bit.
+ * n0*n1*n2 complex64, each fully overwritten. One launch covers all B
+ * vectors, a wave per (block, vector). Each grid equals mn_spread_zsweep's
+ * for its vector bit for bit.
  * ref: nd.py:683-742 (batched output-driven spread), nd.py:744-794.
  */
 int mn_spread_zsweep_batch(const mn_bins *g, float beta, int64_t P, int64_t B, int zseg,

@@ -505,8 +505,8 @@ def spread_zsweep(pts, beta, c, grid, pre=None, zseg=ZSEG, presorted=False):
 
 
 def spread_zsweep_batch(pts, beta, cs, grids, zseg=ZSEG, presorted=False):
-    """grids[b] = spread(cs[b]) for B vectors with the z-sweep, two vectors
-    per wave (overwrites grids)."""
+    """grids[b] = spread(cs[b]) for B vectors with the z-sweep, one launch
+    with a wave per (block, vector) (overwrites grids)."""
     B = cs.shape[0]
     assert grids.shape[0] == B and cs.is_contiguous() and grids.is_contiguous()
     L.check(L.lib().mn_spread_zsweep_batch(ctypes.byref(pts.bins), float(beta), pts.P, B,

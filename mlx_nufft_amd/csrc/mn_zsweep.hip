@@ -609,34 +609,20 @@ struct ZLaunch {
             const int64_t nw = (int64_t)nbx * nby * nseg;
             const float bl2e = (float)(a.beta * 1.4426950408889634);
             const int64_t gs = (int64_t)n0 * n1 * n2;
-            // pairs of vectors share a wave (weights and A operands formed
-            // once); an odd last vector runs alone
-            const int64_t pairs = a.B / 2, rest = a.B % 2;
-            if (pairs) {
-                const dim3 gridp((unsigned)nw, (unsigned)pairs);
-                if (a.pre)
-                    k_spread_zsweep<W, true, 2><<<gridp, 64, 0, a.s>>>(
-                        n0, n1, n2, nbx, nby, nzc, a.zseg, nseg, bl2e, a.zstart, a.perm, a.word,
-                        a.frs, a.c, a.P, a.pre, a.grid, gs);
-                else
-                    k_spread_zsweep<W, false, 2><<<gridp, 64, 0, a.s>>>(
-                        n0, n1, n2, nbx, nby, nzc, a.zseg, nseg, bl2e, a.zstart, a.perm, a.word,
-                        a.frs, a.c, a.P, a.pre, a.grid, gs);
-                MN_LAUNCH_CHECK("spread_zsweep");
-            }
-            if (rest) {
-                const float2 *c1 = a.c + 2 * pairs * a.P;
-                float2 *g1 = a.grid + 2 * pairs * gs;
-                if (a.pre)
-                    k_spread_zsweep<W, true, 1><<<(unsigned)nw, 64, 0, a.s>>>(
-                        n0, n1, n2, nbx, nby, nzc, a.zseg, nseg, bl2e, a.zstart, a.perm, a.word,
-                        a.frs, c1, a.P, a.pre, g1, gs);
-                else
-                    k_spread_zsweep<W, false, 1><<<(unsigned)nw, 64, 0, a.s>>>(
-                        n0, n1, n2, nbx, nby, nzc, a.zseg, nseg, bl2e, a.zstart, a.perm, a.word,
-                        a.frs, c1, a.P, a.pre, g1, gs);
-                MN_LAUNCH_CHECK("spread_zsweep");
-            }
+            // one wave per (block, vector). Waves carrying two vectors (the
+            // weights and A operands formed once) were no faster: the second
+            // vector's B tables take the wave to 29 KB of LDS, 1.25 waves per
+            // SIMD instead of 2 (B = 2: 2.97 against 2.85 ms; B = 8 even).
+            const dim3 gridv((unsigned)nw, (unsigned)a.B);
+            if (a.pre)
+                k_spread_zsweep<W, true, 1><<<gridv, 64, 0, a.s>>>(
+                    n0, n1, n2, nbx, nby, nzc, a.zseg, nseg, bl2e, a.zstart, a.perm, a.word,
+                    a.frs, a.c, a.P, a.pre, a.grid, gs);
+            else
+                k_spread_zsweep<W, false, 1><<<gridv, 64, 0, a.s>>>(
+                    n0, n1, n2, nbx, nby, nzc, a.zseg, nseg, bl2e, a.zstart, a.perm, a.word,
+                    a.frs, a.c, a.P, a.pre, a.grid, gs);
+            MN_LAUNCH_CHECK("spread_zsweep");
             return MN_OK;
         }
     }
