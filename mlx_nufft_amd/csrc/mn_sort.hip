@@ -62,6 +62,33 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t *total)
     return off + inc - v;
 }
 
+// The same for a block of NT threads (NT a multiple of 64).
+template <int NT>
+__device__ __forceinline__ uint32_t block_excl_scan_n(uint32_t v, uint32_t *total) {
+    __shared__ uint32_t wsumn[NT / 64];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    uint32_t inc = wave_incl_scan(v);
+    if (lane == 63) wsumn[wv] = inc;
+    __syncthreads();
+    uint32_t off = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) {
+        uint32_t s = wsumn[w];
+        if (w < wv) off += s;
+        tot += s;
+    }
+    __syncthreads();
+    *total = tot;
+    return off + inc - v;
+}
+
+// The scatter takes a tile with 512 threads, 16 elements each: 104 VGPRs and
+// four waves per SIMD (256 threads with 32 elements each needed 180 VGPRs,
+// two waves per SIMD, and took 0.72 ms for three passes at 2e7 keys and
+// three payload columns against 0.68; 1024 threads with 8 each took 0.79)
+constexpr int ST_THREADS = 512;
+constexpr int ST_ITEMS = RS_TILE / ST_THREADS;
+
 __global__ void k_tile_reduce(const uint32_t *__restrict__ d, int64_t n,
                               uint32_t *__restrict__ partials) {
     int64_t base = (int64_t)blockIdx.x * SC_TILE + (int64_t)threadIdx.x * SC_ITEMS;
@@ -165,12 +192,12 @@ struct SortCols {
 // Stable scatter of one 8192-element tile: the key, its value (the caller
 // index; implicit on the first pass) and up to MN_SORT_MAX_COLS payload
 // columns.
-//  1. Rank: wave w owns the tile's elements [2048w, 2048w + 2048) and visits
-//     them in 32 rounds of 64 consecutive elements; lanes with equal digits
+//  1. Rank: wave w owns the tile's elements [1024w, 1024w + 1024) and visits
+//     them in 16 rounds of 64 consecutive elements; lanes with equal digits
 //     find each other with a ballot match and a wave-private LDS counter per
 //     digit gives the count of the wave's earlier elements with that digit.
 //     No barrier is needed inside a wave (its LDS accesses stay in order).
-//  2. One scan over the 4 x 256 wave counters gives each (wave, digit) its
+//  2. One scan over the 8 x 256 wave counters gives each (wave, digit) its
 //     start in the tile-local sorted order; an element's slot is that start
 //     plus its rank. Index order is kept, so the pass is stable.
 //  3. Every column goes through LDS: written at the slots, read back in slot
@@ -178,13 +205,13 @@ struct SortCols {
 //     store consecutive addresses inside each digit run.
 // Tiles are mapped XCD-contiguously, so the runs that adjacent tiles write
 // for one digit meet in the same L2 and leave as whole lines.
-__global__ __launch_bounds__(RS_THREADS) void k_radix_scatter(
+__global__ __launch_bounds__(ST_THREADS) void k_radix_scatter(
     const uint32_t *__restrict__ kin, const uint32_t *__restrict__ vin, int64_t P, int shift,
     uint32_t kmask, const uint32_t *__restrict__ offs, const uint32_t *__restrict__ totals,
     int64_t nblk, uint32_t *__restrict__ kout, uint32_t *__restrict__ vout, int ncols,
     SortCols cols) {
-    static_assert(RS_THREADS == RS_RADIX && RS_THREADS == SC_THREADS, "a thread per digit");
-    constexpr int NWV = RS_THREADS / 64;
+    static_assert(ST_THREADS >= RS_RADIX, "a thread per digit");
+    constexpr int NWV = ST_THREADS / 64;
     __shared__ uint32_t gbase[RS_RADIX];
     __shared__ uint32_t lstart[RS_RADIX];
     __shared__ uint32_t wcnt[NWV][RS_RADIX];
@@ -193,26 +220,29 @@ __global__ __launch_bounds__(RS_THREADS) void k_radix_scatter(
     const int64_t tile = xcd_remap(blockIdx.x, nblk);
     const int64_t base = tile * RS_TILE;
     const int nvalid = (int)((P - base) < RS_TILE ? (P - base) : RS_TILE);
+    const bool dt = tid < RS_RADIX;  // a thread per digit
     {
         // the digit's base (all smaller digits) plus the tiles before this one
-        const uint32_t toff = offs[(int64_t)tid * nblk + tile];
+        const uint32_t toff = dt ? offs[(int64_t)tid * nblk + tile] : 0u;
         uint32_t all;
-        gbase[tid] = block_excl_scan(totals[tid], &all) + toff;
+        const uint32_t ex = block_excl_scan_n<ST_THREADS>(dt ? totals[tid] : 0u, &all);
+        if (dt) gbase[tid] = ex + toff;
     }
 #pragma unroll
-    for (int w = 0; w < NWV; ++w) wcnt[w][tid] = 0;
+    for (int w = 0; w < NWV; ++w)
+        if (dt) wcnt[w][tid] = 0;
     __syncthreads();
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    uint32_t kv[RS_ITEMS], rk[RS_ITEMS];
+    uint32_t kv[ST_ITEMS], rk[ST_ITEMS];
     const int wbase = wv * (RS_TILE / NWV);
     // all key loads first: one memory latency per tile, not one per round
 #pragma unroll
-    for (int r = 0; r < RS_ITEMS; ++r) {
+    for (int r = 0; r < ST_ITEMS; ++r) {
         const int q = wbase + r * 64 + lane;
         kv[r] = q < nvalid ? kin[base + q] : 0u;
     }
 #pragma unroll
-    for (int r = 0; r < RS_ITEMS; ++r) {
+    for (int r = 0; r < ST_ITEMS; ++r) {
         const int q = wbase + r * 64 + lane;
         const bool valid = q < nvalid;
         const uint32_t k = kv[r];
@@ -235,33 +265,35 @@ __global__ __launch_bounds__(RS_THREADS) void k_radix_scatter(
         uint32_t c[NWV], s = 0;
 #pragma unroll
         for (int w = 0; w < NWV; ++w) {
-            c[w] = wcnt[w][tid];
+            c[w] = dt ? wcnt[w][tid] : 0u;
             s += c[w];
         }
         uint32_t tot;
-        const uint32_t ex = block_excl_scan(s, &tot);
-        lstart[tid] = ex;
-        uint32_t run = ex;
+        const uint32_t ex = block_excl_scan_n<ST_THREADS>(s, &tot);
+        if (dt) {
+            lstart[tid] = ex;
+            uint32_t run = ex;
 #pragma unroll
-        for (int w = 0; w < NWV; ++w) {
-            wcnt[w][tid] = run;
-            run += c[w];
+            for (int w = 0; w < NWV; ++w) {
+                wcnt[w][tid] = run;
+                run += c[w];
+            }
         }
     }
     __syncthreads();
-    int slot[RS_ITEMS];
+    int slot[ST_ITEMS];
 #pragma unroll
-    for (int r = 0; r < RS_ITEMS; ++r)
+    for (int r = 0; r < ST_ITEMS; ++r)
         slot[r] = rk[r] == 0xFFFFFFFFu ? -1 : (int)(wcnt[wv][rk[r] >> 16] + (rk[r] & 0xFFFFu));
     // Keys: stage, then derive each slot's destination from its digit.
 #pragma unroll
-    for (int r = 0; r < RS_ITEMS; ++r)
+    for (int r = 0; r < ST_ITEMS; ++r)
         if (slot[r] >= 0) stage[slot[r]] = kv[r];
     __syncthreads();
-    uint32_t dst[RS_ITEMS];
+    uint32_t dst[ST_ITEMS];
 #pragma unroll
-    for (int r = 0; r < RS_ITEMS; ++r) {
-        const int q = r * RS_THREADS + tid;
+    for (int r = 0; r < ST_ITEMS; ++r) {
+        const int q = r * ST_THREADS + tid;
         dst[r] = 0;
         if (q < nvalid) {
             const uint32_t k = stage[q];
@@ -273,29 +305,29 @@ __global__ __launch_bounds__(RS_THREADS) void k_radix_scatter(
     __syncthreads();
     // Values and payload columns, one LDS round trip each; the next
     // column's loads are issued before the current one is written out.
-    uint32_t cur[RS_ITEMS];
+    uint32_t cur[ST_ITEMS];
 #pragma unroll
-    for (int r = 0; r < RS_ITEMS; ++r) {
+    for (int r = 0; r < ST_ITEMS; ++r) {
         const int64_t idx = base + wbase + r * 64 + lane;
         cur[r] = slot[r] >= 0 ? (vin ? vin[idx] : (uint32_t)idx) : 0u;
     }
     for (int c = -1; c < ncols; ++c) {
         uint32_t *out = c < 0 ? vout : cols.out[c];
 #pragma unroll
-        for (int r = 0; r < RS_ITEMS; ++r)
+        for (int r = 0; r < ST_ITEMS; ++r)
             if (slot[r] >= 0) stage[slot[r]] = cur[r];
         __syncthreads();
         if (c + 1 < ncols) {
             const uint32_t *src = cols.in[c + 1];
 #pragma unroll
-            for (int r = 0; r < RS_ITEMS; ++r) {
+            for (int r = 0; r < ST_ITEMS; ++r) {
                 const int64_t idx = base + wbase + r * 64 + lane;
                 cur[r] = slot[r] >= 0 ? src[idx] : 0u;
             }
         }
 #pragma unroll
-        for (int r = 0; r < RS_ITEMS; ++r) {
-            const int q = r * RS_THREADS + tid;
+        for (int r = 0; r < ST_ITEMS; ++r) {
+            const int q = r * ST_THREADS + tid;
             if (q < nvalid) out[dst[r]] = stage[q];
         }
         __syncthreads();
@@ -531,7 +563,7 @@ int mn_sort_pairs(int64_t P, int key_bits, const uint32_t *key_in, uint32_t *key
         MN_LAUNCH_CHECK("radix hist");
         k_digit_scan<<<RS_RADIX, SC_THREADS, 0, s>>>(w.hist, nblk, w.totals);
         MN_LAUNCH_CHECK("radix digit scan");
-        k_radix_scatter<<<(unsigned)nblk, RS_THREADS, 0, s>>>(ksrc, vsrc, P, shift, kmask, w.hist,
+        k_radix_scatter<<<(unsigned)nblk, ST_THREADS, 0, s>>>(ksrc, vsrc, P, shift, kmask, w.hist,
                                                              w.totals, nblk, kdst, vdst, ncols,
                                                              cur);
         MN_LAUNCH_CHECK("radix scatter");
