@@ -168,7 +168,10 @@ __global__ __launch_bounds__(RS_THREADS) void k_radix_hist(const uint32_t *__res
     __shared__ uint32_t h[RS_RADIX];
     h[threadIdx.x] = 0;
     __syncthreads();
-    int64_t base = (int64_t)blockIdx.x * RS_TILE;
+    // tiles XCD-contiguous, as in the scatter: a digit row's entries of
+    // neighbouring tiles then leave one L2 as whole lines
+    const int64_t tile = xcd_remap(blockIdx.x, nblk);
+    int64_t base = tile * RS_TILE;
     uint32_t kv[RS_ITEMS];
 #pragma unroll
     for (int i = 0; i < RS_ITEMS; ++i) {
@@ -181,7 +184,7 @@ __global__ __launch_bounds__(RS_THREADS) void k_radix_hist(const uint32_t *__res
         if (idx < P) atomicAdd(&h[digit_of(kv[i], kmask, shift)], 1u);
     }
     __syncthreads();
-    hist[(int64_t)threadIdx.x * nblk + blockIdx.x] = h[threadIdx.x];
+    hist[(int64_t)threadIdx.x * nblk + tile] = h[threadIdx.x];
 }
 
 struct SortCols {
