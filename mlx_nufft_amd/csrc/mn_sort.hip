@@ -42,17 +42,19 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
     return v;
 }
 
-// Exclusive scan of the thread totals of one 256-thread block; returns the
-// exclusive prefix of this thread and writes the block total to *total.
-__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t *total) {
-    __shared__ uint32_t wsum[SC_THREADS / 64];
+// Exclusive scan of the thread totals of one block of NT threads (NT a
+// multiple of 64); returns the exclusive prefix of this thread and writes
+// the block total to *total.
+template <int NT>
+__device__ __forceinline__ uint32_t block_excl_scan_n(uint32_t v, uint32_t *total) {
+    __shared__ uint32_t wsum[NT / 64];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     uint32_t inc = wave_incl_scan(v);
     if (lane == 63) wsum[wv] = inc;
     __syncthreads();
     uint32_t off = 0, tot = 0;
 #pragma unroll
-    for (int w = 0; w < SC_THREADS / 64; ++w) {
+    for (int w = 0; w < NT / 64; ++w) {
         uint32_t s = wsum[w];
         if (w < wv) off += s;
         tot += s;
@@ -62,24 +64,8 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t *total)
     return off + inc - v;
 }
 
-// The same for a block of NT threads (NT a multiple of 64).
-template <int NT>
-__device__ __forceinline__ uint32_t block_excl_scan_n(uint32_t v, uint32_t *total) {
-    __shared__ uint32_t wsumn[NT / 64];
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    uint32_t inc = wave_incl_scan(v);
-    if (lane == 63) wsumn[wv] = inc;
-    __syncthreads();
-    uint32_t off = 0, tot = 0;
-#pragma unroll
-    for (int w = 0; w < NT / 64; ++w) {
-        uint32_t s = wsumn[w];
-        if (w < wv) off += s;
-        tot += s;
-    }
-    __syncthreads();
-    *total = tot;
-    return off + inc - v;
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t *total) {
+    return block_excl_scan_n<SC_THREADS>(v, total);
 }
 
 // The scatter takes a tile with 512 threads, 16 elements each: 104 VGPRs and
