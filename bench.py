@@ -238,7 +238,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
-              "multi-GPU sharding is design-only (see DESIGN.md)", file=sys.stderr)
+              "the path would shard the fine grid into x-slabs, one per GPU, but no "
+              "multi-GPU path is built", file=sys.stderr)
         sys.exit(2)
     if args.copy_calibration > 0:
         copy_calibration(args.copy_calibration)
