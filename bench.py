@@ -49,7 +49,7 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--M", type=float, default=2e7)
     ap.add_argument("--N", type=int, default=256)
     ap.add_argument("--eps", type=float, default=1e-5)
