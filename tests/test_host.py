@@ -284,3 +284,15 @@ def test_product_does_not_import_oracle():
         text = f.read_text()
         assert not re.search(r"^\s*(from|import)\s+oracle\b", text, re.M), f
         assert "liboracle" not in text, f
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py runs on one GPU only: --gpus above 1 exits with status 2 and
+    says so, before touching any device."""
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU only" in r.stderr
+    assert r.stdout.strip() == ""
