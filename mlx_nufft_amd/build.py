@@ -44,11 +44,14 @@ def _run(cmd):
 # accumulation registers (one v_accvgpr_read per result element otherwise).
 # The max-ILP scheduler interleaves its tile reductions with the next tile's
 # MFMAs more tightly: 1 % faster at 2e7 points on 512^3 (three runs,
-# bit-identical); it made the z-sweep spread 1.3 % slower and left the sort
-# unchanged.
+# bit-identical). It also speeds the 2D y-window MFMA sweep with 8 vectors
+# per wave by 1-3 % (1e7 points, 2048^2, within 1 % for one vector); it made
+# the z-sweep spread 1.3 % slower, left the sort unchanged and moved the
+# type-1 FFT by -0.3 to +0.7 %, so those keep the default scheduler.
 EXTRA_FLAGS = {
     "mn_zgather.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form",
                        "-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+    "mn_ymfma.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
 }
 
 
