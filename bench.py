@@ -8,12 +8,9 @@ isign = +1, upsampfac 2 (w = 6, fine grid 512^3).
 A step is one end-to-end pass with inputs already resident in HBM:
 set_sources (fp64 fold/rescale, stable sort, z-sweep key starts) + execute
 (spread, pruned 512^3 FFT with crop/deconvolution). W untimed warmup steps,
-then K steps between torch.cuda.synchronize() calls, with nothing else
-enqueued between them: ms_per_step is that region's wall time over K. Each
-HIP event record leaves the GPU idle for about 10 us, so the per-step
-min/median/max and per-stage times (and the spread duration of `roofline`)
-come from K further steps with events on the launch stream around every
-step and stage (read after those steps, so nothing synchronises inside).
+then K steps between torch.cuda.synchronize() calls; HIP events recorded on
+the launch stream inside the timed region give per-step min/median/max and
+per-stage times (read after the region, so nothing synchronises inside it).
 The Python heap is collected and frozen (gc.collect + gc.freeze) before the
 region: a full collection of the interpreter's import-time objects costs
 30-40 ms of host time, and one that lands inside the region leaves the GPU
@@ -23,7 +20,7 @@ One JSON line is printed:
   value      = M / (ms_per_step) in NU pts/s (end to end, device-resident)
   roofline   = the spread kernel (the metric's "spread HBM GB/s"): algorithmic
                bytes M*(8 + 8*3 + 4) + 8*512^3 per launch over its mean
-               HIP-event duration in the instrumented steps, against 8 TB/s; traffic
+               HIP-event duration in the timed steps, against 8 TB/s; traffic
                from the committed rocprofv3 summary when it was measured on
                the current kernel source (None otherwise)
   cpu_baseline = the same type-1 on the host cores (fp32 OpenMP spread +
@@ -280,12 +277,12 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    # Timed region: K steps between two synchronisations, nothing else
-    # enqueued. Then K instrumented steps: HIP events on the launch stream
-    # bracket every step and every stage (the spread kernel is one launch per
-    # step); they are read only after those steps end.
+    # Timed region: K steps between two synchronisations. HIP events on the
+    # launch stream bracket every step and every stage (the spread kernel is
+    # one launch per step); they are read only after the region ends.
     step_ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                for _ in range(args.steps)]
+    plan.profile = plan.profile_deferred = True
     host_ms, gc_ms, gc_t = [], [], [0.0]
 
     def gc_cb(phase, info):
@@ -302,24 +299,17 @@ def main():
     gc.callbacks.append(gc_cb)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for a, b in step_ev:
+        a.record()
         h = time.perf_counter()
         step()
         host_ms.append((time.perf_counter() - h) * 1e3)
+        b.record()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     gc.callbacks.remove(gc_cb)
-    ms = (t1 - t0) * 1e3 / args.steps
-    # instrumented steps
-    plan.profile = plan.profile_deferred = True
-    t2 = time.perf_counter()
-    for a, b in step_ev:
-        a.record()
-        step()
-        b.record()
-    torch.cuda.synchronize()
-    ms_instr = (time.perf_counter() - t2) * 1e3 / args.steps
     plan.profile = plan.profile_deferred = False
+    ms = (t1 - t0) * 1e3 / args.steps
     step_raw = [a.elapsed_time(b) for a, b in step_ev]
     step_ms = sorted(step_raw)
     stage_sum = {}
@@ -381,8 +371,7 @@ def main():
                      "kernel": spread_kernel, "alg_bytes_per_launch": alg_bytes,
                      "ms_per_launch": spread_ms},
         "step_ms": {"min": step_ms[0], "median": step_ms[len(step_ms) // 2],
-                    "max": step_ms[-1], "argmax": step_raw.index(step_ms[-1]),
-                    "instrumented_ms_per_step": ms_instr},
+                    "max": step_ms[-1], "argmax": step_raw.index(step_ms[-1])},
         "host_ms_per_step": {"median": sorted(host_ms)[len(host_ms) // 2], "max": max(host_ms),
                              "argmax": host_ms.index(max(host_ms))},
         "gc_pauses_ms": [round(v, 2) for v in gc_ms],
