@@ -16,6 +16,8 @@ import torch
 
 from . import _lib as L
 
+_require = L.require
+
 MSUB = 1024                 # max points per spread/interp subproblem
 TILE_BUDGET = 80 * 1024     # LDS bytes for one padded tile (2 workgroups/CU)
 
@@ -508,7 +510,9 @@ def spread_zsweep_batch(pts, beta, cs, grids, zseg=ZSEG, presorted=False):
     """grids[b] = spread(cs[b]) for B vectors with the z-sweep, one launch
     with a wave per (block, vector) (overwrites grids)."""
     B = cs.shape[0]
-    assert grids.shape[0] == B and cs.is_contiguous() and grids.is_contiguous()
+    _require(grids.shape[0] == B and cs.shape[1] == pts.P and cs.is_contiguous()
+             and grids.is_contiguous(), "spread_zsweep_batch: cs must be (B, P) and grids "
+             "(B, n0, n1, n2), both contiguous")
     L.check(L.lib().mn_spread_zsweep_batch(ctypes.byref(pts.bins), float(beta), pts.P, B,
                                            int(zseg), L.ptr(pts.zstart),
                                            None if presorted else L.ptr(pts.perm),
@@ -549,7 +553,10 @@ def owner_bins(w, n):
 def spread_owner_c128(pts, beta, c, grid128, pre=None):
     """Owner-computes 3D spread into a complex128 grid that it fully
     overwrites (no zero fill); pts must carry bin starts (kind "zstream")."""
-    assert pts.bstart is not None and grid128.dtype == torch.complex128
+    _require(pts.bstart is not None and grid128.dtype == torch.complex128
+             and grid128.numel() >= int(np.prod([pts.bins.n[d] for d in range(3)])),
+             "spread_owner_c128: needs a point state with bin starts and a complex128 grid of "
+             "the fine-grid size")
     L.check(L.lib().mn_spread_owner_c128(ctypes.byref(pts.bins), float(beta), pts.P,
                                          L.ptr(pts.bstart), L.ptr(pts.perm), L.ptr3(pts.i1_rows()),
                                          L.ptr3(pts.fr_rows()), L.ptr(c),
@@ -694,9 +701,12 @@ def fft64_lines(A, nin, B, n, isign, src128, dec64, out, lines_last=False):
     complex128 -> out (A, n, B), or (n, A*B) with lines_last, complex128 or
     complex64 (by out's dtype)."""
     c64 = out.dtype == torch.complex64
-    assert src128.dtype == torch.complex128 and src128.numel() >= A * nin * B
-    assert out.numel() >= A * n * B and (c64 or out.dtype == torch.complex128)
-    assert dec64 is None or (dec64.dtype == torch.float64 and dec64.numel() >= nin)
+    _require(src128.dtype == torch.complex128 and src128.numel() >= A * nin * B,
+             f"fft64_lines: src must be complex128 with at least {A * nin * B} elements")
+    _require(out.numel() >= A * n * B and (c64 or out.dtype == torch.complex128),
+             f"fft64_lines: out must be complex64/128 with at least {A * n * B} elements")
+    _require(dec64 is None or (dec64.dtype == torch.float64 and dec64.numel() >= nin),
+             f"fft64_lines: dec must be float64 with at least {nin} elements")
     L.check(L.lib().mn_fft64_lines(int(A), int(nin), int(B), int(n), int(isign), L.ptr(src128),
                                    None if dec64 is None else L.ptr(dec64), L.ptr(out), int(c64),
                                    int(bool(lines_last)), L.stream()), "fft64_lines")
@@ -704,8 +714,10 @@ def fft64_lines(A, nin, B, n, isign, src128, dec64, out, lines_last=False):
 
 def transpose_c128(Bt, R, C, src, out):
     """out[b][c][r] = src[b][r][c] for complex128 (Bt, R, C) -> (Bt, C, R)."""
-    assert src.dtype == torch.complex128 and out.dtype == torch.complex128
-    assert src.numel() >= Bt * R * C and out.numel() >= Bt * R * C
+    _require(src.dtype == torch.complex128 and out.dtype == torch.complex128,
+             "transpose_c128: src and out must be complex128")
+    _require(src.numel() >= Bt * R * C and out.numel() >= Bt * R * C,
+             f"transpose_c128: src and out need at least {Bt * R * C} elements")
     L.check(L.lib().mn_transpose_c128(int(Bt), int(R), int(C), L.ptr(src), L.ptr(out),
                                       L.stream()), "transpose_c128")
 

@@ -176,6 +176,14 @@ def check(rc, what):
         raise _EXC.get(rc, RuntimeError)(f"{what}: {msg}")
 
 
+def require(cond, msg):
+    """Raise ValueError(msg) unless cond. Used before raw device pointers go
+    to the C side, which cannot see tensor sizes; unlike assert it is not
+    stripped under python -O."""
+    if not cond:
+        raise ValueError(msg)
+
+
 def stream():
     return c_vp(torch.cuda.current_stream().cuda_stream)
 

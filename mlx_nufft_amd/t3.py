@@ -33,6 +33,7 @@ import torch
 
 from . import _engine as E
 from . import _lib as L
+from .nd import PlanArgumentError
 from .sizing import (inner_kernel_params, kernel_ft, kernel_params, next235even,
                      quadrature, set_nhg_type3)
 
@@ -53,8 +54,12 @@ class GpuT3Plan:
         "vkfft" (not available on this platform: raises RuntimeError).
         ref: gpu_t3.py:288-441.
         """
-        assert prec in ("fp32", "coords64", "phases64", "crit64")
-        assert fft_backend in ("mlx", "vkfft")
+        # the reference asserts these (gpu_t3.py:303-304); PlanArgumentError is
+        # both a ValueError and an AssertionError and is not stripped by -O
+        if prec not in _PREC_FLAGS:
+            raise PlanArgumentError(f"prec must be one of {tuple(_PREC_FLAGS)}, got {prec!r}")
+        if fft_backend not in ("mlx", "vkfft"):
+            raise PlanArgumentError(f"fft_backend must be 'mlx' or 'vkfft', got {fft_backend!r}")
         if fft_backend == "vkfft":
             raise RuntimeError("the VkFFT-Metal FFT backend is not available on this "
                                "platform; use fft_backend='mlx' (rocFFT)")
@@ -311,8 +316,9 @@ class GpuT3Plan:
 
     def _strengths(self, c):
         cd = L.to_dev_c64(c, self.device).reshape(-1)
-        assert cd.numel() == self.P, \
-            f"c.size ({cd.numel()}) must equal number of sources ({self.P})"
+        if cd.numel() != self.P:
+            raise PlanArgumentError(f"c.size ({cd.numel()}) must equal number of sources "
+                                    f"({self.P})")
         return cd
 
     def execute(self, c, return_np=True):

@@ -153,6 +153,43 @@ def test_zsweep_class_ranks():
         assert np.array_equal(reach(o, w) == 3, (o + w - 1 >= 12) & (o > 3))
 
 
+def test_checks_survive_python_O(tmp_path):
+    """The size and option checks in front of raw device pointers (engine
+    wrappers) and the type-3 plan options raise under python -O, which
+    strips assert statements."""
+    import subprocess
+    import sys
+
+    script = tmp_path / "checks.py"
+    script.write_text(
+        "import sys, torch\n"
+        f"sys.path.insert(0, {str(ROOT)!r})\n"
+        "from mlx_nufft_amd import _engine as E, t3\n"
+        "def raises(fn, exc=ValueError):\n"
+        "    try:\n"
+        "        fn()\n"
+        "    except exc:\n"
+        "        return\n"
+        "    raise SystemExit('no ' + exc.__name__ + ' from ' + repr(fn))\n"
+        "c128 = torch.zeros(4, dtype=torch.complex128)\n"
+        "raises(lambda: E.transpose_c128(2, 3, 4, c128, c128))\n"
+        "raises(lambda: E.transpose_c128(1, 2, 2, c128, c128.to(torch.complex64)))\n"
+        "raises(lambda: E.fft64_lines(2, 3, 4, 8, 1, c128, None, c128))\n"
+        "class Pts:\n"
+        "    P = 5\n"
+        "cs = torch.zeros(2, 5, dtype=torch.complex64)\n"
+        "g = torch.zeros(3, 4, 4, 4, dtype=torch.complex64)\n"
+        "raises(lambda: E.spread_zsweep_batch(Pts(), 1.0, cs, g))\n"
+        "x = [torch.zeros(3, dtype=torch.float64)] * 3\n"
+        "raises(lambda: t3.GpuT3Plan(x, x, prec='fp16'))\n"
+        "raises(lambda: t3.GpuT3Plan(x, x, fft_backend='cufft'))\n"
+        "raises(lambda: t3.GpuT3Plan(x, x, prec='fp16'), AssertionError)\n"
+        "print('ok')\n")
+    out = subprocess.run([sys.executable, "-O", str(script)], capture_output=True, text=True,
+                         timeout=300)
+    assert out.returncode == 0 and out.stdout.strip().endswith("ok"), out.stdout + out.stderr
+
+
 # ------------------------------------------------------------ validation --
 
 def test_api_validation_errors(mn):
