@@ -84,7 +84,7 @@ def test_cfg2_2d_t2_radial_full(mn, oracle):
 
 def test_cfg3_3d_t1_t2_full(mn, oracle):
     """The north-star workload: type-1 on sampled modes against the direct
-    sum; the type-2 round trip of its output at 64 of the same points
+    sum; the type-2 round trip of its output at 512 of the same points
     against the direct type-2 sum of that output (gated by the type-1
     oracle error at the same w, beta, n_up); and the adjoint identity
     <T1 c, g> = <c, T2 g> at full size."""
