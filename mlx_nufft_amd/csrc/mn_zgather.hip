@@ -345,8 +345,9 @@ __global__ __launch_bounds__(64) void k_interp_zgather(
         // faster than staging a batch's results in LDS for one store)
         auto store = [&](float r, int q) __attribute__((always_inline)) {
             const int p = 16 * q + 4 * g + ((n & 7) >> 1);
-            if (n < 8 && p >= pb && p < pe)
-                reinterpret_cast<float *>(out)[2 * (int64_t)pmt[p] + (n & 1)] = r;
+            const float o = dpp_f<kDppQuadSwap>(r);
+            if (n < 8 && (n & 1) == 0 && p >= pb && p < pe)
+                out[pmt[p]] = make_float2(r, o);
         };
         for (int t = t0; t < t1; ++t) {
             const int xlo = __builtin_amdgcn_readfirstlane(oxt[max(16 * t, pb)]);
