@@ -254,9 +254,12 @@ int mn_spread_zsweep(const mn_bins *g, float beta, int64_t P, int zseg, const in
 /*
  * B strength vectors over one sorted point set: cs holds B rows of P
  * (caller order, or sorted order when perm is NULL), grids B fine grids of
- * n0*n1*n2 complex64, each fully overwritten. One launch covers all B
- * vectors, a wave per (block, vector). Each grid equals mn_spread_zsweep's
- * for its vector bit for bit.
+ * n0*n1*n2 complex64, each fully overwritten. One launch covers the vectors
+ * in pairs, a wave per (block, pair) sharing the weights and A operands
+ * (an odd last vector gets a wave per block of its own). Each grid equals
+ * mn_spread_zsweep's for its vector to fp32 rounding (the pair kernel sums
+ * the same products in other K-steps; bit for bit with the environment
+ * variable MN_ZSWEEP_PAIRS=0, which gives every vector its own wave).
  * ref: nd.py:683-742 (batched output-driven spread), nd.py:744-794.
  */
 int mn_spread_zsweep_batch(const mn_bins *g, float beta, int64_t P, int64_t B, int zseg,

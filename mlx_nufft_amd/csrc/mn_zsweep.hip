@@ -22,7 +22,8 @@
 // word carries the first tap's x, y cell in its block and its z cell in its
 // chunk, so the sweep needs no cell indices.
 //
-// Per batch (up to 64 points of one chunk, a lane per point):
+// Per batch (up to 64 points of one chunk, a lane per point; the two-vector
+// kernel takes 32-point batches with lane pairs, see its LP comment):
 //  * the lane's W ES weights of each axis (3W evaluations) are computed in
 //    the block of the previous batch's first K-step, where their VALU work
 //    overlaps its MFMAs (measured 1.5-3 % faster than in the prologue);
@@ -67,6 +68,7 @@
 //
 // ref: nd.py:492-579 (the reference's output-driven spread this replaces),
 // nd.py:298-372 (its bin sort and subproblem tables).
+#include <cstdlib>
 #include <cstring>
 
 #include "mn_common.h"
@@ -91,10 +93,9 @@ struct RowLayout {
     static constexpr int YO = (XO + W + 7 + 1) & ~1;
     static constexpr int ROW = ((YO + W + 7) + 3) / 4 * 4 + 2;
 };
-// rows and B entries of point positions 64..71 stay zero: K-step lanes past
-// a batch part read this group
-constexpr int kZeroGroup = 8;
-// halves per B-table slot row: 64 points + pad. 36 dwords: the 16 slots of a
+// (rows and B entries of the point positions just past a batch, 64..71 or
+// 32..39, stay zero: K-step lanes past a batch part read this group)
+// halves per B-table slot row of the one-vector kernel: 64 points + pad. 36 dwords: the 16 slots of a
 // quarter-wave's 16-byte reads start 4 (9 li mod 16) banks in, all apart.
 constexpr int BST = 72;
 constexpr int kTab = 16 * BST;  // halves per B table
@@ -184,10 +185,13 @@ __device__ __forceinline__ void cur_load(Cursor &k, const Ranges &rg, int c, int
 }
 
 // One lane's point of a batch, its loads issued (the strength, which needs
-// src, is loaded one batch later). A batch takes up to 64 points from the
-// current chunk (part A, lanes [0, nA)) and, when that chunk ends first, the
-// head of the next chunk (part B, lanes [oB, oB + nB) from the next multiple
-// of 8), so that the prologue runs on full batches across chunk ends.
+// src, is loaded one batch later). A batch takes up to NBP points (64, or 32
+// when lanes l and l + 32 share a point) from the current chunk (part A,
+// slots [0, nA)) and, when that chunk ends first, the head of the next chunk
+// (part B, slots [oB, oB + nB) from the next multiple of 8), so that the
+// prologue runs on full batches across chunk ends. With 32-point batches the
+// lower lane of a pair loads the point's x fraction into fx, the upper its y
+// fraction; fy is unused.
 struct ZPoint {
     int cA, nA, cB, oB, nB;  // uniform; nA = 0: done
     bool valid, inB;
@@ -197,7 +201,7 @@ struct ZPoint {
     float2 pv;               // prephase (1 if none)
 };
 
-template <bool PRE>
+template <bool PRE, int NBP>
 __device__ __forceinline__ ZPoint zp_next(Cursor &k, const Ranges &rg, int lane,
                                           const uint32_t *__restrict__ perm,
                                           const uint32_t *__restrict__ word, const CF3s &frs,
@@ -208,35 +212,41 @@ __device__ __forceinline__ ZPoint zp_next(Cursor &k, const Ranges &rg, int lane,
         while (k.bat >= k.tot && k.c <= k.clast) cur_load(k, rg, k.c + 1, lane);
     }
     ZPoint q;
+    const int lp = lane & (NBP - 1);  // the point's slot in the batch
     q.cA = k.c;
-    q.nA = k.c <= k.clast ? min(64, k.tot - k.bat) : 0;
+    q.nA = k.c <= k.clast ? min(NBP, k.tot - k.bat) : 0;
     q.cB = k.c + 1;
     q.oB = (q.nA + 7) & ~7;
     q.nB = 0;
-    // part A: elements bat + lane of the current chunk
-    const int eA = k.bat + lane;
+    // part A: elements bat + lp of the current chunk
+    const int eA = k.bat + lp;
     int r = (eA >= k.p1 ? 1 : 0) + (eA >= k.p2 ? 1 : 0) + (eA >= k.p3 ? 1 : 0);
     int dj = r == 0 ? k.dj0 : (r == 1 ? k.dj1 : (r == 2 ? k.dj2 : k.dj3));
     int e = eA;
     k.bat += q.nA;
-    if (q.nA > 0 && q.oB < 64 && k.c + 1 <= k.clast) {
+    if (q.nA > 0 && q.oB < NBP && k.c + 1 <= k.clast) {
         // part B: the head of the next chunk, whose bounds were prefetched
         cur_load(k, rg, k.c + 1, lane);
-        q.nB = min(64 - q.oB, k.tot);
+        q.nB = min(NBP - q.oB, k.tot);
         k.bat = q.nB;
-        if (lane >= q.oB) {
-            e = lane - q.oB;
+        if (lp >= q.oB) {
+            e = lp - q.oB;
             r = (e >= k.p1 ? 1 : 0) + (e >= k.p2 ? 1 : 0) + (e >= k.p3 ? 1 : 0);
             dj = r == 0 ? k.dj0 : (r == 1 ? k.dj1 : (r == 2 ? k.dj2 : k.dj3));
         }
     }
-    q.inB = lane >= q.oB;
-    q.valid = lane < q.nA || (q.inB && lane < q.oB + q.nB);
+    q.inB = lp >= q.oB;
+    q.valid = lp < q.nA || (q.inB && lp < q.oB + q.nB);
     const uint32_t j = q.valid ? (uint32_t)(e + dj) : 0u;
     q.r = r;
     q.wd = word[j];
-    q.fx = frs.p[0][j];
-    q.fy = frs.p[1][j];
+    if constexpr (NBP == 64) {
+        q.fx = frs.p[0][j];
+        q.fy = frs.p[1][j];
+    } else {
+        q.fx = frs.p[lane >> 5][j];
+        q.fy = 0.f;
+    }
     q.fz = frs.p[2][j];
     const uint32_t pj = (perm ? perm : word)[j];
     q.src = perm ? pj : j;
@@ -272,6 +282,20 @@ __device__ __forceinline__ void split_prod8(const float (&x)[8], const float (&y
     }
 }
 
+__device__ __forceinline__ int lane_id() { return (int)threadIdx.x; }
+
+// Wave-wide maximum, over the lanes of mask m, of a small non-negative
+// integer (< 512), by ballots.
+__device__ __forceinline__ int masked_max9(int v, uint64_t m) {
+    int r = 0;
+#pragma unroll
+    for (int b = 8; b >= 0; --b) {
+        const int cand = r | (1 << b);
+        if (__ballot(v >= cand) & m) r = cand;
+    }
+    return r;
+}
+
 #ifndef ZS_OCC
 #define ZS_OCC 2
 #endif
@@ -286,8 +310,23 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
     static_assert(VB == 1 || VB == 2, "one or two strength vectors per wave");
     constexpr float kAxisScale = 128.0f;
     constexpr int XO = RowLayout<W>::XO, YO = RowLayout<W>::YO, ROW = RowLayout<W>::ROW;
-    __shared__ __align__(16) float rows[(8 * kZeroGroup + 8) * ROW];
-    __shared__ __align__(16) _Float16 btab[VB][4 * kTab];
+    // Two vectors per wave take 32-point batches (LP: lanes l and l + 32
+    // share a point): the lower lane evaluates its x weights and writes its
+    // x row and vector 0's B column, the upper lane its y weights, y row and
+    // vector 1's B column, and each evaluates half of its z weights (the
+    // pair swaps them), so the prologue is one instruction stream for both
+    // and the tables take 16 KB (two waves per SIMD; 64-point tables for two
+    // vectors took 29 KB, 1.25 waves per SIMD).
+    constexpr bool LP = VB == 2;
+    constexpr int NBP = LP ? 32 : 64;          // points per batch
+    constexpr int ZGP = NBP / 8;               // the always-zero group
+    constexpr int BSTP = LP ? NBP + 8 : BST;   // halves per B-table slot row
+    constexpr int kTabP = 16 * BSTP;           // halves per B table
+    constexpr int HW = (W + 1) / 2;            // z weights per lane of a pair
+    static_assert(!LP || BSTP % 4 == 0, "16-byte B reads");
+    __shared__ __align__(16) float rows[(NBP + 8) * ROW];
+    __shared__ __align__(16) _Float16 btab[VB][4 * kTabP];
+    const bool lx = !LP || lane_id() < 32;  // x half of a lane pair (every lane when !LP)
     int bx, by, seg;
     zs_block(xcd_remap(blockIdx.x, (int64_t)nbx * nby * nseg), nbx, nby, bx, by, seg);
     // this wave's strength vectors and grids
@@ -367,7 +406,7 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
     // the K-step of 32 points over the 8-point groups [gs, min(gs + 4, g1))
     // of the tables; lanes past g1 read the zero group
     auto kstep = [&](int gs, int g1) __attribute__((always_inline)) {
-        const int pos = 8 * (gs + lk < g1 ? gs + lk : kZeroGroup);
+        const int pos = 8 * (gs + lk < g1 ? gs + lk : ZGP);
         float wx0[8], wx1[8], wy0[8], wy1[8];
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
@@ -383,13 +422,13 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
 #pragma unroll
         for (int q = 0; q < 4; ++q)
             split_prod8((q >> 1) ? wx1 : wx0, (q & 1) ? wy1 : wy0, ah[q], al[q]);
-        const int bo = li * BST + pos;
+        const int bo = li * BSTP + pos;
 #pragma unroll
         for (int v = 0; v < VB; ++v) {
             const mh8 brh = *reinterpret_cast<const mh8 *>(&btab[v][bo]);
-            const mh8 brl = *reinterpret_cast<const mh8 *>(&btab[v][kTab + bo]);
-            const mh8 bih = *reinterpret_cast<const mh8 *>(&btab[v][2 * kTab + bo]);
-            const mh8 bil = *reinterpret_cast<const mh8 *>(&btab[v][3 * kTab + bo]);
+            const mh8 brl = *reinterpret_cast<const mh8 *>(&btab[v][kTabP + bo]);
+            const mh8 bih = *reinterpret_cast<const mh8 *>(&btab[v][2 * kTabP + bo]);
+            const mh8 bil = *reinterpret_cast<const mh8 *>(&btab[v][3 * kTabP + bo]);
             // consecutive MFMAs go to different accumulators: each of
             // the 8 tiles of a vector is used again only 8 instructions
             // later
@@ -419,31 +458,72 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
     };
 
     // the 3W ES weights of a point (x and y scaled by kAxisScale); the scaled
-    // distance (a - f) 2/w of tap a is one fma
-    auto es_eval = [&](const ZPoint &p, float (&ew)[3][W]) __attribute__((always_inline)) {
+    // distance (a - f) 2/w of tap a is one fma. A lane pair (LP) splits them:
+    // ew[0] holds the lane's x (lower lane) or y (upper lane) weights, ew[1]
+    // z weights [0, HW) (lower) or [HW, 2 HW) (upper; tap W is a dummy when
+    // W is odd).
+    constexpr int NE = LP ? 2 : 3;
+    auto es_eval = [&](const ZPoint &p, float (&ew)[NE][W]) __attribute__((always_inline)) {
         constexpr float ih = 2.0f / W;
+        if constexpr (LP) {
+            const float zo = lx ? 0.f : (float)HW * ih;
 #pragma unroll
-        for (int a = 0; a < W; ++a) {
-            const float ca = (float)a * ih;
-            ew[0][a] = zs_es(__builtin_fmaf(-p.fx, ih, ca), bl2e) * kAxisScale;
-            ew[1][a] = zs_es(__builtin_fmaf(-p.fy, ih, ca), bl2e) * kAxisScale;
-            ew[2][a] = zs_es(__builtin_fmaf(-p.fz, ih, ca), bl2e);
+            for (int a = 0; a < W; ++a)
+                ew[0][a] = zs_es(__builtin_fmaf(-p.fx, ih, (float)a * ih), bl2e) * kAxisScale;
+#pragma unroll
+            for (int a = 0; a < HW; ++a)
+                ew[1][a] = zs_es(__builtin_fmaf(-p.fz, ih, zo + (float)a * ih), bl2e);
+        } else {
+#pragma unroll
+            for (int a = 0; a < W; ++a) {
+                const float ca = (float)a * ih;
+                ew[0][a] = zs_es(__builtin_fmaf(-p.fx, ih, ca), bl2e) * kAxisScale;
+                ew[1][a] = zs_es(__builtin_fmaf(-p.fy, ih, ca), bl2e) * kAxisScale;
+                ew[2][a] = zs_es(__builtin_fmaf(-p.fz, ih, ca), bl2e);
+            }
         }
     };
+    constexpr int NV = LP ? 1 : VB;  // strength vectors a lane carries
 
     // batch p with its strengths cp and weights ew; computes ewn for the next
     // batch pn
-    auto process = [&](const ZPoint &p, const float2 (&cp)[VB], const float (&ew)[3][W],
-                       const ZPoint &pn, float (&ewn)[3][W]) __attribute__((always_inline)) {
+    auto process = [&](const ZPoint &p, const float2 (&cp)[NV], const float (&ew)[NE][W],
+                       const ZPoint &pn, float (&ewn)[NE][W]) __attribute__((always_inline)) {
         int wcA, offA, wcB, offB;
         chunk_pos(p.cA, wrap_off, wcA, offA);
         chunk_pos(p.cB, wrap_off, wcB, offB);
         const int off = p.inB ? offB : offA;
         // points of chunk -2 below the reach of z = 0 take no part
         const bool valid = p.valid && (int)(p.wd >> 29) + off >= 0;
-        float2 cv[VB];
+        float2 cv[NV];
+        if constexpr (LP) {
+            // the lane's own vector (lower lanes 0, upper lanes 1); the scale
+            // of vector v is checked over its half of the wave
+            cv[0] = valid ? make_float2(cp[0].x * p.pv.x - cp[0].y * p.pv.y,
+                                        cp[0].x * p.pv.y + cp[0].y * p.pv.x)
+                          : make_float2(0.f, 0.f);
+            const float mx = fmaxf(fabsf(cv[0].x), fabsf(cv[0].y));
+            const int eb = (__float_as_int(mx) >> 23) & 0xff;
 #pragma unroll
-        for (int v = 0; v < VB; ++v) {
+            for (int v = 0; v < VB; ++v) {
+                const uint64_t hm = v ? 0xFFFFFFFF00000000ull : 0x00000000FFFFFFFFull;
+                if (sexp[v] == INT32_MIN || (__ballot(eb > 140 - sexp[v]) & hm)) {
+                    const int want = min(140 - masked_max9(eb, hm), 139);
+                    if (sexp[v] != INT32_MIN) {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                are[v][q][r] = __builtin_amdgcn_ldexpf(are[v][q][r], want - sexp[v]);
+                                aim[v][q][r] = __builtin_amdgcn_ldexpf(aim[v][q][r], want - sexp[v]);
+                            }
+                    }
+                    sexp[v] = want;
+                }
+            }
+        }
+#pragma unroll
+        for (int v = 0; v < (LP ? 0 : VB); ++v) {
             cv[v] = valid ? make_float2(cp[v].x * p.pv.x - cp[v].y * p.pv.y,
                                         cp[v].x * p.pv.y + cp[v].y * p.pv.x)
                           : make_float2(0.f, 0.f);
@@ -468,20 +548,58 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
         window_to(p.cA);
         __syncthreads();  // the previous batch's K-steps are done with the tables
         {
-            float2 *rzx = reinterpret_cast<float2 *>(rows + lane * ROW + XO);
-            float2 *rzy = reinterpret_cast<float2 *>(rows + lane * ROW + YO);
+            if constexpr (LP) {
+                float2 *rz = reinterpret_cast<float2 *>(rows + (lane & 31) * ROW + (lx ? XO : YO));
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                rzx[i] = make_float2(0.f, 0.f);
-                rzy[i] = make_float2(0.f, 0.f);
+                for (int i = 0; i < 4; ++i) rz[i] = make_float2(0.f, 0.f);
+            } else {
+                float2 *rzx = reinterpret_cast<float2 *>(rows + lane * ROW + XO);
+                float2 *rzy = reinterpret_cast<float2 *>(rows + lane * ROW + YO);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    rzx[i] = make_float2(0.f, 0.f);
+                    rzy[i] = make_float2(0.f, 0.f);
+                }
             }
             float4 *bz = reinterpret_cast<float4 *>(&btab[0][0]);
-            constexpr int nb4 = VB * 4 * kTab / 8;  // float4 count of the B tables
+            constexpr int nb4 = VB * 4 * kTabP / 8;  // float4 count of the B tables
 #pragma unroll
             for (int i = lane; i < nb4; i += 64) bz[i] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
         __syncthreads();
-        if (valid) {
+        if constexpr (LP) {
+            // the pair's z weights: each lane holds half and takes the other
+            // half from its partner (every lane swaps, valid or not)
+            float wz[W];
+#pragma unroll
+            for (int a = 0; a < HW; ++a) {
+                const float mine = ew[1][a];
+                const float oth = __shfl_xor(mine, 32, 64);
+                wz[a] = lx ? mine : oth;
+                if (HW + a < W) wz[HW + a] = lx ? oth : mine;
+            }
+            if (valid) {
+                const int lp = lane & 31;
+                const int ox = (int)((p.wd >> 23) & 7u) - ((p.r & 1) ? ZB : 0);
+                const int oy = (int)((p.wd >> 26) & 7u) - ((p.r & 2) ? ZB : 0);
+                const int sz = (int)(p.wd >> 29) + off;
+                const int se = lx ? sexp[0] : sexp[1];
+                const float2 cb = make_float2(__builtin_amdgcn_ldexpf(cv[0].x, se),
+                                              __builtin_amdgcn_ldexpf(cv[0].y, se));
+                float *rr = rows + lp * ROW + (lx ? XO + ox : YO + oy);
+                _Float16 *bt = &btab[lx ? 0 : 1][0] + sz * BSTP + lp;
+#pragma unroll
+                for (int a = 0; a < W; ++a) {
+                    rr[a] = ew[0][a];
+                    _Float16 *o = bt + a * BSTP;
+                    const auto h = __builtin_amdgcn_cvt_pkrtz(cb.x * wz[a], cb.y * wz[a]);
+                    o[0] = h[0];
+                    o[kTabP] = (_Float16)__builtin_fmaf(cb.x, wz[a], -(float)h[0]);
+                    o[2 * kTabP] = h[1];
+                    o[3 * kTabP] = (_Float16)__builtin_fmaf(cb.y, wz[a], -(float)h[1]);
+                }
+            }
+        } else if (valid) {
             // first tap relative to this block (minus 8 for points of the -x
             // / -y neighbour blocks) and its slot in its chunk's window
             const int ox = (int)((p.wd >> 23) & 7u) - ((p.r & 1) ? ZB : 0);
@@ -522,37 +640,41 @@ k_spread_zsweep(int n0, int n1, int n2, int nbx, int nby, int nzc, int zseg, int
         }
     };
 
-    auto strengths = [&](const ZPoint &p, float2 (&cv)[VB]) __attribute__((always_inline)) {
+    auto strengths = [&](const ZPoint &p, float2 (&cv)[NV]) __attribute__((always_inline)) {
+        if constexpr (LP) {
+            cv[0] = c[(lane >> 5) * cstride + p.src];
+        } else {
 #pragma unroll
-        for (int v = 0; v < VB; ++v) cv[v] = c[v * cstride + p.src];
+            for (int v = 0; v < VB; ++v) cv[v] = c[v * cstride + p.src];
+        }
     };
 
     // the zero group's rows (the B tables are cleared with every batch)
-    for (int i = lane; i < 8 * ROW; i += 64) rows[8 * kZeroGroup * ROW + i] = 0.f;
+    for (int i = lane; i < 8 * ROW; i += 64) rows[8 * ZGP * ROW + i] = 0.f;
     const int clast = (zend - 1) / ZC;  // the last chunk of the segment
     const Ranges rg{bx, by, bxm - bx, bym - by, nby, nzc, clast, zstart};
     Cursor cur;
     cur.pc = INT32_MIN;
     cur.clast = clast;
     cur_load(cur, rg, (z0 == 0 && wrap_off > 0) ? -2 : z0 / ZC - 1, lane);
-    ZPoint pa = zp_next<PRE>(cur, rg, lane, perm, word, frs, pre);
-    float2 ca[VB], cb[VB], cc[VB];
-    float ewa[3][W], ewb[3][W], ewc[3][W];
+    ZPoint pa = zp_next<PRE, NBP>(cur, rg, lane, perm, word, frs, pre);
+    float2 ca[NV], cb[NV], cc[NV];
+    float ewa[NE][W], ewb[NE][W], ewc[NE][W];
     strengths(pa, ca);  // idle lanes read c[perm[0]]: their rows stay zero
     es_eval(pa, ewa);
-    ZPoint pb = zp_next<PRE>(cur, rg, lane, perm, word, frs, pre);
+    ZPoint pb = zp_next<PRE, NBP>(cur, rg, lane, perm, word, frs, pre);
     ZPoint pc;
     for (;;) {
         if (pa.nA == 0) break;
-        pc = zp_next<PRE>(cur, rg, lane, perm, word, frs, pre);
+        pc = zp_next<PRE, NBP>(cur, rg, lane, perm, word, frs, pre);
         strengths(pb, cb);
         process(pa, ca, ewa, pb, ewb);
         if (pb.nA == 0) break;
-        pa = zp_next<PRE>(cur, rg, lane, perm, word, frs, pre);
+        pa = zp_next<PRE, NBP>(cur, rg, lane, perm, word, frs, pre);
         strengths(pc, cc);
         process(pb, cb, ewb, pc, ewc);
         if (pc.nA == 0) break;
-        pb = zp_next<PRE>(cur, rg, lane, perm, word, frs, pre);
+        pb = zp_next<PRE, NBP>(cur, rg, lane, perm, word, frs, pre);
         strengths(pa, ca);
         process(pc, cc, ewc, pa, ewa);
     }
@@ -580,6 +702,11 @@ int64_t zsweep_nkeys(const mn_bins *g) {
 }
 
 namespace {
+
+bool zsweep_pairs() {
+    const char *e = std::getenv("MN_ZSWEEP_PAIRS");
+    return !(e && e[0] == '0' && e[1] == '\0');
+}
 
 struct ZArgs {
     const mn_bins *g;
@@ -609,19 +736,32 @@ struct ZLaunch {
             const int64_t nw = (int64_t)nbx * nby * nseg;
             const float bl2e = (float)(a.beta * 1.4426950408889634);
             const int64_t gs = (int64_t)n0 * n1 * n2;
-            // one wave per (block, vector). Waves carrying two vectors (the
-            // weights and A operands formed once) were no faster: the second
-            // vector's B tables take the wave to 29 KB of LDS, 1.25 waves per
-            // SIMD instead of 2 (B = 2: 2.97 against 2.85 ms; B = 8 even).
-            const dim3 gridv((unsigned)nw, (unsigned)a.B);
+            // Batches of vectors: one wave per (block, pair of vectors), in
+            // 32-point batches (the weights, point loads and A operands are
+            // formed once for both vectors); an odd last vector, and single
+            // vectors, take one wave per (block, vector). MN_ZSWEEP_PAIRS=0
+            // in the environment gives every vector its own wave.
+            int64_t B1 = a.B;
+            if (a.B >= 2 && !a.pre && zsweep_pairs()) {
+                const int64_t np = a.B / 2;
+                k_spread_zsweep<W, false, 2><<<dim3((unsigned)nw, (unsigned)np), 64, 0, a.s>>>(
+                    n0, n1, n2, nbx, nby, nzc, a.zseg, nseg, bl2e, a.zstart, a.perm, a.word,
+                    a.frs, a.c, a.P, nullptr, a.grid, gs);
+                MN_LAUNCH_CHECK("spread_zsweep (vector pairs)");
+                if ((a.B & 1) == 0) return MN_OK;
+                B1 = 1;
+            }
+            const float2 *c1 = a.c + (a.B - B1) * a.P;
+            float2 *g1 = a.grid + (a.B - B1) * gs;
+            const dim3 gridv((unsigned)nw, (unsigned)B1);
             if (a.pre)
                 k_spread_zsweep<W, true, 1><<<gridv, 64, 0, a.s>>>(
                     n0, n1, n2, nbx, nby, nzc, a.zseg, nseg, bl2e, a.zstart, a.perm, a.word,
-                    a.frs, a.c, a.P, a.pre, a.grid, gs);
+                    a.frs, c1, a.P, a.pre, g1, gs);
             else
                 k_spread_zsweep<W, false, 1><<<gridv, 64, 0, a.s>>>(
                     n0, n1, n2, nbx, nby, nzc, a.zseg, nseg, bl2e, a.zstart, a.perm, a.word,
-                    a.frs, a.c, a.P, a.pre, a.grid, gs);
+                    a.frs, c1, a.P, a.pre, g1, gs);
             MN_LAUNCH_CHECK("spread_zsweep");
             return MN_OK;
         }
