@@ -30,8 +30,9 @@
 // The wx sum runs on the accumulator layout (lane (n, g) holds rows 4g + i
 // of column n), the wz weights and the scales multiply it, and a
 // reduce-scatter over each 8 lanes of a row (then a sum of the two halves)
-// leaves each of the tile's 8 results (4 points x re, im) in two lanes, one
-// of which stores it.
+// leaves each of the tile's 8 results (4 points x re, im) in two lanes; the
+// lane holding a point's real part takes the imaginary part from its DPP
+// partner and stores the pair as one 8-byte value.
 //
 // Batches. Up to 64 points (a lane per point): the prologue evaluates the
 // point's 3w ES weights once and writes the tables the tiles read -- its A
