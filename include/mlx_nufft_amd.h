@@ -361,6 +361,16 @@ int mn_spread_ymfma(const mn_bins *g, float beta, int64_t P, int64_t B, int yseg
                     mn_stream_t stream);
 
 /*
+ * out (P x B, point-major) = the transpose of in (B x P, vector-major), for
+ * B complex64 strength vectors of P points: the layout mn_spread_ymfma
+ * reads with point_major = 1, so that a point visit gathers its B
+ * strengths as one run. in and out must not overlap.
+ * ref: nd.py:683-742 (the reference's batched spread takes the (n_trans, M)
+ * strength matrix whole).
+ */
+int mn_pointmajor_c64(int64_t B, int64_t P, const void *in, void *out, mn_stream_t stream);
+
+/*
  * out[j] = in[perm[j]] for P complex64 values (a strength vector into
  * sorted order). ref: nd.py:603 (mx.take of c by perm, GM spread).
  */

@@ -483,7 +483,12 @@ def spread_ymfma(pts, beta, cs, grids):
     V2 = ctypes.c_void_p * 2
     pm = 0
     if B > 1:
-        cs = cs.t().contiguous()
+        _require(cs.is_contiguous() and cs.dtype == torch.complex64,
+                 "spread_ymfma: cs must be a contiguous complex64 (B, P) tensor")
+        ct = torch.empty((int(cs.shape[1]), B), dtype=torch.complex64, device=cs.device)
+        L.check(L.lib().mn_pointmajor_c64(B, int(cs.shape[1]), L.ptr(cs), L.ptr(ct), L.stream()),
+                "pointmajor")
+        cs = ct
         pm = 1
     L.check(L.lib().mn_spread_ymfma(ctypes.byref(pts.bins), float(beta), pts.P, B,
                                     ymfma_segment(n_up, B), L.ptr(pts.ystart), L.ptr(pts.perm),

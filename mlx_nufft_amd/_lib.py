@@ -84,6 +84,7 @@ _SIGS = [
     ("mn_interp_zgather", c_int, [ctypes.POINTER(Bins), c_float, c_int64, c_int64, c_int, c_vp,
                                   c_vp, c_vp, VP3, c_vp, c_vp, c_vp]),
     ("mn_permute_c64", c_int, [c_int64, c_vp, c_vp, c_vp, c_vp]),
+    ("mn_pointmajor_c64", c_int, [c_int64, c_int64, c_vp, c_vp, c_vp]),
     ("mn_ysweep_nkeys", c_int64, [ctypes.POINTER(Bins)]),
     ("mn_ysweep_setpts", c_int, [ctypes.POINTER(Bins), c_int64, ctypes.c_void_p * 2, c_int, c_vp,
                                  ctypes.c_void_p * 2, c_vp]),

@@ -196,3 +196,21 @@ def test_type1_2d_ysweep_vs_direct(N, isign, path, oracle, mn):
     err = oracle.rel_l2(f, fe)
     print(f"  err={err:.3e} ref_err={ref_err:.3e}")
     assert err <= max(eps, 2 * ref_err)
+
+
+@pytest.mark.parametrize("B", [1, 2, 3, 4, 5, 8, 9])
+def test_pointmajor_transpose(B, mn):
+    """mn_pointmajor_c64 (vector-major strengths to the point-major layout
+    the y-window MFMA sweep reads) equals torch's transpose bit for bit,
+    for the LDS-tiled B = 2, 4, 8 and the per-element other B, with P not a
+    multiple of any tile (partial last tiles)."""
+    from mlx_nufft_amd import _lib as L
+
+    print(f"case pointmajor B={B}", flush=True)
+    rng = np.random.default_rng(60 + B)
+    for P in (1, 1000, 2048 * 3 + 17):
+        cs = torch.from_numpy((rng.standard_normal((B, P)) + 1j * rng.standard_normal((B, P)))
+                              .astype(np.complex64)).cuda()
+        out = torch.full((P, B), float("nan"), dtype=torch.complex64, device="cuda")
+        L.check(L.lib().mn_pointmajor_c64(B, P, L.ptr(cs), L.ptr(out), L.stream()), "pointmajor")
+        assert torch.equal(out, cs.t().contiguous()), (B, P)
