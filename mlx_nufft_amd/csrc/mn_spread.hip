@@ -81,9 +81,59 @@ __global__ __launch_bounds__(256) void k_spread_tiled(Geom g, float bl2e, float 
     }
     const int nvec = BATCH ? bc : 1;
     for (int q = threadIdx.x; q < 2 * T * nvec; q += 256) lds[q] = 0.0;
+
+    // 3D fp64 tiles: the lanes of one atomic instruction add the same tap
+    // offset to their points' tile bases, so two lanes whose bases agree
+    // modulo 32 doubles (the 64 four-byte banks) collide. The subproblem's
+    // points are taken in an order that deals them round-robin over the 32
+    // residues of their base (round k holds the k-th point of every residue
+    // that has one), so that consecutive lanes hit distinct banks while
+    // every residue still has points.
+    constexpr bool RORD = F64 && DIM == 3;
+    constexpr int ORD_MAX = 1024;  // points per subproblem the reordering takes
+    __shared__ uint16_t ord[RORD ? ORD_MAX : 1];
+    __shared__ int rcnt[32];
+    const bool use_ord = RORD && cnt <= ORD_MAX;
+    if (use_ord) {
+        if (threadIdx.x < 32) rcnt[threadIdx.x] = 0;
+        __syncthreads();
+        constexpr int NI = ORD_MAX / 256;
+        int res[NI], rk[NI];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int t = threadIdx.x + 256 * i;
+            res[i] = rk[i] = 0;
+            if (t < cnt) {
+                const int64_t j = (int64_t)s0 + t;
+                int lc[3];
+#pragma unroll
+                for (int d = 0; d < 3; ++d)
+                    lc[d] = local_cell(i1s.p[d][j], W / 2, g.n[d], b[d], g.m[d]);
+                res[i] = (((lc[0] * p1 + lc[1]) * p2 + lc[2]) & 31);
+                rk[i] = atomicAdd(&rcnt[res[i]], 1);
+            }
+        }
+        __syncthreads();
+        // slot = points in earlier rounds (sum over residues of min(n_r, k))
+        // plus the residues below this one that reach round k
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int t = threadIdx.x + 256 * i;
+            if (t < cnt) {
+                int slot = 0;
+#pragma unroll
+                for (int r = 0; r < 32; ++r) {
+                    const int n = rcnt[r];
+                    slot += min(n, rk[i]) + ((r < res[i] && n > rk[i]) ? 1 : 0);
+                }
+                ord[slot] = (uint16_t)t;
+            }
+        }
+    }
     __syncthreads();
 
-    for (int t = threadIdx.x; t < cnt; t += 256) {
+    for (int t0 = threadIdx.x; t0 < cnt; t0 += 256) {
+        const int t = use_ord ? (int)ord[t0] : t0;
         const int64_t j = (int64_t)s0 + t;
         const uint32_t src = perm[j];
         float wt[DIM][W];
