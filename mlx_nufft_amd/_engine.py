@@ -41,10 +41,11 @@ SPREAD_CELL_BYTES = 16   # spread tiles accumulate complex values in fp64
 INTERP_CELL_BYTES = 8    # interp tiles hold complex64 grid values
 
 
-def bin_sizes(dim, w, n_up, cell_bytes=SPREAD_CELL_BYTES):
+def bin_sizes(dim, w, n_up, cell_bytes=SPREAD_CELL_BYTES, npts=None):
     """Bin size m per dim: the padded tile (m + w - 1 cells per dim,
-    cell_bytes each) must fit tile_budget() bytes of LDS. Overridable with
-    the environment variable MN_BIN_M="m0,m1,m2" (tuning)."""
+    cell_bytes each) must fit tile_budget() bytes of LDS. npts (the number
+    of points, when known) lets the 3D interp tiles grow for sparse points.
+    Overridable with the environment variable MN_BIN_M="m0,m1,m2" (tuning)."""
     budget = tile_budget()
     env = os.environ.get("MN_BIN_M")
     if env:
@@ -64,7 +65,14 @@ def bin_sizes(dim, w, n_up, cell_bytes=SPREAD_CELL_BYTES):
         # 512^3, m = (8, 8, m2): w = 5: 2.11 ms at m2 = 8, 1.94 at 13;
         # w = 6: 2.44 at 8, 2.35 at 12, 3.07 at 11; w = 7: 3.13 at 8, 3.03
         # at 11, 4.19 at 10. At w = 4, 8 is best within 2 %.
-        m = [8, 8, max(8, 18 - w) if w >= 5 else 8]
+        # Sparse points (under 0.1 per cell, as type-3 targets) leave few
+        # points per bin, so the tile load dominates and wider bins re-read
+        # less halo: cfg 5's targets (1e6 on 240^3, w = 9) gather in 0.276 ms
+        # with m = (11, 11, 9), 0.289 with 10^3, 0.318 with 9^3, 0.361 with
+        # (8, 8, 9).
+        mxy = 11 if (dim == 3 and npts is not None
+                     and npts < 0.1 * float(np.prod([float(n) for n in n_up]))) else 8
+        m = [mxy, mxy, max(8, 18 - w) if w >= 5 else 8]
     else:
         side = int(round((budget / cell_bytes) ** (1.0 / 3.0) - 1e-9))
         while cell_bytes * side ** 3 > budget:
@@ -77,9 +85,9 @@ def bin_sizes(dim, w, n_up, cell_bytes=SPREAD_CELL_BYTES):
     return m
 
 
-def make_bins(dim, w, n_up, m=None, cell_bytes=SPREAD_CELL_BYTES):
+def make_bins(dim, w, n_up, m=None, cell_bytes=SPREAD_CELL_BYTES, npts=None):
     if m is None:
-        m = bin_sizes(dim, w, n_up, cell_bytes)
+        m = bin_sizes(dim, w, n_up, cell_bytes, npts=npts)
     return L.Bins.make(dim, w, list(n_up), m)
 
 

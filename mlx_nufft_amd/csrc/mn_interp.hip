@@ -112,10 +112,59 @@ __global__ __launch_bounds__(256) void k_interp_tiled(Geom g, float bl2e, float 
     __syncthreads();
 
     if constexpr (DIM == 3) {
+        // The lanes of one tile read add the same tap offset to their
+        // points' bases, so points whose bases agree modulo 32 float2 (the
+        // 64 four-byte banks) collide. The subproblem's points are taken in
+        // an order that deals them round-robin over 16 classes of base / 2
+        // (a lane pair reads base and base + p1 p2 for its two x-planes):
+        // round k holds the k-th point of every class that has one.
+        constexpr int ORD_MAX = 1024;  // points per subproblem the reordering takes
+        __shared__ uint16_t ord[ORD_MAX];
+        __shared__ int rcnt[16];
+        const bool use_ord = cnt <= ORD_MAX;
+        if (use_ord) {
+            if (threadIdx.x < 16) rcnt[threadIdx.x] = 0;
+            __syncthreads();
+            constexpr int NI = ORD_MAX / 256;
+            int res[NI], rk[NI];
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const int t = threadIdx.x + 256 * i;
+                res[i] = rk[i] = 0;
+                if (t < cnt && (int)blockDim.x == 256) {
+                    const int64_t j = (int64_t)s0 + t;
+                    int lc[3];
+#pragma unroll
+                    for (int d = 0; d < 3; ++d) {
+                        int v = wrap1(i1s.p[d][j] + W / 2, g.n[d]);
+                        if ((unsigned)v >= (unsigned)g.n[d]) v = pmod(v, g.n[d]);
+                        lc[d] = v - b[d] * g.m[d];
+                    }
+                    res[i] = (((lc[0] * p1 + lc[1]) * p2 + lc[2]) >> 1) & 15;
+                    rk[i] = atomicAdd(&rcnt[res[i]], 1);
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const int t = threadIdx.x + 256 * i;
+                if (t < cnt && (int)blockDim.x == 256) {
+                    int slot = 0;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int n = rcnt[r];
+                        slot += min(n, rk[i]) + ((r < res[i] && n > rk[i]) ? 1 : 0);
+                    }
+                    ord[slot] = (uint16_t)t;
+                }
+            }
+            __syncthreads();
+        }
+        const bool ordered = use_ord && (int)blockDim.x == 256;
         // two lanes per point (a pair of neighbouring lanes): lane h of the
         // pair sums the x-planes a0 = h, h + 2, ...; one shuffle adds them
         for (int t = threadIdx.x; t < 2 * cnt; t += blockDim.x) {
-            const int pt = t >> 1, h = t & 1;
+            const int pt = ordered ? (int)ord[t >> 1] : (t >> 1), h = t & 1;
             const int64_t j = (int64_t)s0 + pt;
             int loc[3];
             bool ok = true;

@@ -138,7 +138,7 @@ class GpuT3Plan:
         stream = E.zstream_eligible(3, self.w2)
         self.bins_trg = (E.make_bins(3, self.w2, self.grid_shape, m=E.ZSTREAM_M) if stream else
                          E.make_bins(3, self.w2, self.grid_shape,
-                                     cell_bytes=E.INTERP_CELL_BYTES))
+                                     cell_bytes=E.INTERP_CELL_BYTES, npts=self.M))
         hd = [2.0 * PI / nf for nf in self.nf]
         hg = [hd[d] * self.gam[d] for d in range(3)]
         h2 = [2.0 * PI / n for n in self.n_up]
