@@ -95,12 +95,16 @@ def test_sort_matches_numpy_stable(case, oracle):
 
 @pytest.mark.parametrize("P,nbits,ncols", [(1, 5, 3), (4095, 7, 0), (4097, 12, 1),
                                              (300_001, 23, 3), (1_000_000, 32, 8),
-                                             (65_536, 16, 6), (4096 * 8192 + 3, 22, 1)])
+                                             (65_536, 16, 6), (4096 * 8192 + 3, 22, 1),
+                                             (50_001, 10, 2), (200_003, 17, 1),
+                                             (100_000, 25, 0), (8192 * 3, 11, 3)])
 def test_sort_pairs_payload(P, nbits, ncols):
     """Stable sort on the low nbits of each key, bits above nbits travelling
     with the key, and payload columns following their keys: against numpy's
-    stable argsort. The largest case has 4097 tiles of 8192 keys, so the
-    per-digit scan over the tiles runs its carry loop twice."""
+    stable argsort. Key widths from one pass (5, 7) to four (25, 32), with
+    a last pass of 1 to 8 bits. The 22-bit case has 4097 tiles of 8192
+    keys, so the per-digit scan over the tiles runs its carry loop twice;
+    the 11-bit case fills exactly three tiles."""
     from mlx_nufft_amd import _engine as E
 
     print(f"case sort_pairs P={P} nbits={nbits} ncols={ncols}", flush=True)
