@@ -53,12 +53,17 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--exec-only", action="store_true",
                     help="time execute() only (plan built once), for profiling")
-    ap.add_argument("--workload", choices=["t1", "t3-generic", "t1-1d", "t3"], default="t1",
+    ap.add_argument("--workload", default="t1",
+                    choices=["t1", "t3-generic", "t1-1d", "t1-2d-batch", "t2-2d-radial", "t3",
+                             "expi"],
                     help="t1: the north-star line (default). t3-generic: the reference's "
                          "type-3 Table I case (generic geometry, 1e6 sources on a 640^3 "
-                         "grid, M = N^2 targets), execute() only. t1-1d and t3: "
-                         "BASELINE.json configs[0] (1D type-1) and configs[4] (3D type-3), "
-                         "execute() only, for profiling their spread paths")
+                         "grid, M = N^2 targets), execute() only. t1-1d, t1-2d-batch, "
+                         "t2-2d-radial, t3 and expi: BASELINE.json configs[0] (1D type-1), "
+                         "configs[1] (2D type-1, execute_batch of 8 vectors), configs[2] "
+                         "(2D type-2 on radial spokes), configs[4] (3D type-3) and its expi "
+                         "leg (1e7 phases), the plan built once, for timing and profiling "
+                         "those paths")
     ap.add_argument("--t3-N", type=int, default=1024, choices=[512, 1024, 2048],
                     help="t3-generic: targets M = N^2")
     ap.add_argument("--copy-calibration", type=float, default=0.0, metavar="GIB",
@@ -196,10 +201,21 @@ def bench_t3(args):
 
 
 def bench_other(args):
-    """execute() of BASELINE.json configs[0] (1D type-1: M = 1e5, N = 4096,
-    eps 1e-6) or configs[4] (3D type-3: 1e6 sources in [-1, 1]^3, 1e6
-    targets in [-200, 200]^3, eps 1e-5), the plan built once and the
-    strengths resident in HBM; one JSON line with the time per execute."""
+    """One call of the path, the plan built once and its inputs resident in
+    HBM, for BASELINE.json's other configurations (their shapes,
+    distributions and default_rng(0) data):
+      t1-1d         configs[0]: 1D type-1, M = 1e5, N = 4096, eps 1e-6, execute();
+      t1-2d-batch   configs[1]: 2D type-1, M = 1e7 shared by 8 vectors,
+                    N = 1024^2, eps 1e-6, execute_batch();
+      t2-2d-radial  configs[2]: 2D type-2 on 512 spokes x 2048 samples
+                    (angles uniform in [0, pi), radii evenly spaced in
+                    [-pi, pi)), N = 1024^2, eps 1e-6, isign -1, execute();
+      t3            configs[4]: 3D type-3, 1e6 sources in [-1, 1]^3, 1e6
+                    targets in [-200, 200]^3, eps 1e-5, execute();
+      expi          configs[4]'s expi leg: 1e7 fp64 phases in [-1e6, 1e6].
+    One JSON line: the time per call (host clock over the timed calls) and,
+    where the plan times its stages with HIP events, one profiled call's
+    stages."""
     import numpy as np
     import torch
 
@@ -208,30 +224,69 @@ def bench_other(args):
 
     _lib.require_gpu()
     rng = np.random.default_rng(0)
-    if args.workload == "t1-1d":
+
+    def cplx(shape):
+        return (rng.standard_normal(shape) + 1j * rng.standard_normal(shape)).astype(np.complex64)
+
+    wl = args.workload
+    plan = None
+    if wl == "t1-1d":
         M = 100_000
         x = (rng.uniform(-np.pi, np.pi, M),)
         plan = mn.Type1PlanND(x, (4096,), eps=1e-6, isign=+1)
+        cd = torch.from_numpy(cplx(M)).cuda()
         cfg = {"workload": "1D type-1 M=1e5 N=4096 eps=1e-6 (BASELINE.json configs[0])"}
-    else:
+        run = lambda: plan.execute(cd, return_np=False)  # noqa: E731
+    elif wl == "t1-2d-batch":
+        M, B = 10_000_000, 8
+        x = tuple(rng.uniform(-np.pi, np.pi, M) for _ in range(2))
+        cd = torch.from_numpy(cplx((B, M))).cuda()
+        plan = mn.Type1PlanND(x, (1024, 1024), eps=1e-6, isign=+1)
+        cfg = {"workload": "2D type-1 M=1e7 x 8 vectors N=1024^2 eps=1e-6 "
+                           "(BASELINE.json configs[1]), execute_batch", "spread": plan.pts.kind}
+        run = lambda: plan.execute_batch(cd, return_np=False)  # noqa: E731
+    elif wl == "t2-2d-radial":
+        f = cplx((1024, 1024))
+        theta = rng.uniform(0.0, np.pi, 512)
+        r = np.linspace(-np.pi, np.pi, 2048, endpoint=False)
+        x = (np.outer(np.cos(theta), r).ravel(), np.outer(np.sin(theta), r).ravel())
+        plan = mn.Type2PlanND(x, (1024, 1024), eps=1e-6, isign=-1)
+        fd = torch.from_numpy(f).cuda()
+        cfg = {"workload": "2D type-2 radial 512 spokes x 2048 samples N=1024^2 eps=1e-6 "
+                           "(BASELINE.json configs[2])"}
+        run = lambda: plan.execute(fd, return_np=False)  # noqa: E731
+    elif wl == "t3":
         M = 1_000_000
         x = tuple(rng.uniform(-1.0, 1.0, M) for _ in range(3))
         s = tuple(rng.uniform(-200.0, 200.0, M) for _ in range(3))
         plan = mn.Type3Plan(x, s, eps=1e-5, isign=+1)
+        cd = torch.from_numpy(cplx(M)).cuda()
         cfg = {"workload": "3D type-3 1e6 x 1e6 eps=1e-5 (BASELINE.json configs[4])"}
-    c = (rng.standard_normal(M) + 1j * rng.standard_normal(M)).astype(np.complex64)
-    cd = torch.from_numpy(c).cuda()
+        run = lambda: plan.execute(cd, return_np=False)  # noqa: E731
+    else:
+        phi = torch.from_numpy(rng.uniform(-1e6, 1e6, 10_000_000)).cuda()
+        cfg = {"workload": "expi on 1e7 fp64 phases in [-1e6, 1e6] (BASELINE.json configs[4])"}
+        run = lambda: mn.expi(phi)  # noqa: E731
     for _ in range(args.warmup):
-        plan.execute(cd, return_np=False)
+        run()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        plan.execute(cd, return_np=False)
+        run()
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    print(json.dumps({"metric": "execute time", "value": ms, "unit": "ms", "n_gpus": 1,
-                      "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
-                      "higher_is_better": False, "config": cfg}))
+    out = {"metric": "execute time", "value": ms, "unit": "ms", "n_gpus": 1,
+           "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+           "higher_is_better": False, "config": cfg}
+    if wl == "t3":
+        _, st = plan.execute_profiled(cd)
+        out["stages_ms"] = {k: round(v * 1e3, 4) for k, v in st.items()}
+    elif plan is not None:
+        plan.profile = True
+        run()
+        out["stages_ms"] = {k: round(v, 4) for k, v in plan.last_profile.items()}
+        plan.profile = False
+    print(json.dumps(out))
 
 
 def main():
@@ -247,7 +302,7 @@ def main():
     if args.workload == "t3-generic":
         bench_t3(args)
         return
-    if args.workload in ("t1-1d", "t3"):
+    if args.workload != "t1":
         bench_other(args)
         return
     import numpy as np
