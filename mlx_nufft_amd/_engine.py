@@ -549,6 +549,16 @@ def spread_c128(pts, beta, c, grid128, pre=None):
                                    L.stream()), "spread_c128")
 
 
+def t3_tile_bins(w, n):
+    """Bins of the type-3 LDS-tile spread. With w <= 16 the matrix-core
+    kernel takes the tiles, so bins are 17 - w cells wide: padded tiles of 16
+    cells per dim (one 16 x 16 MFMA tile per x plane). MN_T3_TILE_MFMA=0
+    selects the LDS-atomic kernel and the LDS budget's bins instead."""
+    if w <= 16 and os.environ.get("MN_T3_TILE_MFMA", "") != "0":
+        return make_bins(3, w, n, m=[max(1, min(17 - w, int(k))) for k in n])
+    return make_bins(3, w, n, cell_bytes=SPREAD_CELL_BYTES)
+
+
 OWNER_M = 16   # owner-computes spread bins: 16^3 fp64 complex cells = 64 KB of LDS
 
 

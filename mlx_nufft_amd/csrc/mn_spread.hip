@@ -8,12 +8,16 @@
 // taps into LDS with ds_add_f64. On CDNA4 fp32 LDS atomics retire about one
 // lane every two clocks per CU, several times slower than fp64 ones, and the
 // fp64 tile also sums more accurately. After a barrier the tile is flushed
-// to the periodic fine grid with fp32 global atomics (skipping cells that
-// stayed zero). Workgroups are remapped so each XCD walks a contiguous run
-// of bins.
+// to the periodic fine grid with global atomics (fp32, or fp64 into a
+// complex128 grid), one component per lane so that an instruction's lanes
+// hit adjacent addresses, skipping components that stayed zero. Workgroups
+// are remapped so each XCD walks a contiguous run of bins. 3D fp64 tiles of
+// at most 16 cells per dim are accumulated on the matrix cores instead
+// (k_spread_tile_mfma).
 // ref: nd.py:492-579 (OD spread), nd.py:683-742 (batched), gpu_t3.py:565-591.
 #include "mn_common.h"
 
+#include <cstdlib>
 #include <type_traits>
 
 namespace mn {
@@ -205,7 +209,12 @@ __global__ __launch_bounds__(256) void k_spread_tiled(Geom g, float bl2e, float 
     const int o1 = DIM >= 2 ? b[1] * g.m[1] - W / 2 : 0;
     const int o2 = DIM >= 3 ? b[2] * g.m[2] - W / 2 : 0;
     const int64_t gsz = (int64_t)g.n[0] * g.n[1] * g.n[2];
-    for (int q = threadIdx.x; q < T; q += 256) {
+    // one component per thread: thread e adds component e % 2 (re, im) of
+    // cell e / 2, so consecutive lanes hit adjacent addresses (L2 atomics
+    // are paid per cache line; with re and im in one thread the lines of an
+    // instruction were half used)
+    for (int e = threadIdx.x; e < 2 * T; e += 256) {
+        const int q = e >> 1, comp = e & 1;
         const int q2 = q % p2, r12 = q / p2;
         const int q1 = r12 % p1, q0 = r12 / p1;
         const int g0 = wrap_tile(o0 + q0, g.n[0]);
@@ -213,20 +222,223 @@ __global__ __launch_bounds__(256) void k_spread_tiled(Geom g, float bl2e, float 
         const int g2 = DIM >= 3 ? wrap_tile(o2 + q2, g.n[2]) : 0;
         const int64_t cell = ((int64_t)g0 * g.n[1] + g1) * g.n[2] + g2;
         for (int v = 0; v < nvec; ++v) {
-            const double *tre = lds + (size_t)2 * T * v;
+            const double val = lds[(size_t)2 * T * v + (size_t)comp * T + q];
+            if (val == 0.0) continue;
             if constexpr (F64) {
-                const double re = tre[q], im = tre[T + q];
-                if (re == 0.0 && im == 0.0) continue;
-                double *dst = reinterpret_cast<double *>(grid) + 2 * cell;
-                unsafeAtomicAdd(dst, re);
-                unsafeAtomicAdd(dst + 1, im);
+                unsafeAtomicAdd(reinterpret_cast<double *>(grid) + 2 * cell + comp, val);
             } else {
-                const float re = (float)tre[q], im = (float)tre[T + q];
-                if (re == 0.0f && im == 0.0f) continue;
                 float *dst = reinterpret_cast<float *>(
                     reinterpret_cast<float2 *>(grid) + (BATCH ? (b0 + v) * gsz : 0) + cell);
-                unsafeAtomicAdd(dst, re);
-                unsafeAtomicAdd(dst + 1, im);
+                unsafeAtomicAdd(dst + comp, (float)val);
+            }
+        }
+    }
+}
+
+// 3D fp64 tile spread on the matrix cores (type-3 sources, complex128 grid),
+// for padded tiles of at most 16 cells per dim. Instead of one LDS atomic per
+// tap, the tile is accumulated by v_mfma_f64_16x16x4f64 outer products: for
+// each x plane of the tile, D[y][z] += sum over 4 points k of A[y][k] B[k][z]
+// with A = wx(x) wy(y) (exact in fp64: the weights are fp32) and
+// B = c_k wz(z) (the strength times its prephase, fp64, as the LDS-atomic
+// kernel forms it); the real and imaginary planes are two MFMAs sharing A.
+// Wave w of the four owns the x planes w, w + 4, w + 8 and w + 12: eight
+// 16x16 fp64 accumulators (4 planes, re and im) in registers.
+// Per batch of 64 points the workgroup writes each point's x and y weight
+// rows (16 cells, zero outside the footprint; the x row permuted so that a
+// wave's four planes are adjacent) and its two B rows (16 z cells, fp64),
+// one role per thread; then every wave sweeps the batch in K-steps of 4
+// points, skipping the MFMAs of a plane that none of the 4 points reaches
+// (the batch is taken in x-footprint order, so neighbouring points share
+// planes). After the last batch the accumulators are flushed to the grid
+// with fp64 atomics, re and im of a cell from adjacent lanes, skipping
+// zeros. Only the summation order differs from the LDS-atomic kernel.
+typedef double mn_v4d __attribute__((ext_vector_type(4)));
+constexpr int TM_NB = 64;            // points per batch
+constexpr int MN_SUB_MAX_ORDER = 1024;  // points per subproblem the x-order takes
+
+template <int W>
+__global__ __launch_bounds__(256) void k_spread_tile_mfma(Geom g, float bl2e, float inv_hw,
+                                                         int64_t nsub,
+                                                         const int32_t *__restrict__ info,
+                                                         const uint32_t *__restrict__ perm,
+                                                         CI3s i1s, CF3s frs,
+                                                         const float2 *__restrict__ c,
+                                                         const float2 *__restrict__ pre,
+                                                         double *__restrict__ grid) {
+    static_assert(W <= 16, "the footprint must fit a 16-cell tile");
+    __shared__ __align__(16) float xw[TM_NB][16];  // x cell x at (x & 3) * 4 + (x >> 2)
+    __shared__ __align__(16) float yw[TM_NB][16];
+    __shared__ __align__(16) double bre[TM_NB][16], bim[TM_NB][16];
+    __shared__ uint32_t xmask[TM_NB];  // planes reached by each point
+    __shared__ uint16_t ord[MN_SUB_MAX_ORDER];
+    __shared__ int xcnt[16];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int64_t sub = xcd_remap(blockIdx.x, nsub);
+    const int bin = info[3 * sub], s0 = info[3 * sub + 1], cnt = info[3 * sub + 2];
+    int b[3];
+    {
+        int rem = bin;
+#pragma unroll
+        for (int d = 2; d >= 0; --d) {
+            b[d] = rem % g.nb[d];
+            rem /= g.nb[d];
+        }
+    }
+    const int p0 = g.p[0], p1 = g.p[1], p2 = g.p[2];
+
+    // order of the subproblem's points: by the x cell of their first tap
+    // (a counting sort; stable), so that a K-step's 4 points reach few planes
+    const bool ordered = cnt <= MN_SUB_MAX_ORDER;
+    if (ordered) {
+        if (tid < 16) xcnt[tid] = 0;
+        __syncthreads();
+        constexpr int NI = MN_SUB_MAX_ORDER / 256;
+        int lx[NI], rk[NI];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int t = tid + 256 * i;
+            lx[i] = 0;
+            rk[i] = 0;
+            if (t < cnt) {
+                lx[i] = local_cell(i1s.p[0][(int64_t)s0 + t], W / 2, g.n[0], b[0], g.m[0]);
+                lx[i] = lx[i] < 0 ? 0 : lx[i];
+                rk[i] = atomicAdd(&xcnt[lx[i]], 1);
+            }
+        }
+        __syncthreads();
+        // ranks within a cell follow the atomic order, not the index order;
+        // any order within a cell keeps the planes reached the same
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int t = tid + 256 * i;
+            if (t < cnt) {
+                int base = 0;
+                for (int x = 0; x < lx[i]; ++x) base += xcnt[x];
+                ord[base + rk[i]] = (uint16_t)t;
+            }
+        }
+    }
+
+    mn_v4d are[4], aim[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        are[q] = mn_v4d{0.0, 0.0, 0.0, 0.0};
+        aim[q] = mn_v4d{0.0, 0.0, 0.0, 0.0};
+    }
+    const int pt_role = tid & 3, pslot = tid >> 2;
+    for (int bb = 0; bb < cnt; bb += TM_NB) {
+        const int nb = min(TM_NB, cnt - bb);
+        __syncthreads();  // the previous batch's K-steps are done with the tables
+        {
+            // prologue: point pslot of the batch, role pt_role (x row, y row,
+            // B re row, B im row); rows of absent points stay zero
+            const bool valid = pslot < nb;
+            int t = bb + pslot;
+            if (valid && ordered) t = ord[t];
+            const int64_t j = (int64_t)s0 + (valid ? t : 0);
+            const int d = pt_role < 2 ? pt_role : 2;
+            int loc = local_cell(i1s.p[d][j], W / 2, g.n[d], b[d], g.m[d]);
+            loc = loc < 0 ? 0 : loc;  // cannot happen for keys built by setpts
+            const float fr = frs.p[d][j];
+            float wt[W];
+#pragma unroll
+            for (int a = 0; a < W; ++a) wt[a] = es_weight_stable((float)a - fr, bl2e, inv_hw);
+            // each thread zeroes its row, then writes its taps over it (its
+            // own LDS accesses stay in order)
+            if (pt_role < 2) {
+                float *row = pt_role == 0 ? &xw[pslot][0] : &yw[pslot][0];
+                float4 *r4 = reinterpret_cast<float4 *>(row);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) r4[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (valid) {
+#pragma unroll
+                    for (int a = 0; a < W; ++a) {
+                        const int x = loc + a;
+                        row[pt_role == 0 ? (x & 3) * 4 + (x >> 2) : x] = wt[a];
+                    }
+                }
+                if (pt_role == 0) xmask[pslot] = valid ? (((1u << W) - 1u) << loc) : 0u;
+            } else {
+                // the strength times its prephase, in fp64 (as the LDS kernel)
+                double cv = 0.0;
+                if (valid) {
+                    const float2 c0 = c[perm[j]];
+                    double cx = c0.x, cy = c0.y;
+                    if (pre) {
+                        const float2 pv = pre[j];
+                        const double px = pv.x, py = pv.y;
+                        const double rx = cx * px - cy * py;
+                        cy = cx * py + cy * px;
+                        cx = rx;
+                    }
+                    cv = pt_role == 2 ? cx : cy;
+                }
+                double *row = pt_role == 2 ? &bre[pslot][0] : &bim[pslot][0];
+                double2 *r2 = reinterpret_cast<double2 *>(row);
+#pragma unroll
+                for (int q = 0; q < 8; ++q) r2[q] = make_double2(0.0, 0.0);
+                if (valid) {
+#pragma unroll
+                    for (int a = 0; a < W; ++a) row[loc + a] = cv * (double)wt[a];
+                }
+            }
+        }
+        __syncthreads();
+        // K-steps: lane (i, k) = (lane % 16, lane / 16) supplies A[y = i][k]
+        // and B[k][z = i] of point 4 s + k
+        const int i = lane & 15, k = lane >> 4;
+        for (int s = 0; s < (nb + 3) >> 2; ++s) {
+            const int pt = 4 * s + k;
+            const uint32_t reach = xmask[4 * s] | xmask[4 * s + 1] | xmask[4 * s + 2] |
+                                   xmask[4 * s + 3];
+            const float4 xv = *reinterpret_cast<const float4 *>(&xw[pt][4 * wv]);
+            const double yv = (double)yw[pt][i];
+            const double br = bre[pt][i], bi = bim[pt][i];
+            const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int x = wv + 4 * q;
+                if (x < p0 && ((reach >> x) & 1u)) {
+                    const double a = (double)xs[q] * yv;
+                    are[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, br, are[q], 0, 0, 0);
+                    aim[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, bi, aim[q], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+    // Flush. Lane l holds D[y = 4 r + l / 16][z = l % 16] in entry r (the
+    // layout of v_mfma_f64_16x16x4f64's result, checked on MI355X). The
+    // atomics go out in lane pairs: in half h, lane L adds component L % 2
+    // (re, im) of the cell that lane 32 h + L / 2 holds, so one instruction
+    // covers 32 whole cells, 512 contiguous bytes of a z-row pair. L2
+    // atomics are paid per cache line: this took the flush at cfg 5 from
+    // 0.46 to 0.16 ms against one lane per cell (re and im apart).
+    const int o0 = b[0] * g.m[0] - W / 2;
+    const int o1 = b[1] * g.m[1] - W / 2;
+    const int o2 = b[2] * g.m[2] - W / 2;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int x = wv + 4 * q;
+        if (x >= p0) continue;
+        const int g0 = wrap_tile(o0 + x, g.n[0]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int src = 32 * h + (lane >> 1);
+                const double vre = __shfl(are[q][r], src, 64);
+                const double vim = __shfl(aim[q][r], src, 64);
+                const double v = (lane & 1) ? vim : vre;
+                const int z = src & 15, y = 4 * r + (src >> 4);
+                if (z < p2 && y < p1 && v != 0.0) {
+                    const int g1 = wrap_tile(o1 + y, g.n[1]);
+                    const int g2 = wrap_tile(o2 + z, g.n[2]);
+                    unsafeAtomicAdd(grid + 2 * (((int64_t)g0 * g.n[1] + g1) * g.n[2] + g2) +
+                                        (lane & 1),
+                                    v);
+                }
             }
         }
     }
@@ -453,6 +665,13 @@ struct OwnerLaunch {
     }
 };
 
+// The fp64 3D tiles go through the matrix cores unless MN_T3_TILE_MFMA=0
+// (read at every launch, so that a test can compare both kernels).
+inline bool spread_tile_mfma() {
+    const char *e = std::getenv("MN_T3_TILE_MFMA");
+    return !(e && std::atoi(e) == 0);
+}
+
 template <int DIM, int W>
 struct SpreadLaunch {
     static int run(const SpreadArgs &a) {
@@ -467,6 +686,16 @@ struct SpreadLaunch {
             return MN_EINVAL;
         }
         if (a.nsub == 0) return MN_OK;
+        if constexpr (DIM == 3 && W <= 16) {
+            if (a.f64 && !batch && g.p[0] <= 16 && g.p[1] <= 16 && g.p[2] <= 16 &&
+                spread_tile_mfma()) {
+                k_spread_tile_mfma<W><<<(unsigned)a.nsub, 256, 0, a.s>>>(
+                    g, bl2e, inv_hw, a.nsub, a.info, a.perm, a.i1s, a.frs, a.c, a.pre,
+                    static_cast<double *>(a.grid));
+                MN_LAUNCH_CHECK("spread (matrix-core tiles)");
+                return MN_OK;
+            }
+        }
         auto kern = batch   ? k_spread_tiled<DIM, W, true, false>
                     : a.f64 ? k_spread_tiled<DIM, W, false, true>
                             : k_spread_tiled<DIM, W, false, false>;

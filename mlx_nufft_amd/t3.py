@@ -195,7 +195,7 @@ class GpuT3Plan:
         if self.spread_owner:
             self.bins_src = E.owner_bins(self.w, self.nf)
         else:
-            self.bins_src = E.make_bins(3, self.w, self.nf, cell_bytes=E.SPREAD_CELL_BYTES)
+            self.bins_src = E.t3_tile_bins(self.w, self.nf)
         self._hd = hd
         self._bf = None
         self._H = None

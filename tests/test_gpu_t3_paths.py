@@ -229,6 +229,62 @@ def test_spread_owner_equals_tiles(n, w, clustered, mn):
     assert L.lib().mn_spread_owner_c128 is not None
 
 
+@pytest.mark.parametrize("n,w,clustered,P", [
+    ((40, 36, 33), 9, False, 30_000),  # partial last bins (m = 8)
+    ((50, 48, 20), 8, True, 30_000),   # points packed at the periodic corner
+    ((16, 18, 17), 16, False, 5_000),  # w = 16: one-cell bins, tiles of 16
+    ((64, 64, 64), 2, False, 50_000),  # bins of 15
+    ((12, 30, 7), 6, True, 20_000),    # dims narrower than a bin (tiles under 16)
+    ((24, 24, 24), 9, True, 3_000),    # clustered: subproblems split at 1024 points
+])
+def test_spread_tile_mfma_equals_lds_tiles(n, w, clustered, P, mn, monkeypatch):
+    """The matrix-core fp64 tile spread against the LDS-atomic fp64 tile
+    spread on the same sorted points and bins (type-3 tile bins: padded tiles
+    of at most 16 cells), and against the owner-computes spread: three
+    independent fp64 accumulations of the same taps."""
+    from mlx_nufft_amd import _engine as E
+
+    print(f"case spread tile mfma n={n} w={w} clustered={clustered} P={P}", flush=True)
+    rng = np.random.default_rng(sum(n) * 7 + w)
+    beta = 2.3 * w
+    if clustered:
+        i1 = np.stack([(-w // 2 + rng.integers(-2, 3, P)) % k for k in n])
+    else:
+        i1 = np.stack([rng.integers(-w, k, P) for k in n])
+    fr = rng.uniform(0, 1, (3, P)).astype(np.float32)
+    c = torch.from_numpy((rng.standard_normal(P) + 1j * rng.standard_normal(P))
+                         .astype(np.complex64)).cuda()
+    pre = torch.from_numpy(np.exp(1j * rng.uniform(0, 6.3, P)).astype(np.complex64)).cuda()
+    i1d = torch.from_numpy(i1.astype(np.int32)).cuda()
+    frd = torch.from_numpy(fr).cuda()
+    bt = E.t3_tile_bins(w, n)
+    assert all(bt.m[d] + w - 1 <= 16 for d in range(3))
+    hw = w // 2
+    k = np.zeros(P, np.int64)
+    for d in range(3):
+        k = k * bt.nb[d] + ((i1[d] + hw) % n[d]) // bt.m[d]
+    pt = E.SortedPoints(bt, i1d, frd, torch.from_numpy(k.astype(np.int32)).cuda())
+    pre_s = pre[pt.perm.long()]
+    g_mfma = torch.full(n, complex(np.nan, np.nan), dtype=torch.complex128, device="cuda")
+    E.spread_c128(pt, beta, c, g_mfma, pre=pre_s)
+    monkeypatch.setenv("MN_T3_TILE_MFMA", "0")
+    g_lds = torch.full(n, complex(np.nan, np.nan), dtype=torch.complex128, device="cuda")
+    E.spread_c128(pt, beta, c, g_lds, pre=pre_s)
+    monkeypatch.delenv("MN_T3_TILE_MFMA")
+    bo = E.make_bins(3, w, n, m=[min(E.OWNER_M, kk) for kk in n])
+    kk = np.zeros(P, np.int64)
+    for d in range(3):
+        kk = kk * bo.nb[d] + ((i1[d] + hw) % n[d]) // bo.m[d]
+    po = E.SortedPoints(bo, i1d, frd, torch.from_numpy(kk.astype(np.int32)).cuda(), stream=True)
+    g_own = torch.empty(n, dtype=torch.complex128, device="cuda")
+    E.spread_owner_c128(po, beta, c, g_own, pre=pre[po.perm.long()])
+    a, b, o = g_mfma.cpu().numpy(), g_lds.cpu().numpy(), g_own.cpu().numpy()
+    assert np.isfinite(a).all() and np.isfinite(b).all()
+    scale = np.abs(b).max()
+    assert np.abs(a - b).max() / scale < 1e-13
+    assert np.abs(a - o).max() / scale < 1e-13
+
+
 def test_type3_owner_equals_tiles_spread(oracle, mn, monkeypatch):
     """Type-3 through each spread (forced), equal to within the c64 rounding."""
     print("case t3 owner vs tiles spread", flush=True)
