@@ -236,43 +236,48 @@ __global__ __launch_bounds__(256) void k_spread_tiled(Geom g, float bl2e, float 
 }
 
 // 3D fp64 tile spread on the matrix cores (type-3 sources, complex128 grid),
-// for padded tiles of at most 16 cells per dim. Instead of one LDS atomic per
-// tap, the tile is accumulated by v_mfma_f64_16x16x4f64 outer products: for
-// each x plane of the tile, D[y][z] += sum over 4 points k of A[y][k] B[k][z]
-// with A = wx(x) wy(y) (exact in fp64: the weights are fp32) and
-// B = c_k wz(z) (the strength times its prephase, fp64, as the LDS-atomic
-// kernel forms it); the real and imaginary planes are two MFMAs sharing A.
-// Wave w of the four owns the x planes w, w + 4, w + 8 and w + 12: eight
+// for padded tiles of at most 16 cells per dim. Instead of one LDS
+// atomic per tap, the tile is accumulated by v_mfma_f64_16x16x4f64 outer
+// products: for each x plane of the tile, D[y][z] += sum over 4 points k of
+// A[y][k] B[k][z] with A = wx(x) wy(y) (exact in fp64: the weights are fp32)
+// and B = c_k wz(z) (the strength times its prephase, fp64, as the
+// LDS-atomic kernel forms it); the real and imaginary planes are two MFMAs
+// sharing A. Wave w of the four owns the x planes w + 4 q, q < 4: eight
 // 16x16 fp64 accumulators (4 planes, re and im) in registers.
-// Per batch of 64 points the workgroup writes each point's x and y weight
-// rows (16 cells, zero outside the footprint; the x row permuted so that a
+// Per batch of 64 points the workgroup writes each point's x and y
+// weight rows (zero outside the footprint; the x row permuted so that a
 // wave's four planes are adjacent) and its two B rows (16 z cells, fp64),
 // one role per thread; then every wave sweeps the batch in K-steps of 4
 // points, skipping the MFMAs of a plane that none of the 4 points reaches
-// (the batch is taken in x-footprint order, so neighbouring points share
-// planes). After the last batch the accumulators are flushed to the grid
-// with fp64 atomics, re and im of a cell from adjacent lanes, skipping
+// (the subproblem is taken in x-footprint order, so neighbouring points
+// share planes). After the last batch the accumulators are flushed to the
+// grid with fp64 atomics, re and im of a cell from adjacent lanes, skipping
 // zeros. Only the summation order differs from the LDS-atomic kernel.
+// (Tiles of 32 x 16 x 16 cells with eight waves, bins of 33 - w along x,
+// measured 5 % slower at cfg 5: 0.477 against 0.456 ms.)
 typedef double mn_v4d __attribute__((ext_vector_type(4)));
-constexpr int TM_NB = 64;            // points per batch
 constexpr int MN_SUB_MAX_ORDER = 1024;  // points per subproblem the x-order takes
 
 template <int W>
-__global__ __launch_bounds__(256) void k_spread_tile_mfma(Geom g, float bl2e, float inv_hw,
-                                                         int64_t nsub,
-                                                         const int32_t *__restrict__ info,
-                                                         const uint32_t *__restrict__ perm,
-                                                         CI3s i1s, CF3s frs,
-                                                         const float2 *__restrict__ c,
-                                                         const float2 *__restrict__ pre,
-                                                         double *__restrict__ grid) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_spread_tile_mfma(Geom g, float bl2e, float inv_hw,
+                                                              int64_t nsub,
+                                                              const int32_t *__restrict__ info,
+                                                              const uint32_t *__restrict__ perm,
+                                                              CI3s i1s, CF3s frs,
+                                                              const float2 *__restrict__ c,
+                                                              const float2 *__restrict__ pre,
+                                                              double *__restrict__ grid) {
     static_assert(W <= 16, "the footprint must fit a 16-cell tile");
-    __shared__ __align__(16) float xw[TM_NB][16];  // x cell x at (x & 3) * 4 + (x >> 2)
-    __shared__ __align__(16) float yw[TM_NB][16];
-    __shared__ __align__(16) double bre[TM_NB][16], bim[TM_NB][16];
-    __shared__ uint32_t xmask[TM_NB];  // planes reached by each point
+    constexpr int NWV = 4;        // waves
+    constexpr int NT = 64 * NWV;  // threads
+    constexpr int PX = 4 * NWV;   // x planes
+    constexpr int NB = NT / 4;    // points per batch (four roles each)
+    __shared__ __align__(16) float xw[NB][PX];  // x cell x at (x % NWV) * 4 + x / NWV
+    __shared__ __align__(16) float yw[NB][16];
+    __shared__ __align__(16) double bre[NB][16], bim[NB][16];
+    __shared__ uint32_t xmask[NB];  // planes reached by each point
     __shared__ uint16_t ord[MN_SUB_MAX_ORDER];
-    __shared__ int xcnt[16];
+    __shared__ int xcnt[PX];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int64_t sub = xcd_remap(blockIdx.x, nsub);
     const int bin = info[3 * sub], s0 = info[3 * sub + 1], cnt = info[3 * sub + 2];
@@ -287,17 +292,18 @@ __global__ __launch_bounds__(256) void k_spread_tile_mfma(Geom g, float bl2e, fl
     }
     const int p0 = g.p[0], p1 = g.p[1], p2 = g.p[2];
 
-    // order of the subproblem's points: by the x cell of their first tap
-    // (a counting sort; stable), so that a K-step's 4 points reach few planes
+    // order of the subproblem's points: by the x cell of their first tap (a
+    // counting sort in LDS; within a cell, the atomics' order), so that a
+    // K-step's 4 points reach few planes
     const bool ordered = cnt <= MN_SUB_MAX_ORDER;
     if (ordered) {
-        if (tid < 16) xcnt[tid] = 0;
+        if (tid < PX) xcnt[tid] = 0;
         __syncthreads();
-        constexpr int NI = MN_SUB_MAX_ORDER / 256;
+        constexpr int NI = MN_SUB_MAX_ORDER / NT;
         int lx[NI], rk[NI];
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
-            const int t = tid + 256 * i;
+            const int t = tid + NT * i;
             lx[i] = 0;
             rk[i] = 0;
             if (t < cnt) {
@@ -311,7 +317,7 @@ __global__ __launch_bounds__(256) void k_spread_tile_mfma(Geom g, float bl2e, fl
         // any order within a cell keeps the planes reached the same
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
-            const int t = tid + 256 * i;
+            const int t = tid + NT * i;
             if (t < cnt) {
                 int base = 0;
                 for (int x = 0; x < lx[i]; ++x) base += xcnt[x];
@@ -327,8 +333,8 @@ __global__ __launch_bounds__(256) void k_spread_tile_mfma(Geom g, float bl2e, fl
         aim[q] = mn_v4d{0.0, 0.0, 0.0, 0.0};
     }
     const int pt_role = tid & 3, pslot = tid >> 2;
-    for (int bb = 0; bb < cnt; bb += TM_NB) {
-        const int nb = min(TM_NB, cnt - bb);
+    for (int bb = 0; bb < cnt; bb += NB) {
+        const int nb = min(NB, cnt - bb);
         __syncthreads();  // the previous batch's K-steps are done with the tables
         {
             // prologue: point pslot of the batch, role pt_role (x row, y row,
@@ -346,18 +352,29 @@ __global__ __launch_bounds__(256) void k_spread_tile_mfma(Geom g, float bl2e, fl
             for (int a = 0; a < W; ++a) wt[a] = es_weight_stable((float)a - fr, bl2e, inv_hw);
             // each thread zeroes its row, then writes its taps over it (its
             // own LDS accesses stay in order)
-            if (pt_role < 2) {
-                float *row = pt_role == 0 ? &xw[pslot][0] : &yw[pslot][0];
+            if (pt_role == 0) {
+                float *row = &xw[pslot][0];
+                float4 *r4 = reinterpret_cast<float4 *>(row);
+#pragma unroll
+                for (int q = 0; q < PX / 4; ++q) r4[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (valid) {
+#pragma unroll
+                    for (int a = 0; a < W; ++a) {
+                        const int x = loc + a;
+                        row[(x % NWV) * 4 + x / NWV] = wt[a];
+                    }
+                }
+            } else if (pt_role == 1) {
+                float *row = &yw[pslot][0];
                 float4 *r4 = reinterpret_cast<float4 *>(row);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) r4[q] = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (valid) {
 #pragma unroll
-                    for (int a = 0; a < W; ++a) {
-                        const int x = loc + a;
-                        row[pt_role == 0 ? (x & 3) * 4 + (x >> 2) : x] = wt[a];
-                    }
+                    for (int a = 0; a < W; ++a) row[loc + a] = wt[a];
                 }
+            }
+            if (pt_role < 2) {
                 if (pt_role == 0) xmask[pslot] = valid ? (((1u << W) - 1u) << loc) : 0u;
             } else {
                 // the strength times its prephase, in fp64 (as the LDS kernel)
@@ -398,7 +415,7 @@ __global__ __launch_bounds__(256) void k_spread_tile_mfma(Geom g, float bl2e, fl
             const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const int x = wv + 4 * q;
+                const int x = wv + NWV * q;
                 if (x < p0 && ((reach >> x) & 1u)) {
                     const double a = (double)xs[q] * yv;
                     are[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, br, are[q], 0, 0, 0);
@@ -420,7 +437,7 @@ __global__ __launch_bounds__(256) void k_spread_tile_mfma(Geom g, float bl2e, fl
     const int o2 = b[2] * g.m[2] - W / 2;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const int x = wv + 4 * q;
+        const int x = wv + NWV * q;
         if (x >= p0) continue;
         const int g0 = wrap_tile(o0 + x, g.n[0]);
 #pragma unroll
