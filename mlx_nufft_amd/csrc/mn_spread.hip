@@ -476,6 +476,57 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 constexpr int OWN_THREADS = 256;
 constexpr int OWN_MAXQ = 4;  // reaching bins per dim
 
+// The point ranges that can reach owner bin (lo, cnt), for lane `lane` of
+// the wave that calls it: every lane finds the reaching bins of each dim (a
+// little arithmetic), then lane r takes combination r of them: its start in
+// the sorted points (st[r]) and, by a wave scan of the range sizes, the
+// number of reaching points before it (pf[r]; pf[64] = all of them).
+template <int W>
+__device__ __forceinline__ void owner_ranges(const Geom &g, const int (&lo)[3],
+                                             const int (&cnt)[3],
+                                             const int32_t *__restrict__ bstart, int tid,
+                                             int *pf, int *st) {
+    int qs[3][OWN_MAXQ], nq[3];
+#pragma unroll
+    for (int d = 0; d < 3; ++d) {
+        const int n = g.n[d], m = g.m[d];
+        const int len = cnt[d] + W - 1;
+        nq[d] = 0;
+        if (len >= n) {
+            for (int q = 0; q < g.nb[d] && q < OWN_MAXQ; ++q) qs[d][nq[d]++] = q;
+        } else {
+            int cell = pmod(lo[d] - (W - 1 - W / 2), n), left = len;
+            while (left > 0 && nq[d] < OWN_MAXQ) {
+                const int q = cell / m;
+                bool dup = false;
+                for (int k = 0; k < nq[d]; ++k) dup = dup || qs[d][k] == q;
+                if (!dup) qs[d][nq[d]++] = q;
+                const int end = min(q * m + m, n);
+                left -= end - cell;
+                cell = end == n ? 0 : end;
+            }
+        }
+    }
+    const int ncomb = nq[0] * nq[1] * nq[2];
+    int s0 = 0, len = 0;
+    if (tid < ncomb) {
+        const int i2 = tid % nq[2], i01 = tid / nq[2];
+        const int i1 = i01 % nq[1], i0 = i01 / nq[1];
+        const int64_t nbr = ((int64_t)qs[0][i0] * g.nb[1] + qs[1][i1]) * g.nb[2] + qs[2][i2];
+        s0 = bstart[nbr];
+        len = bstart[nbr + 1] - s0;
+    }
+    int incl = len;
+#pragma unroll
+    for (int k = 1; k < 64; k <<= 1) {
+        const int v = __shfl_up(incl, k, 64);
+        incl += tid >= k ? v : 0;
+    }
+    pf[tid] = incl - len;
+    st[tid] = s0;
+    if (tid == 63) pf[64] = incl;
+}
+
 template <int W>
 __global__ __launch_bounds__(OWN_THREADS) void k_spread_owner(
     Geom g, float bl2e, float inv_hw, int64_t nbins, const int32_t *__restrict__ bstart,
@@ -502,50 +553,7 @@ __global__ __launch_bounds__(OWN_THREADS) void k_spread_owner(
     }
     const int T = cnt[0] * cnt[1] * cnt[2];
     double *tre = own, *tim = own + T;
-    if (tid < 64) {
-        // every lane of wave 0 finds the reaching bins of each dim (a little
-        // arithmetic), then lane r takes combination r: its point range, and
-        // a wave scan of the range sizes
-        int qs[3][OWN_MAXQ], nq[3];
-#pragma unroll
-        for (int d = 0; d < 3; ++d) {
-            const int n = g.n[d], m = g.m[d];
-            const int len = cnt[d] + W - 1;
-            nq[d] = 0;
-            if (len >= n) {
-                for (int q = 0; q < g.nb[d] && q < OWN_MAXQ; ++q) qs[d][nq[d]++] = q;
-            } else {
-                int cell = pmod(lo[d] - (W - 1 - W / 2), n), left = len;
-                while (left > 0 && nq[d] < OWN_MAXQ) {
-                    const int q = cell / m;
-                    bool dup = false;
-                    for (int k = 0; k < nq[d]; ++k) dup = dup || qs[d][k] == q;
-                    if (!dup) qs[d][nq[d]++] = q;
-                    const int end = min(q * m + m, n);
-                    left -= end - cell;
-                    cell = end == n ? 0 : end;
-                }
-            }
-        }
-        const int ncomb = nq[0] * nq[1] * nq[2];
-        int s0 = 0, len = 0;
-        if (tid < ncomb) {
-            const int i2 = tid % nq[2], i01 = tid / nq[2];
-            const int i1 = i01 % nq[1], i0 = i01 / nq[1];
-            const int64_t nbr = ((int64_t)qs[0][i0] * g.nb[1] + qs[1][i1]) * g.nb[2] + qs[2][i2];
-            s0 = bstart[nbr];
-            len = bstart[nbr + 1] - s0;
-        }
-        int incl = len;
-#pragma unroll
-        for (int k = 1; k < 64; k <<= 1) {
-            const int v = __shfl_up(incl, k, 64);
-            incl += tid >= k ? v : 0;
-        }
-        pf[tid] = incl - len;
-        st[tid] = s0;
-        if (tid == 63) pf[64] = incl;
-    }
+    if (tid < 64) owner_ranges<W>(g, lo, cnt, bstart, tid, pf, st);
     __syncthreads();
     const int tot = pf[OWN_MAXQ * OWN_MAXQ * OWN_MAXQ];
     if (tot == 0) {  // no point reaches the bin: zeros straight to the grid
@@ -637,6 +645,230 @@ __global__ __launch_bounds__(OWN_THREADS) void k_spread_owner(
     }
 }
 
+// Owner-computes spread on the matrix cores, for owner bins of at most 16
+// cells per dim: the bin is accumulated like a k_spread_tile_mfma tile (a
+// wave per four x planes, v_mfma_f64_16x16x4f64 outer products of the x-y
+// weight products with the strength-weighted z rows, planes that none of a
+// K-step's points reaches skipped), from the points of every reaching bin
+// whose footprint meets the bin (compacted per chunk of reaching points, in
+// order of the first x cell they reach), each tap kept only when it lands
+// inside the bin. The bin is then stored with plain writes, zeros included,
+// so that every cell is written by one workgroup.
+template <int W>
+__global__ __launch_bounds__(OWN_THREADS) __attribute__((amdgpu_waves_per_eu(3))) void
+k_spread_owner_mfma(Geom g, float bl2e, float inv_hw, int64_t nbins,
+                    const int32_t *__restrict__ bstart, const uint32_t *__restrict__ perm,
+                    CI3s i1s, CF3s frs, const float2 *__restrict__ c,
+                    const float2 *__restrict__ pre, double2 *__restrict__ grid) {
+    static_assert(OWN_THREADS == 256, "four waves");
+    constexpr int NB = 64;  // points per batch (four roles each)
+    __shared__ __align__(16) float xw[NB][16];  // x cell x at (x & 3) * 4 + (x >> 2)
+    __shared__ __align__(16) float yw[NB][16];
+    __shared__ __align__(16) double bre[NB][16], bim[NB][16];
+    __shared__ uint32_t xmask[NB];
+    __shared__ int32_t ordj[MN_SUB_MAX_ORDER];  // sorted index of each ordered point
+    __shared__ int xcnt[16];
+    __shared__ int pf[OWN_MAXQ * OWN_MAXQ * OWN_MAXQ + 1];
+    __shared__ int st[OWN_MAXQ * OWN_MAXQ * OWN_MAXQ];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int64_t bin = xcd_remap(blockIdx.x, nbins);
+    int b[3], lo[3], cnt[3];
+    {
+        int64_t rem = bin;
+#pragma unroll
+        for (int d = 2; d >= 0; --d) {
+            b[d] = (int)(rem % g.nb[d]);
+            rem /= g.nb[d];
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < 3; ++d) {
+        lo[d] = b[d] * g.m[d];
+        cnt[d] = min(g.m[d], g.n[d] - lo[d]);
+    }
+    if (tid < 64) owner_ranges<W>(g, lo, cnt, bstart, tid, pf, st);
+    __syncthreads();
+    const int tot = pf[OWN_MAXQ * OWN_MAXQ * OWN_MAXQ];
+    // sorted index of reaching point t: its range q (pf[q] <= t < pf[q + 1],
+    // a binary search) and its place in that range
+    auto point = [&](int t) __attribute__((always_inline)) {
+        int qa = 0, qb = OWN_MAXQ * OWN_MAXQ * OWN_MAXQ;
+        while (qb - qa > 1) {
+            const int mid = (qa + qb) >> 1;
+            if (pf[mid] <= t) qa = mid;
+            else qb = mid;
+        }
+        return st[qa] + (t - pf[qa]);
+    };
+    // whether the footprint of a point whose first tap along d is i1 meets
+    // the bin along d, and its first in-bin cell (taps land at
+    // (i1 + a - lo) mod n; a footprint entering from below starts at 0)
+    auto meets = [&](int i1, int d) __attribute__((always_inline)) {
+        const int v = pmod(i1 - lo[d], g.n[d]);
+        return v < cnt[d] || v + W - 1 >= g.n[d];
+    };
+    auto first_x = [&](int i1) __attribute__((always_inline)) {
+        const int v = pmod(i1 - lo[0], g.n[0]);
+        return v < cnt[0] ? v : 0;
+    };
+
+    mn_v4d are[4], aim[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        are[q] = mn_v4d{0.0, 0.0, 0.0, 0.0};
+        aim[q] = mn_v4d{0.0, 0.0, 0.0, 0.0};
+    }
+    const int pt_role = tid & 3, pslot = tid >> 2;
+    // Chunks of up to MN_SUB_MAX_ORDER reaching points: most of a reaching
+    // bin's points do not touch this bin, so each chunk is first compacted
+    // to the points whose footprint meets the bin in all three dims, in
+    // order of their first x cell (a counting sort in LDS)
+    for (int c0 = 0; c0 < tot; c0 += MN_SUB_MAX_ORDER) {
+        const int cn = min(MN_SUB_MAX_ORDER, tot - c0);
+        __syncthreads();  // the previous chunk's batches are done with ordj
+        if (tid < 16) xcnt[tid] = 0;
+        __syncthreads();
+        constexpr int NI = MN_SUB_MAX_ORDER / OWN_THREADS;
+        int lx[NI], rk[NI], jj[NI];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int t = tid + OWN_THREADS * i;
+            lx[i] = -1;
+            rk[i] = 0;
+            jj[i] = 0;
+            if (t < cn) {
+                jj[i] = point(c0 + t);
+                const int ix = i1s.p[0][jj[i]];
+                if (meets(ix, 0) && meets(i1s.p[1][jj[i]], 1) && meets(i1s.p[2][jj[i]], 2)) {
+                    lx[i] = first_x(ix);
+                    rk[i] = atomicAdd(&xcnt[lx[i]], 1);
+                }
+            }
+        }
+        __syncthreads();
+        int nkeep = 0;
+#pragma unroll
+        for (int x = 0; x < 16; ++x) nkeep += xcnt[x];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            if (lx[i] >= 0) {
+                int base = 0;
+                for (int x = 0; x < lx[i]; ++x) base += xcnt[x];
+                ordj[base + rk[i]] = jj[i];
+            }
+        }
+        for (int bb = 0; bb < nkeep; bb += NB) {
+            const int nb = min(NB, nkeep - bb);
+            __syncthreads();  // ordj is written; the previous K-steps are done
+            {
+                const bool valid = pslot < nb;
+                const int64_t j = valid ? ordj[bb + pslot] : 0;
+                const int d = pt_role < 2 ? pt_role : 2;
+                const int n = g.n[d];
+                // tap a lands at in-bin cell (a - a0) mod n; kept when below cnt
+                const int a0 = pmod(lo[d] - i1s.p[d][j], n);
+                const float fr = frs.p[d][j];
+                int v[W];
+                float wt[W];
+#pragma unroll
+                for (int a = 0; a < W; ++a) {
+                    int va = a - a0;
+                    va += va < 0 ? n : 0;
+                    v[a] = va;
+                    wt[a] = es_weight_stable((float)a - fr, bl2e, inv_hw);
+                }
+                if (pt_role == 0) {
+                    float *row = &xw[pslot][0];
+                    float4 *r4 = reinterpret_cast<float4 *>(row);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) r4[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    uint32_t mask = 0;
+                    if (valid) {
+#pragma unroll
+                        for (int a = 0; a < W; ++a)
+                            if (v[a] < cnt[0]) {
+                                row[(v[a] & 3) * 4 + (v[a] >> 2)] = wt[a];
+                                mask |= 1u << v[a];
+                            }
+                    }
+                    xmask[pslot] = mask;
+                } else if (pt_role == 1) {
+                    float *row = &yw[pslot][0];
+                    float4 *r4 = reinterpret_cast<float4 *>(row);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) r4[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (valid) {
+#pragma unroll
+                        for (int a = 0; a < W; ++a)
+                            if (v[a] < cnt[1]) row[v[a]] = wt[a];
+                    }
+                } else {
+                    double cv = 0.0;
+                    if (valid) {
+                        const float2 c0v = c[perm[j]];
+                        double cx = c0v.x, cy = c0v.y;
+                        if (pre) {
+                            const float2 pv = pre[j];
+                            const double px = pv.x, py = pv.y;
+                            const double rx = cx * px - cy * py;
+                            cy = cx * py + cy * px;
+                            cx = rx;
+                        }
+                        cv = pt_role == 2 ? cx : cy;
+                    }
+                    double *row = pt_role == 2 ? &bre[pslot][0] : &bim[pslot][0];
+                    double2 *r2 = reinterpret_cast<double2 *>(row);
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) r2[q] = make_double2(0.0, 0.0);
+                    if (valid) {
+#pragma unroll
+                        for (int a = 0; a < W; ++a)
+                            if (v[a] < cnt[2]) row[v[a]] = cv * (double)wt[a];
+                    }
+                }
+            }
+            __syncthreads();
+            const int i = lane & 15, k = lane >> 4;
+            for (int s = 0; s < (nb + 3) >> 2; ++s) {
+                const int pt = 4 * s + k;
+                const uint32_t reach = xmask[4 * s] | xmask[4 * s + 1] | xmask[4 * s + 2] |
+                                       xmask[4 * s + 3];
+                const float4 xv = *reinterpret_cast<const float4 *>(&xw[pt][4 * wv]);
+                const double yv = (double)yw[pt][i];
+                const double br = bre[pt][i], bi = bim[pt][i];
+                const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int x = wv + 4 * q;
+                    if (x < cnt[0] && ((reach >> x) & 1u)) {
+                        const double a = (double)xs[q] * yv;
+                        are[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, br, are[q], 0, 0, 0);
+                        aim[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, bi, aim[q], 0, 0, 0);
+                    }
+                }
+            }
+        }
+    }
+
+    // store: lane l holds D[y = 4 r + l / 16][z = l % 16] in entry r; 16
+    // lanes write one 256-byte z-row
+    const int64_t n12 = (int64_t)g.n[1] * g.n[2];
+    const int z = lane & 15;
+    if (z >= cnt[2]) return;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int x = wv + 4 * q;
+        if (x >= cnt[0]) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int y = 4 * r + (lane >> 4);
+            if (y >= cnt[1]) continue;
+            grid[(int64_t)(lo[0] + x) * n12 + (int64_t)(lo[1] + y) * g.n[2] + lo[2] + z] =
+                make_double2(are[q][r], aim[q][r]);
+        }
+    }
+}
+
 struct OwnerArgs {
     const mn_bins *g;
     float beta;
@@ -648,6 +880,13 @@ struct OwnerArgs {
     double2 *grid;
     hipStream_t s;
 };
+
+// Owner bins of at most 16 cells per dim go through the matrix cores unless
+// MN_T3_OWNER_MFMA=0 (read at every launch).
+inline bool spread_owner_mfma() {
+    const char *e = std::getenv("MN_T3_OWNER_MFMA");
+    return !(e && std::atoi(e) == 0);
+}
 
 template <int DIM, int W>
 struct OwnerLaunch {
@@ -670,6 +909,14 @@ struct OwnerLaunch {
                     set_error("spread_owner: bins must be at least w - 1 cells wide");
                     return MN_EINVAL;
                 }
+            // (a footprint longer than an axis would land twice on a cell)
+            if (g.m[0] <= 16 && g.m[1] <= 16 && g.m[2] <= 16 && g.n[0] >= W && g.n[1] >= W &&
+                g.n[2] >= W && spread_owner_mfma()) {
+                k_spread_owner_mfma<W><<<(unsigned)nb, OWN_THREADS, 0, a.s>>>(
+                    g, bl2e, inv_hw, nb, a.bstart, a.perm, a.i1s, a.frs, a.c, a.pre, a.grid);
+                MN_LAUNCH_CHECK("spread_owner (matrix cores)");
+                return MN_OK;
+            }
             auto kern = k_spread_owner<W>;
             if (lds > 60000)  // with the static range tables, past the 64 KB default
                 MN_HIP_CHECK(hipFuncSetAttribute(

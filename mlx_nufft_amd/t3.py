@@ -178,20 +178,25 @@ class GpuT3Plan:
                         for v in self.decs]
         self.dev_dec64 = [torch.from_numpy(np.ascontiguousarray(v, dtype=np.float64))
                           .to(self.device) for v in self.decs]
-        # spread: the LDS-tile spread (zero fill, atomic halo flushes) or the
+        # spread: the tile spread (zero fill, atomic halo flushes) or the
         # owner-computes spread (bins of about 16^3 cells, each cell written
-        # once). Measured on MI355X, the owner spread wins when taps per fine
-        # cell (P w^3 / prod nf) lie in about [0.3, 20] on grids without a
-        # thin axis: the tiles' halo flushes dominate there (486^3, 1e6
-        # points: 3.1 against 8.1 ms); sparser grids favour the tiles' fast
-        # zero fill, denser ones their single visit per point (180^3, 1e6
-        # points: 1.2 against 4.2 ms). MN_T3_SPREAD=owner|tiles forces one.
+        # once), both accumulated on the matrix cores where their bins allow.
+        # Measured on MI355X with uniform points (owner / tiles, ms), the
+        # owner spread wins when taps per fine cell (P w^3 / prod nf) lie in
+        # about [0.12, 45] on grids without a thin axis: 486^3 with 1e4 / 1e5
+        # / 1e6 points 0.57 / 0.66 / 1.35 against 0.47 / 1.21 / 4.24; 300^3,
+        # 1e6 (27 taps) 1.27 against 2.08; 240^3 (53) 1.47 against 1.20;
+        # 180^3 (125) 1.69 against 0.56. Sparser grids favour the tiles' fast
+        # zero fill, denser ones their single visit per point; thin slabs
+        # (an axis of at most 18 cells) keep the LDS owner kernel and favour
+        # the tiles (5760^2 x 18, 4e4 points: 4.9 against 2.3).
+        # MN_T3_SPREAD=owner|tiles forces one.
         taps = float(self.P) * self.w ** 3 / float(np.prod([float(n) for n in self.nf]))
         mode = os.environ.get("MN_T3_SPREAD")
         if mode not in (None, "owner", "tiles"):
             raise ValueError(f"MN_T3_SPREAD must be 'owner' or 'tiles', not {mode!r}")
         self.spread_owner = (mode == "owner" or
-                             (mode is None and 0.3 <= taps <= 20.0 and min(self.nf) > 18))
+                             (mode is None and 0.12 <= taps <= 45.0 and min(self.nf) > 18))
         if self.spread_owner:
             self.bins_src = E.owner_bins(self.w, self.nf)
         else:

@@ -240,8 +240,10 @@ def test_spread_owner_equals_tiles(n, w, clustered, mn):
 def test_spread_tile_mfma_equals_lds_tiles(n, w, clustered, P, mn, monkeypatch):
     """The matrix-core fp64 tile spread against the LDS-atomic fp64 tile
     spread on the same sorted points and bins (type-3 tile bins: padded tiles
-    of at most 16 cells), and against the owner-computes spread: three
-    independent fp64 accumulations of the same taps."""
+    of at most 16 cells), and against the owner-computes spread on its
+    matrix-core and LDS-atomic kernels (owner bins of at most 16 cells):
+    four independent fp64 accumulations of the same taps. The owner grids
+    start as NaN, so a cell the owner kernel left unwritten fails."""
     from mlx_nufft_amd import _engine as E
 
     print(f"case spread tile mfma n={n} w={w} clustered={clustered} P={P}", flush=True)
@@ -276,13 +278,20 @@ def test_spread_tile_mfma_equals_lds_tiles(n, w, clustered, P, mn, monkeypatch):
     for d in range(3):
         kk = kk * bo.nb[d] + ((i1[d] + hw) % n[d]) // bo.m[d]
     po = E.SortedPoints(bo, i1d, frd, torch.from_numpy(kk.astype(np.int32)).cuda(), stream=True)
-    g_own = torch.empty(n, dtype=torch.complex128, device="cuda")
+    g_own = torch.full(n, complex(np.nan, np.nan), dtype=torch.complex128, device="cuda")
     E.spread_owner_c128(po, beta, c, g_own, pre=pre[po.perm.long()])
-    a, b, o = g_mfma.cpu().numpy(), g_lds.cpu().numpy(), g_own.cpu().numpy()
+    monkeypatch.setenv("MN_T3_OWNER_MFMA", "0")
+    g_own_lds = torch.full(n, complex(np.nan, np.nan), dtype=torch.complex128, device="cuda")
+    E.spread_owner_c128(po, beta, c, g_own_lds, pre=pre[po.perm.long()])
+    monkeypatch.delenv("MN_T3_OWNER_MFMA")
+    a, b = g_mfma.cpu().numpy(), g_lds.cpu().numpy()
+    o, ol = g_own.cpu().numpy(), g_own_lds.cpu().numpy()
     assert np.isfinite(a).all() and np.isfinite(b).all()
+    assert np.isfinite(o).all() and np.isfinite(ol).all()
     scale = np.abs(b).max()
     assert np.abs(a - b).max() / scale < 1e-13
     assert np.abs(a - o).max() / scale < 1e-13
+    assert np.abs(o - ol).max() / scale < 1e-13
 
 
 def test_type3_owner_equals_tiles_spread(oracle, mn, monkeypatch):
