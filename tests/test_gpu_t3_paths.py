@@ -229,15 +229,16 @@ def test_spread_owner_equals_tiles(n, w, clustered, mn):
     assert L.lib().mn_spread_owner_c128 is not None
 
 
-@pytest.mark.parametrize("n,w,clustered,P", [
-    ((40, 36, 33), 9, False, 30_000),  # partial last bins (m = 8)
-    ((50, 48, 20), 8, True, 30_000),   # points packed at the periodic corner
-    ((16, 18, 17), 16, False, 5_000),  # w = 16: one-cell bins, tiles of 16
-    ((64, 64, 64), 2, False, 50_000),  # bins of 15
-    ((12, 30, 7), 6, True, 20_000),    # dims narrower than a bin (tiles under 16)
-    ((24, 24, 24), 9, True, 3_000),    # clustered: subproblems split at 1024 points
+@pytest.mark.parametrize("n,w,clustered,P,use_pre", [
+    ((40, 36, 33), 9, False, 30_000, True),  # partial last bins (m = 8)
+    ((50, 48, 20), 8, True, 30_000, True),   # points packed at the periodic corner
+    ((16, 18, 17), 16, False, 5_000, True),  # w = 16: one-cell bins, tiles of 16
+    ((64, 64, 64), 2, False, 50_000, True),  # bins of 15
+    ((12, 30, 7), 6, True, 20_000, True),    # dims narrower than a bin (tiles under 16)
+    ((24, 24, 24), 9, True, 3_000, True),    # clustered: subproblems split at 1024 points
+    ((32, 40, 24), 7, False, 20_000, False),  # no prephase (a NULL pre pointer)
 ])
-def test_spread_tile_mfma_equals_lds_tiles(n, w, clustered, P, mn, monkeypatch):
+def test_spread_tile_mfma_equals_lds_tiles(n, w, clustered, P, use_pre, mn, monkeypatch):
     """The matrix-core fp64 tile spread against the LDS-atomic fp64 tile
     spread on the same sorted points and bins (type-3 tile bins: padded tiles
     of at most 16 cells), and against the owner-computes spread on its
@@ -246,7 +247,8 @@ def test_spread_tile_mfma_equals_lds_tiles(n, w, clustered, P, mn, monkeypatch):
     start as NaN, so a cell the owner kernel left unwritten fails."""
     from mlx_nufft_amd import _engine as E
 
-    print(f"case spread tile mfma n={n} w={w} clustered={clustered} P={P}", flush=True)
+    print(f"case spread tile mfma n={n} w={w} clustered={clustered} P={P} pre={use_pre}",
+          flush=True)
     rng = np.random.default_rng(sum(n) * 7 + w)
     beta = 2.3 * w
     if clustered:
@@ -266,7 +268,7 @@ def test_spread_tile_mfma_equals_lds_tiles(n, w, clustered, P, mn, monkeypatch):
     for d in range(3):
         k = k * bt.nb[d] + ((i1[d] + hw) % n[d]) // bt.m[d]
     pt = E.SortedPoints(bt, i1d, frd, torch.from_numpy(k.astype(np.int32)).cuda())
-    pre_s = pre[pt.perm.long()]
+    pre_s = pre[pt.perm.long()] if use_pre else None
     g_mfma = torch.full(n, complex(np.nan, np.nan), dtype=torch.complex128, device="cuda")
     E.spread_c128(pt, beta, c, g_mfma, pre=pre_s)
     monkeypatch.setenv("MN_T3_TILE_MFMA", "0")
@@ -279,10 +281,11 @@ def test_spread_tile_mfma_equals_lds_tiles(n, w, clustered, P, mn, monkeypatch):
         kk = kk * bo.nb[d] + ((i1[d] + hw) % n[d]) // bo.m[d]
     po = E.SortedPoints(bo, i1d, frd, torch.from_numpy(kk.astype(np.int32)).cuda(), stream=True)
     g_own = torch.full(n, complex(np.nan, np.nan), dtype=torch.complex128, device="cuda")
-    E.spread_owner_c128(po, beta, c, g_own, pre=pre[po.perm.long()])
+    pre_o = pre[po.perm.long()] if use_pre else None
+    E.spread_owner_c128(po, beta, c, g_own, pre=pre_o)
     monkeypatch.setenv("MN_T3_OWNER_MFMA", "0")
     g_own_lds = torch.full(n, complex(np.nan, np.nan), dtype=torch.complex128, device="cuda")
-    E.spread_owner_c128(po, beta, c, g_own_lds, pre=pre[po.perm.long()])
+    E.spread_owner_c128(po, beta, c, g_own_lds, pre=pre_o)
     monkeypatch.delenv("MN_T3_OWNER_MFMA")
     a, b = g_mfma.cpu().numpy(), g_lds.cpu().numpy()
     o, ol = g_own.cpu().numpy(), g_own_lds.cpu().numpy()
