@@ -259,14 +259,11 @@ typedef double mn_v4d __attribute__((ext_vector_type(4)));
 constexpr int MN_SUB_MAX_ORDER = 1024;  // points per subproblem the x-order takes
 
 template <int W>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_spread_tile_mfma(Geom g, float bl2e, float inv_hw,
-                                                              int64_t nsub,
-                                                              const int32_t *__restrict__ info,
-                                                              const uint32_t *__restrict__ perm,
-                                                              CI3s i1s, CF3s frs,
-                                                              const float2 *__restrict__ c,
-                                                              const float2 *__restrict__ pre,
-                                                              double *__restrict__ grid) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void
+k_spread_tile_mfma(Geom g, float bl2e, float inv_hw, int64_t nsub,
+                   const int32_t *__restrict__ info, const uint32_t *__restrict__ perm, CI3s i1s,
+                   CF3s frs, const float2 *__restrict__ c, const float2 *__restrict__ pre,
+                   double *__restrict__ grid) {
     static_assert(W <= 16, "the footprint must fit a 16-cell tile");
     constexpr int NWV = 4;        // waves
     constexpr int NT = 64 * NWV;  // threads
