@@ -557,13 +557,16 @@ int mn_round_c64(int64_t n, const void *in, void *out, mn_stream_t stream);
  * Batched zero-padding line FFTs in double precision: one axis pass of the
  * type-3 inner-grid transform, with that axis's pad and deconvolution fused.
  * `in` is complex128 of shape (A, nin, B), C order; `out` has shape
- * (A, n, B), or (n, A*B) with the line index fastest when lines_last != 0,
- * complex128, or complex64 when out_c64 != 0. Line (a, b) is
+ * (A, n, B) when out_layout == 0, (n, A*B) with the line index fastest when
+ * out_layout == 1, or (A*B, n) with each line's n values contiguous when
+ * out_layout == 2; complex128, or complex64 when out_c64 != 0. Line (a, b) is
  * in[a, :, b]: element m, times dec[m] (fp64, length nin; NULL for none),
  * sits at FFT index (m - nin/2) mod n with zeros elsewhere, and
  *   out[a, r, b] = sum_p x[p] exp(isign 2 pi i p r / n)   (unnormalised).
  * Three passes (z, y, x) of bf (nf0 nf1 nf2) give
- * FFT(pad(bf * dec0 x dec1 x dec2)) on n_up without a padded fp64 grid.
+ * FFT(pad(bf * dec0 x dec1 x dec2)) on n_up without a padded fp64 grid
+ * (the x pass in layout 2 writes it as (n1, n2, n0), x innermost, in whole
+ * lines instead of runs of B's low power of two).
  * n must be 2^a 3^b 5^c in [2, 8192] (mn_fft64_lines_supported), 1 <= nin <=
  * n, A*B < 2^31, and in and out must not overlap. The twiddle tables are
  * cached per (device, n, sign) and released by mn_fft_cache_clear.
@@ -573,7 +576,7 @@ int mn_round_c64(int64_t n, const void *in, void *out, mn_stream_t stream);
  */
 int mn_fft64_lines_supported(int64_t n);
 int mn_fft64_lines(int64_t A, int64_t nin, int64_t B, int64_t n, int isign, const void *in,
-                   const double *dec, void *out, int out_c64, int lines_last,
+                   const double *dec, void *out, int out_c64, int out_layout,
                    mn_stream_t stream);
 
 /*

@@ -719,10 +719,15 @@ def fft64_lines_supported(n):
     return bool(L.lib().mn_fft64_lines_supported(int(n)))
 
 
-def fft64_lines(A, nin, B, n, isign, src128, dec64, out, lines_last=False):
+FFT64_LAYOUTS = {"anb": 0, "lines_last": 1, "lines_first": 2}
+
+
+def fft64_lines(A, nin, B, n, isign, src128, dec64, out, layout="anb"):
     """One axis pass of the zero-padding fp64 line FFT: src128 (A, nin, B)
-    complex128 -> out (A, n, B), or (n, A*B) with lines_last, complex128 or
-    complex64 (by out's dtype)."""
+    complex128 -> out (A, n, B) ("anb"), (n, A*B) with the line index fastest
+    ("lines_last") or (A*B, n) with each line contiguous ("lines_first"),
+    complex128 or complex64 (by out's dtype)."""
+    _require(layout in FFT64_LAYOUTS, f"fft64_lines: layout must be one of {tuple(FFT64_LAYOUTS)}")
     c64 = out.dtype == torch.complex64
     _require(src128.dtype == torch.complex128 and src128.numel() >= A * nin * B,
              f"fft64_lines: src must be complex128 with at least {A * nin * B} elements")
@@ -732,7 +737,7 @@ def fft64_lines(A, nin, B, n, isign, src128, dec64, out, lines_last=False):
              f"fft64_lines: dec must be float64 with at least {nin} elements")
     L.check(L.lib().mn_fft64_lines(int(A), int(nin), int(B), int(n), int(isign), L.ptr(src128),
                                    None if dec64 is None else L.ptr(dec64), L.ptr(out), int(c64),
-                                   int(bool(lines_last)), L.stream()), "fft64_lines")
+                                   FFT64_LAYOUTS[layout], L.stream()), "fft64_lines")
 
 
 def transpose_c128(Bt, R, C, src, out):

@@ -445,10 +445,11 @@ int mn_fft64_lines_supported(int64_t n) {
 }
 
 int mn_fft64_lines(int64_t A, int64_t nin, int64_t B, int64_t n, int isign, const void *in,
-                   const double *dec, void *out, int out_c64, int lines_last,
+                   const double *dec, void *out, int out_c64, int out_layout,
                    mn_stream_t stream) {
     clear_error();
     MN_REQUIRE(in && out, "fft64_lines: NULL input or output");
+    MN_REQUIRE(out_layout >= 0 && out_layout <= 2, "fft64_lines: out_layout must be 0, 1 or 2");
     MN_REQUIRE(in != out, "fft64_lines: input and output must not alias");
     MN_REQUIRE(A >= 1 && B >= 1, "fft64_lines: A and B must be >= 1");
     MN_REQUIRE(mn_fft64_lines_supported(n), "fft64_lines: n must be 2^a 3^b 5^c in [2, 8192]");
@@ -475,8 +476,9 @@ int mn_fft64_lines(int64_t A, int64_t nin, int64_t B, int64_t n, int isign, cons
     const bool longl = n > 4096;
     const int vals = longl ? 8192 : 4096;
     int lti = 0;
-    // output line stride: B, or all lines when the line index runs fastest
-    const int64_t Bo = lines_last ? A * B : B;
+    // output line stride: B (layout 0), all lines when the line index runs
+    // fastest (1), or 1 when each line's values are contiguous (2)
+    const int64_t Bo = out_layout == 1 ? A * B : (out_layout == 2 ? 1 : B);
     int bpow = B > 1 ? __builtin_ctzll((unsigned long long)B) : 30;
     if (Bo > 1) bpow = min(bpow, (int)__builtin_ctzll((unsigned long long)Bo));
     while (lti < bpow && (int64_t)(1 << (lti + 1)) <= nlines &&

@@ -20,8 +20,9 @@ padded fp64 grid; this is the role of the reference's slab mode
 FFTs), generalised to every axis. Axes longer than 8192 or not 5-smooth
 fall back to pad + rocFFT. When an x or y line is long (> 1365 points), the
 passes run in reversed axis order with one transpose, so every long line is
-read contiguously, and the grid comes out as (n2, n1, n0); the targets are
-then set up with their axes reversed. MI355X holds every grid the reference
+read contiguously, and the grid comes out as (n2, n1, n0); otherwise the x
+pass stores each x line whole and the grid comes out as (n1, n2, n0). The
+targets are set up with their axes in the grid's order. MI355X holds every grid the reference
 handles in HBM, so there is no slab switch.
 """
 
@@ -131,7 +132,9 @@ class GpuT3Plan:
         self.fft_rev = (self.fft_lines and max(nu[0], nu[1]) > 1365 and nu[2] <= 65535
                         and (nf[0] + 31) // 32 <= 65535 and nu[2] * nf[0] < 2**31
                         and nu[2] * nu[1] < 2**31)
-        ax = [2, 1, 0] if self.fft_rev else [0, 1, 2]   # grid axis k holds axis ax[k]
+        # grid axis k holds axis ax[k]: the forward-order x pass writes whole
+        # lines, x innermost, (n1, n2, n0)
+        ax = [2, 1, 0] if self.fft_rev else ([1, 2, 0] if self.fft_lines else [0, 1, 2])
         self.grid_shape = [nu[a] for a in ax]
 
         # ---- targets: rescale, post factor, bin sort (device fp64) ----------
@@ -276,7 +279,7 @@ class GpuT3Plan:
                 # z lines -> (n2, nf0, nf1); y lines -> (n2, nf0, n1); transpose
                 # -> (n2, n1, nf0); x lines -> H (n2, n1, n0)
                 E.fft64_lines(nf[0] * nf[1], nf[2], 1, nu[2], self.isign, bf, d[2], T1,
-                              lines_last=True)
+                              layout="lines_last")
                 E.fft64_lines(nu[2] * nf[0], nf[1], 1, nu[1], self.isign, T1, d[1], T2)
                 E.transpose_c128(nu[2], nf[0], nu[1], T2, T3)
                 E.fft64_lines(nu[2] * nu[1], nf[0], 1, nu[0], self.isign, T3, d[0], H)
@@ -284,9 +287,14 @@ class GpuT3Plan:
         if self.fft_lines:
             T1, T2 = self._T
             with tm("fft"):
+                # z lines -> (nf0, nf1, n2); y lines -> (nf0, n1, n2); x lines
+                # -> H (n1, n2, n0), each x line stored whole: 2.31 against
+                # 2.55 ms for the x pass at 640^3 when the strided x lines
+                # were stored in place (runs of 4 complex64 values)
                 E.fft64_lines(nf[0] * nf[1], nf[2], 1, nu[2], self.isign, bf, d[2], T1)
                 E.fft64_lines(nf[0], nf[1], nu[2], nu[1], self.isign, T1, d[1], T2)
-                E.fft64_lines(1, nf[0], nu[1] * nu[2], nu[0], self.isign, T2, d[0], H)
+                E.fft64_lines(1, nf[0], nu[1] * nu[2], nu[0], self.isign, T2, d[0], H,
+                              layout="lines_first")
             return
         with tm("pad+deconv"):
             E.pad_deconv_c128(self.n_up, self.nf, bf, d, H64)
