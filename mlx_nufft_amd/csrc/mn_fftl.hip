@@ -41,11 +41,13 @@ namespace mn {
 namespace {
 
 constexpr int FL_NMAX = 8192;   // longest line: 128 KB of LDS
+constexpr int FL_WIDE = 5120;   // values of an unpadded strided tile (80 KB)
 constexpr int FL_MAXST = 16;
 
 // ti = 2^lti lines per tile, stored element-major in LDS (value p of line l
 // at p*ts + l, ts = ti + 1 for ti > 1 so that radix strides do not map the
-// lanes of a wave onto the same banks).
+// lanes of a wave onto the same banks; ts = ti for the unpadded tiles of
+// 8 or more strided lines, see mn_fft64_lines).
 struct FlPlan {
     int n, nin, lti, ts, nst;
     float rn, rnin;           // 1/n, 1/nin
@@ -484,8 +486,21 @@ int mn_fft64_lines(int64_t A, int64_t nin, int64_t B, int64_t n, int isign, cons
     while (lti < bpow && (int64_t)(1 << (lti + 1)) <= nlines &&
            n * ((1 << (lti + 1)) + 1) <= vals)
         ++lti;
+    // Strided lines (B > 1) read ti contiguous values per element. When a
+    // tile without the pad column, of up to FL_WIDE values (80 KB: two
+    // workgroups still share a CU), holds twice the lines, and at least 8,
+    // take it: a 16-lane LDS access then spans at most two butterflies, so
+    // conflicts stay rare. Measured on MI355X at 640^3 (type-3 Table I): 8
+    // lines per tile, 128-byte reads, took the three passes from 5.60 to
+    // 5.15 ms against 4 padded lines (51 KB, three workgroups per CU).
+    bool wide = false;
+    if (!longl && B > 1 && lti >= 2 && lti < bpow && (int64_t(2) << lti) <= nlines &&
+        n * (int64_t(2) << lti) <= FL_WIDE) {
+        ++lti;
+        wide = true;
+    }
     p.lti = lti;
-    p.ts = lti > 0 ? (1 << lti) + 1 : 1;
+    p.ts = wide ? (1 << lti) : (lti > 0 ? (1 << lti) + 1 : 1);
     const int ntiles = (nlines + (1 << lti) - 1) >> lti;
     hipStream_t s = as_stream(stream);
     const int S = isign >= 0 ? 1 : -1;
@@ -513,7 +528,10 @@ int mn_fft64_lines(int64_t A, int64_t nin, int64_t B, int64_t n, int isign, cons
     using K = void (*)(const double2 *, void *, const double *, const double2 *, int, int, int,
                        int, FlPlan);
     K kern;
-    if (longl)
+    if (wide)
+        kern = S > 0 ? (out_c64 ? k_fft64_lines<1, true, 512, FL_WIDE> : k_fft64_lines<1, false, 512, FL_WIDE>)
+                     : (out_c64 ? k_fft64_lines<-1, true, 512, FL_WIDE> : k_fft64_lines<-1, false, 512, FL_WIDE>);
+    else if (longl)
         kern = S > 0 ? (out_c64 ? k_fft64_lines<1, true, 1024, 8192> : k_fft64_lines<1, false, 1024, 8192>)
                      : (out_c64 ? k_fft64_lines<-1, true, 1024, 8192> : k_fft64_lines<-1, false, 1024, 8192>);
     else

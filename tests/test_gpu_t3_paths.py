@@ -44,6 +44,10 @@ CASES = [  # (A, nin, B, n)
     (5, 13, 1, 16), (3, 40, 9, 64), (2, 25, 6, 30), (1, 180, 17, 240), (9, 486, 1, 640),
     (1, 639, 8, 640), (3, 625, 2, 625), (2, 729, 3, 729), (1, 5760, 3, 7200),
     (2, 8192, 1, 8192), (1, 4001, 2, 4096), (300, 7, 1, 12), (1, 90, 1000, 120),
+    # unpadded tiles of strided lines: 8 (n = 640, 512, 486), 16 (n = 320,
+    # 256) and 32 (n = 160) lines
+    (2, 486, 16, 640), (1, 400, 64, 512), (3, 480, 8, 486), (2, 300, 32, 320),
+    (1, 200, 64, 256), (2, 150, 64, 160),
 ]
 
 
