@@ -32,8 +32,7 @@ namespace mn {
 namespace {
 
 typedef float fp2 __attribute__((ext_vector_type(2)));
-constexpr int FP_THREADS = 256;          // contiguous lines
-constexpr int FP_THREADS_STRIDED = 512;  // strided lines (see fp_ti_shift)
+constexpr int FP_THREADS = 512;  // threads per workgroup (see fp_ti_shift)
 constexpr int FP_ELEMS = 8192;  // complex values per workgroup tile (64 KB)
 
 __device__ __forceinline__ float2 cadd(float2 a, float2 b) { return make_float2(a.x + b.x, a.y + b.y); }
@@ -155,15 +154,15 @@ __device__ __forceinline__ int mode_of(int p, int M, int hM) {
 
 // Middle Stockham stage of radix R (LDS to LDS); Ns = product of the radices
 // of the earlier stages; tw[m] = exp(S 2 pi i m / N).
-template <int N, int TI, int R, int S, int NT>
+template <int N, int TI, int R, int S>
 __device__ __forceinline__ void stage(float2 *buf, const float2 *tw, int Ns) {
     constexpr int NJ = N / R, NB = NJ * TI;
-    constexpr int MB = (NB + NT - 1) / NT;
+    constexpr int MB = (NB + FP_THREADS - 1) / FP_THREADS;
     float2 v[MB][R];
     const int tstep = N / (Ns * R);
 #pragma unroll
     for (int m = 0; m < MB; ++m) {
-        const int b = threadIdx.x + m * NT;
+        const int b = threadIdx.x + m * FP_THREADS;
         if (b < NB) {
             const int t = b % TI, j = b / TI, k = j & (Ns - 1);
 #pragma unroll
@@ -176,7 +175,7 @@ __device__ __forceinline__ void stage(float2 *buf, const float2 *tw, int Ns) {
     __syncthreads();
 #pragma unroll
     for (int m = 0; m < MB; ++m) {
-        const int b = threadIdx.x + m * NT;
+        const int b = threadIdx.x + m * FP_THREADS;
         if (b < NB) {
             const int t = b % TI, j = b / TI, k = j & (Ns - 1);
             const int base = (j - k) * R + k;
@@ -192,8 +191,8 @@ __device__ __forceinline__ void stage(float2 *buf, const float2 *tw, int Ns) {
 // The first radix-8 stage reads its inputs straight from global memory and
 // the last stage writes its outputs straight back; LDS carries the stages
 // in between.
-template <int LOGN, int TI, int S, bool PRUNE_OUT, int NT>
-__global__ __launch_bounds__(NT) void k_fft_axis(const float2 *__restrict__ in,
+template <int LOGN, int TI, int S, bool PRUNE_OUT>
+__global__ __launch_bounds__(FP_THREADS) void k_fft_axis(const float2 *__restrict__ in,
                                                          float2 *__restrict__ out, AxisArgs a) {
     constexpr int N = 1 << LOGN;
     constexpr int N8 = LOGN / 3, REM = LOGN % 3;
@@ -206,7 +205,7 @@ __global__ __launch_bounds__(NT) void k_fft_axis(const float2 *__restrict__ in,
     const int64_t ntile = (a.nlines + TI - 1) / TI;
     const int64_t line0 = xcd_remap(blockIdx.x, ntile) * TI;
     const bool contig = a.inner == 1;  // the lines are contiguous rows
-    for (int m = tid; m < N; m += NT) {
+    for (int m = tid; m < N; m += FP_THREADS) {
         double sn, cs;
         sincospi(2.0 * (double)m / (double)N, &sn, &cs);
         tw[m] = make_float2((float)cs, (float)(S * sn));
@@ -221,11 +220,11 @@ __global__ __launch_bounds__(NT) void k_fft_axis(const float2 *__restrict__ in,
 
     // ---- first stage: radix 8, Ns = 1, inputs from global memory ----
     {
-        constexpr int NJ = N / 8, NB = NJ * TI, MB = (NB + NT - 1) / NT;
+        constexpr int NJ = N / 8, NB = NJ * TI, MB = (NB + FP_THREADS - 1) / FP_THREADS;
         float2 v[MB][8];
 #pragma unroll
         for (int m = 0; m < MB; ++m) {
-            const int b = tid + m * NT;
+            const int b = tid + m * FP_THREADS;
             int t = 0, j = 0;
             bfly_of<TI, NJ>(b, contig, t, j);
             const int64_t lb = b < NB ? lbi[t] : -1;
@@ -250,7 +249,7 @@ __global__ __launch_bounds__(NT) void k_fft_axis(const float2 *__restrict__ in,
         }
 #pragma unroll
         for (int m = 0; m < MB; ++m) {
-            const int b = tid + m * NT;
+            const int b = tid + m * FP_THREADS;
             if (b < NB) {
                 int t, j;
                 bfly_of<TI, NJ>(b, contig, t, j);
@@ -266,16 +265,16 @@ __global__ __launch_bounds__(NT) void k_fft_axis(const float2 *__restrict__ in,
     int Ns = 8;
 #pragma unroll
     for (int s = 1; s < (REM == 0 ? N8 - 1 : N8); ++s) {
-        stage<N, TI, 8, S, NT>(buf, tw, Ns);
+        stage<N, TI, 8, S>(buf, tw, Ns);
         Ns *= 8;
     }
 
     // ---- last stage: radix RL, Ns = N / RL, outputs to global memory ----
     {
-        constexpr int NJ = N / RL, NB = NJ * TI, MB = (NB + NT - 1) / NT;
+        constexpr int NJ = N / RL, NB = NJ * TI, MB = (NB + FP_THREADS - 1) / FP_THREADS;
 #pragma unroll
         for (int m = 0; m < MB; ++m) {
-            const int b = tid + m * NT;
+            const int b = tid + m * FP_THREADS;
             if (b < NB) {
                 int t, j;
                 bfly_of<TI, NJ>(b, contig, t, j);
@@ -320,38 +319,31 @@ int launch_axis_ti(bool prune_out, int isign, const float2 *in, float2 *out, con
         return MN_EINVAL;
     }
     const dim3 grid((unsigned)ntile);
-    if (a.inner != 1) {  // strided lines: FP_THREADS_STRIDED threads
-        if (prune_out) {
-            if (isign > 0) k_fft_axis<LOGN, TI, 1, true, FP_THREADS_STRIDED><<<grid, FP_THREADS_STRIDED, 0, s>>>(in, out, a);
-            else k_fft_axis<LOGN, TI, -1, true, FP_THREADS_STRIDED><<<grid, FP_THREADS_STRIDED, 0, s>>>(in, out, a);
-        } else {
-            if (isign > 0) k_fft_axis<LOGN, TI, 1, false, FP_THREADS_STRIDED><<<grid, FP_THREADS_STRIDED, 0, s>>>(in, out, a);
-            else k_fft_axis<LOGN, TI, -1, false, FP_THREADS_STRIDED><<<grid, FP_THREADS_STRIDED, 0, s>>>(in, out, a);
-        }
-    } else if (prune_out) {
-        if (isign > 0) k_fft_axis<LOGN, TI, 1, true, FP_THREADS><<<grid, FP_THREADS, 0, s>>>(in, out, a);
-        else k_fft_axis<LOGN, TI, -1, true, FP_THREADS><<<grid, FP_THREADS, 0, s>>>(in, out, a);
+    if (prune_out) {
+        if (isign > 0) k_fft_axis<LOGN, TI, 1, true><<<grid, FP_THREADS, 0, s>>>(in, out, a);
+        else k_fft_axis<LOGN, TI, -1, true><<<grid, FP_THREADS, 0, s>>>(in, out, a);
     } else {
-        if (isign > 0) k_fft_axis<LOGN, TI, 1, false, FP_THREADS><<<grid, FP_THREADS, 0, s>>>(in, out, a);
-        else k_fft_axis<LOGN, TI, -1, false, FP_THREADS><<<grid, FP_THREADS, 0, s>>>(in, out, a);
+        if (isign > 0) k_fft_axis<LOGN, TI, 1, false><<<grid, FP_THREADS, 0, s>>>(in, out, a);
+        else k_fft_axis<LOGN, TI, -1, false><<<grid, FP_THREADS, 0, s>>>(in, out, a);
     }
     MN_LAUNCH_CHECK("fft axis");
     return MN_OK;
 }
 
-// Lines per workgroup: fp_ti(LOGN) fills 64 KB of LDS. Measured on MI355X
-// at 512^3, a quarter of that for contiguous lines (the last axis) runs
-// fastest with 256 threads, and for strided ones half, with 512 threads:
-// the three type-1 passes (crop) took 0.565 ms against 0.587 with 256
-// threads (and 0.588 with all 16 lines), the type-2 passes (pad) 0.660
-// against 0.711 with a quarter at 256 threads (0.77 with a quarter at
-// 512); the 2D batched passes of 2048^2 x 8 0.208 against 0.22 ms. More
-// resident waves per CU keep more loads in flight.
+// Lines per workgroup: fp_ti(LOGN) fills 64 KB of LDS; half of that, with
+// 512 threads, runs fastest on MI355X. At 512^3 the type-1 passes (crop)
+// took 0.556 ms, against 0.587 with 256 threads, a quarter tile for the
+// contiguous lines and half for the strided ones (0.588 with all 16 lines
+// on the strided ones), and the type-2 passes (pad) 0.627 ms against 0.711
+// with 256 threads and quarter tiles; a quarter tile at 512 threads took
+// 0.59 and 0.74 ms, an eighth 0.72 and 0.97. The 2D batched passes of
+// 2048^2 x 8: 0.208 against 0.22 ms. More resident waves per CU keep more
+// loads in flight.
 // MN_FFT_TI_SHIFT / MN_FFT_TI_SHIFT_STRIDED override the shifts (tuning).
 int fp_ti_shift(bool contig) {
     static const int vc = [] {
         const char *e = getenv("MN_FFT_TI_SHIFT");
-        return e ? atoi(e) : 2;
+        return e ? atoi(e) : 1;
     }();
     static const int vs = [] {
         const char *e = getenv("MN_FFT_TI_SHIFT_STRIDED");
