@@ -47,7 +47,7 @@ constexpr int FL_MAXST = 16;
 // ti = 2^lti lines per tile, stored element-major in LDS (value p of line l
 // at p*ts + l, ts = ti + 1 for ti > 1 so that radix strides do not map the
 // lanes of a wave onto the same banks; ts = ti for the unpadded tiles of
-// 8 or more strided lines, see mn_fft64_lines).
+// 8 or more lines, see mn_fft64_lines).
 struct FlPlan {
     int n, nin, lti, ts, nst;
     float rn, rnin;           // 1/n, 1/nin
@@ -486,15 +486,18 @@ int mn_fft64_lines(int64_t A, int64_t nin, int64_t B, int64_t n, int isign, cons
     while (lti < bpow && (int64_t)(1 << (lti + 1)) <= nlines &&
            n * ((1 << (lti + 1)) + 1) <= vals)
         ++lti;
-    // Strided lines (B > 1) read ti contiguous values per element. When a
-    // tile without the pad column, of up to FL_WIDE values (80 KB: two
-    // workgroups still share a CU), holds twice the lines, and at least 8,
-    // take it: a 16-lane LDS access then spans at most two butterflies, so
-    // conflicts stay rare. Measured on MI355X at 640^3 (type-3 Table I): 8
-    // lines per tile, 128-byte reads, took the three passes from 5.60 to
-    // 5.15 ms against 4 padded lines (51 KB, three workgroups per CU).
+    // A tile without the pad column, of up to FL_WIDE values (80 KB: two
+    // workgroups still share a CU), is taken when it holds twice the lines,
+    // and at least 8: strided lines (B > 1) then read 2 ti contiguous values
+    // per element. A 16-lane LDS access of the stages spans at most two
+    // butterflies, so their conflicts stay rare; the fill and drain of
+    // contiguous lines, which walk one line per 16 lanes, conflict, and
+    // still come out ahead. Measured on MI355X at 640^3 (type-3 Table I,
+    // 8 lines per tile instead of 4 padded ones at three workgroups per
+    // CU): the strided passes took the transform from 5.60 to 5.15 ms, the
+    // contiguous z pass then from 5.12 to 5.01 ms.
     bool wide = false;
-    if (!longl && B > 1 && lti >= 2 && lti < bpow && (int64_t(2) << lti) <= nlines &&
+    if (!longl && lti >= 2 && lti < bpow && (int64_t(2) << lti) <= nlines &&
         n * (int64_t(2) << lti) <= FL_WIDE) {
         ++lti;
         wide = true;
