@@ -12,9 +12,11 @@ then K steps between torch.cuda.synchronize() calls; HIP events recorded on
 the launch stream inside the timed region give per-step min/median/max and
 per-stage times (read after the region, so nothing synchronises inside it).
 The Python heap is collected and frozen (gc.collect + gc.freeze) before the
-region: a full collection of the interpreter's import-time objects costs
+warm-up: a full collection of the interpreter's import-time objects costs
 30-40 ms of host time, and one that lands inside the region leaves the GPU
-idle for that long. Collector pauses inside the region are reported.
+idle for that long (one just before the region left the GPU at lower
+clocks for its first steps). The warm-up records the same stage events as
+the timed steps. Collector pauses inside the region are reported.
 
 One JSON line is printed:
   value      = M / (ms_per_step) in NU pts/s (end to end, device-resident)
@@ -158,11 +160,11 @@ def bench_t3(args):
     c = (rng.uniform(0.2, 1.0, P) * np.exp(1j * rng.uniform(0, 2 * np.pi, P))).astype(np.complex64)
     cd = torch.from_numpy(c).cuda()
     plan = mn.Type3Plan(x, s, eps=3e-5, isign=+1, prec="crit64")
+    gc.collect()  # before the warm-up, not between it and the timed steps
     for _ in range(args.warmup):
         plan.execute(cd, return_np=False)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(args.steps)]
-    gc.collect()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for a, b in ev:
@@ -329,15 +331,25 @@ def main():
             plan.set_sources(tuple(xd))
         plan.execute(cd, return_np=False)
 
+    # A full collection of the interpreter's import-time objects takes 30-40 ms
+    # of host time; landing in the timed region it starves the GPU for that
+    # long. Collect and freeze them first (GC stays on; pauses are reported),
+    # before the warm-up: a GPU left idle for that long ran the next 8 or so
+    # steps at lower clocks (3.3 down to 2.83 ms).
+    gc.collect()
+    gc.freeze()
+    # The warm-up steps run as the timed ones do, stage events included;
+    # their times are dropped.
+    plan.profile = plan.profile_deferred = True
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    plan.drain_profiles()
     # Timed region: K steps between two synchronisations. HIP events on the
     # launch stream bracket every step and every stage (the spread kernel is
     # one launch per step); they are read only after the region ends.
     step_ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                for _ in range(args.steps)]
-    plan.profile = plan.profile_deferred = True
     host_ms, gc_ms, gc_t = [], [], [0.0]
 
     def gc_cb(phase, info):
@@ -346,11 +358,6 @@ def main():
         else:
             gc_ms.append((time.perf_counter() - gc_t[0]) * 1e3)
 
-    # A full collection of the interpreter's import-time objects takes 30-40 ms
-    # of host time; landing in the timed region it starves the GPU for that
-    # long. Collect and freeze them first (GC stays on; pauses are reported).
-    gc.collect()
-    gc.freeze()
     gc.callbacks.append(gc_cb)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
