@@ -230,25 +230,51 @@ __global__ __launch_bounds__(T) void k_fft64_lines(const double2 *__restrict__ i
     const int gap0 = nin - half;
     for (int e = tid; e < (n - nin) << lti; e += T)
         fl_buf[(gap0 + (e >> lti)) * ts + (e & lmask)] = make_double2(0.0, 0.0);
+    // All of a thread's loads (at most FV values and their dec factors) are
+    // issued before the first LDS write, at clamped (in-range) indices, so
+    // that they are in flight together; a load-then-store loop kept one
+    // load per thread in flight.
+    constexpr int FV = (VALS + T - 1) / T;
+    double2 fv[FV];
+    double fd[FV];
     if (Bn == 1) {
         const int64_t base = (int64_t)li0 * nin;
         const int cnt = min(ti, nlines - li0) * nin;
-        for (int e = tid; e < cnt; e += T) {
-            const int l = fdiv(e, nin, p.rnin), m = e - l * nin;
-            double2 v = in[base + e];
-            if (dec) v = dscale(v, dec[m]);
-            const int r = m < half ? m - half + n : m - half;
-            fl_buf[r * ts + l] = v;
+#pragma unroll
+        for (int i = 0; i < FV; ++i) {
+            const int e = min(tid + i * T, cnt - 1);
+            fv[i] = in[base + e];
+            fd[i] = dec ? dec[e - fdiv(e, nin, p.rnin) * nin] : 1.0;
+        }
+#pragma unroll
+        for (int i = 0; i < FV; ++i) {
+            const int e = tid + i * T;
+            if (e < cnt) {
+                const int l = fdiv(e, nin, p.rnin), m = e - l * nin;
+                const double2 v = dec ? dscale(fv[i], fd[i]) : fv[i];
+                const int r = m < half ? m - half + n : m - half;
+                fl_buf[r * ts + l] = v;
+            }
         }
     } else {
         const int a = li0 / Bn, b0 = li0 - a * Bn;
         const double2 *src = in + (int64_t)a * nin * Bn + b0;
-        for (int e = tid; e < nin << lti; e += T) {
-            const int m = e >> lti, l = e & lmask;
-            double2 v = src[(int64_t)m * Bn + l];
-            if (dec) v = dscale(v, dec[m]);
-            const int r = m < half ? m - half + n : m - half;
-            fl_buf[r * ts + l] = v;
+        const int cnt = nin << lti;
+#pragma unroll
+        for (int i = 0; i < FV; ++i) {
+            const int e = min(tid + i * T, cnt - 1);
+            fv[i] = src[(int64_t)(e >> lti) * Bn + (e & lmask)];
+            fd[i] = dec ? dec[e >> lti] : 1.0;
+        }
+#pragma unroll
+        for (int i = 0; i < FV; ++i) {
+            const int e = tid + i * T;
+            if (e < cnt) {
+                const int m = e >> lti, l = e & lmask;
+                const double2 v = dec ? dscale(fv[i], fd[i]) : fv[i];
+                const int r = m < half ? m - half + n : m - half;
+                fl_buf[r * ts + l] = v;
+            }
         }
     }
     __syncthreads();
