@@ -332,6 +332,9 @@ __global__ __launch_bounds__(DI_THREADS) void k_interp_direct(Geom g, float bl2e
     const float wz = es_weight((float)z - f2, bl2e, inv_hw);
     const int gz = wrap_tile_i(i2 + z, n2);
     float ar = 0.0f, ai = 0.0f;
+    // unrolled: the W x W loads stay in flight across x-planes (rolled, each
+    // plane waited for its W loads)
+#pragma unroll
     for (int a0 = 0; a0 < W; ++a0) {
         const int64_t gx = wrap_tile_i(i0 + a0, n0);
         const float2 *col = grid + gx * n1 * (int64_t)n2 + gz;
