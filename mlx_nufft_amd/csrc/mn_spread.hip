@@ -726,20 +726,31 @@ k_spread_owner_mfma(Geom g, float bl2e, float inv_hw, int64_t nbins,
         if (tid < 16) xcnt[tid] = 0;
         __syncthreads();
         constexpr int NI = MN_SUB_MAX_ORDER / OWN_THREADS;
-        int lx[NI], rk[NI], jj[NI];
+        // in steps over the thread's NI candidates, so that each step's
+        // loads are in flight together: the sorted indices, the x cells,
+        // then the y and z cells of the candidates that meet the bin in x
+        int lx[NI], rk[NI], jj[NI], cx[NI], cy[NI], cz[NI];
+        bool mx[NI];
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const int t = tid + OWN_THREADS * i;
+            jj[i] = t < cn ? point(c0 + t) : 0;
+        }
+#pragma unroll
+        for (int i = 0; i < NI; ++i) cx[i] = i1s.p[0][jj[i]];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            mx[i] = tid + OWN_THREADS * i < cn && meets(cx[i], 0);
+            cy[i] = mx[i] ? i1s.p[1][jj[i]] : 0;
+            cz[i] = mx[i] ? i1s.p[2][jj[i]] : 0;
+        }
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
             lx[i] = -1;
             rk[i] = 0;
-            jj[i] = 0;
-            if (t < cn) {
-                jj[i] = point(c0 + t);
-                const int ix = i1s.p[0][jj[i]];
-                if (meets(ix, 0) && meets(i1s.p[1][jj[i]], 1) && meets(i1s.p[2][jj[i]], 2)) {
-                    lx[i] = first_x(ix);
-                    rk[i] = atomicAdd(&xcnt[lx[i]], 1);
-                }
+            if (mx[i] && meets(cy[i], 1) && meets(cz[i], 2)) {
+                lx[i] = first_x(cx[i]);
+                rk[i] = atomicAdd(&xcnt[lx[i]], 1);
             }
         }
         __syncthreads();
