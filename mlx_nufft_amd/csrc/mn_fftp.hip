@@ -228,23 +228,30 @@ __global__ __launch_bounds__(FP_THREADS) void k_fft_axis(const float2 *__restric
             int t = 0, j = 0;
             bfly_of<TI, NJ>(b, contig, t, j);
             const int64_t lb = b < NB ? lbi[t] : -1;
+            if constexpr (PRUNE_OUT) {
 #pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                const int p = j + r * NJ;
-                float2 x = make_float2(0.f, 0.f);
-                if (lb >= 0) {
-                    if constexpr (PRUNE_OUT) {
-                        x = in[lb + (int64_t)p * a.inner];
-                    } else {
-                        const int i = mode_of<N>(p, a.M, a.hM);
-                        if (i >= 0) {
-                            const float2 y = in[lb + (int64_t)i * a.inner];
-                            const float d = a.dec[i];
-                            x = make_float2(y.x * d, y.y * d);
-                        }
-                    }
+                for (int r = 0; r < 8; ++r) {
+                    const int p = j + r * NJ;
+                    v[m][r] = lb >= 0 ? in[lb + (int64_t)p * a.inner] : make_float2(0.f, 0.f);
                 }
-                v[m][r] = x;
+            } else {
+                // every mode and factor load is issued (at index 0 where no
+                // mode is kept) before any is used: loaded and scaled inside
+                // a branch, each waited for its own pair of loads
+                float2 y[8];
+                float d[8];
+                bool ok[8];
+#pragma unroll
+                for (int r = 0; r < 8; ++r) {
+                    const int i = mode_of<N>(j + r * NJ, a.M, a.hM);
+                    ok[r] = lb >= 0 && i >= 0;
+                    y[r] = in[ok[r] ? lb + (int64_t)i * a.inner : 0];
+                    d[r] = a.dec[ok[r] ? i : 0];
+                }
+#pragma unroll
+                for (int r = 0; r < 8; ++r)
+                    v[m][r] = ok[r] ? make_float2(y[r].x * d[r], y[r].y * d[r])
+                                    : make_float2(0.f, 0.f);
             }
         }
 #pragma unroll
