@@ -285,6 +285,18 @@ __global__ __launch_bounds__(FP_THREADS) void k_fft_axis(const float2 *__restric
             if (b < NB) {
                 int t, j;
                 bfly_of<TI, NJ>(b, contig, t, j);
+                // the kept modes' deconvolution factors are loaded first, all
+                // at once, under the LDS reads and the DFT (loaded at the
+                // store, each waited for its own)
+                int im[RL];
+                float dm[RL];
+                if constexpr (PRUNE_OUT) {
+#pragma unroll
+                    for (int r = 0; r < RL; ++r) {
+                        im[r] = mode_of<N>(j + r * NJ, a.M, a.hM);
+                        dm[r] = a.dec[im[r] >= 0 ? im[r] : 0];
+                    }
+                }
                 float2 v[RL];
 #pragma unroll
                 for (int r = 0; r < RL; ++r) v[r] = buf[lds_at<TI>(j + r * NJ, t)];
@@ -297,12 +309,9 @@ __global__ __launch_bounds__(FP_THREADS) void k_fft_axis(const float2 *__restric
                     for (int r = 0; r < RL; ++r) {
                         const int p = j + r * NJ;  // natural-order output position
                         if constexpr (PRUNE_OUT) {
-                            const int i = mode_of<N>(p, a.M, a.hM);
-                            if (i >= 0) {
-                                const float d = a.dec[i];
-                                store_out(out, lb + (int64_t)i * a.inner,
-                                          make_float2(v[r].x * d, v[r].y * d), contig);
-                            }
+                            if (im[r] >= 0)
+                                store_out(out, lb + (int64_t)im[r] * a.inner,
+                                          make_float2(v[r].x * dm[r], v[r].y * dm[r]), contig);
                         } else {
                             store_out(out, lb + (int64_t)p * a.inner, v[r], contig);
                         }
