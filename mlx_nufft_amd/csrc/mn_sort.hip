@@ -1,6 +1,7 @@
 // Stable bin sort and subproblem tables.
 //
-// The bin sort is an LSD radix sort over 8-bit digits of the bin key. Each
+// The bin sort is an LSD radix sort over digits of the bin key (at most 8
+// bits, the key split evenly over the passes). Each
 // pass is (1) a per-tile digit histogram, (2) an exclusive scan of each
 // digit's counts over the tiles (the scatter adds the digit bases, the scan
 // of the 256 digit totals), (3) a stable scatter in which every tile
@@ -111,8 +112,11 @@ __global__ void k_tile_scan(uint32_t *__restrict__ d, int64_t n,
 
 // ---------------------------------------------------------- radix sort ----
 
-__device__ __forceinline__ uint32_t digit_of(uint32_t k, uint32_t kmask, int shift) {
-    return ((k & kmask) >> shift) & (RS_RADIX - 1);
+// The pass's digit: width bits of the masked key from shift on, dmask =
+// 2^width - 1 (width <= 8).
+__device__ __forceinline__ uint32_t digit_of(uint32_t k, uint32_t kmask, int shift,
+                                             uint32_t dmask) {
+    return ((k & kmask) >> shift) & dmask;
 }
 
 // Row d of the digit-major histogram (hist[d * nblk + t], t = tile) scanned
@@ -149,6 +153,7 @@ __global__ __launch_bounds__(SC_THREADS) void k_digit_scan(uint32_t *__restrict_
 
 __global__ __launch_bounds__(RS_THREADS) void k_radix_hist(const uint32_t *__restrict__ keys,
                                                            int64_t P, int shift, uint32_t kmask,
+                                                           uint32_t dmask,
                                                            uint32_t *__restrict__ hist,
                                                            int64_t nblk) {
     __shared__ uint32_t h[RS_RADIX];
@@ -167,7 +172,7 @@ __global__ __launch_bounds__(RS_THREADS) void k_radix_hist(const uint32_t *__res
 #pragma unroll
     for (int i = 0; i < RS_ITEMS; ++i) {
         int64_t idx = base + (int64_t)i * RS_THREADS + threadIdx.x;
-        if (idx < P) atomicAdd(&h[digit_of(kv[i], kmask, shift)], 1u);
+        if (idx < P) atomicAdd(&h[digit_of(kv[i], kmask, shift, dmask)], 1u);
     }
     __syncthreads();
     hist[(int64_t)threadIdx.x * nblk + tile] = h[threadIdx.x];
@@ -196,7 +201,7 @@ struct SortCols {
 // for one digit meet in the same L2 and leave as whole lines.
 __global__ __launch_bounds__(ST_THREADS) void k_radix_scatter(
     const uint32_t *__restrict__ kin, const uint32_t *__restrict__ vin, int64_t P, int shift,
-    uint32_t kmask, const uint32_t *__restrict__ offs, const uint32_t *__restrict__ totals,
+    uint32_t kmask, uint32_t dmask, const uint32_t *__restrict__ offs, const uint32_t *__restrict__ totals,
     int64_t nblk, uint32_t *__restrict__ kout, uint32_t *__restrict__ vout, int ncols,
     SortCols cols) {
     static_assert(ST_THREADS >= RS_RADIX, "a thread per digit");
@@ -235,7 +240,7 @@ __global__ __launch_bounds__(ST_THREADS) void k_radix_scatter(
         const int q = wbase + r * 64 + lane;
         const bool valid = q < nvalid;
         const uint32_t k = kv[r];
-        const uint32_t dg = digit_of(k, kmask, shift);
+        const uint32_t dg = digit_of(k, kmask, shift, dmask);
         uint64_t peers = __ballot(valid);
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
@@ -286,7 +291,7 @@ __global__ __launch_bounds__(ST_THREADS) void k_radix_scatter(
         dst[r] = 0;
         if (q < nvalid) {
             const uint32_t k = stage[q];
-            const uint32_t d = digit_of(k, kmask, shift);
+            const uint32_t d = digit_of(k, kmask, shift, dmask);
             dst[r] = gbase[d] + (uint32_t)q - lstart[d];
             kout[dst[r]] = k;
         }
@@ -535,6 +540,9 @@ int mn_sort_pairs(int64_t P, int key_bits, const uint32_t *key_in, uint32_t *key
     SortWs w = sort_layout(P, ncols, static_cast<char *>(ws));
     MN_REQUIRE(ws_bytes >= w.bytes, "sort: workspace too small");
     hipStream_t s = as_stream(stream);
+    // Passes of at most 8 bits, the key split evenly over them (the first
+    // ones a bit wider): a 22-bit key as 8 + 7 + 7 bits, so no pass has
+    // 256 digits where 128 do
     const int npass = key_bits <= 0 ? 1 : (key_bits + 7) / 8;
     const uint32_t kmask = key_bits >= 32 ? 0xFFFFFFFFu : ((1u << key_bits) - 1u);
     const int64_t nblk = (P + RS_TILE - 1) / RS_TILE;
@@ -542,20 +550,24 @@ int mn_sort_pairs(int64_t P, int key_bits, const uint32_t *key_in, uint32_t *key
     const uint32_t *vsrc = nullptr;  // identity values on the first pass
     SortCols cur{};
     for (int c = 0; c < ncols; ++c) cur.in[c] = user.in[c];
+    int shift = 0;
     for (int p = 0; p < npass; ++p) {
         const bool to_out = ((npass - 1 - p) % 2) == 0;
         uint32_t *kdst = to_out ? key_out : w.kalt;
         uint32_t *vdst = to_out ? perm_out : w.valt;
         for (int c = 0; c < ncols; ++c) cur.out[c] = to_out ? user.out[c] : w.calt[c];
-        const int shift = 8 * p;
-        k_radix_hist<<<(unsigned)nblk, RS_THREADS, 0, s>>>(ksrc, P, shift, kmask, w.hist, nblk);
+        const int width = key_bits <= 0 ? 8 : key_bits / npass + (p < key_bits % npass ? 1 : 0);
+        const uint32_t dmask = (1u << width) - 1u;
+        k_radix_hist<<<(unsigned)nblk, RS_THREADS, 0, s>>>(ksrc, P, shift, kmask, dmask, w.hist,
+                                                           nblk);
         MN_LAUNCH_CHECK("radix hist");
         k_digit_scan<<<RS_RADIX, SC_THREADS, 0, s>>>(w.hist, nblk, w.totals);
         MN_LAUNCH_CHECK("radix digit scan");
-        k_radix_scatter<<<(unsigned)nblk, ST_THREADS, 0, s>>>(ksrc, vsrc, P, shift, kmask, w.hist,
-                                                             w.totals, nblk, kdst, vdst, ncols,
-                                                             cur);
+        k_radix_scatter<<<(unsigned)nblk, ST_THREADS, 0, s>>>(ksrc, vsrc, P, shift, kmask, dmask,
+                                                             w.hist, w.totals, nblk, kdst, vdst,
+                                                             ncols, cur);
         MN_LAUNCH_CHECK("radix scatter");
+        shift += width;
         ksrc = kdst;
         vsrc = vdst;
         for (int c = 0; c < ncols; ++c) cur.in[c] = cur.out[c];

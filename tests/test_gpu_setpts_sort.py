@@ -101,8 +101,9 @@ def test_sort_matches_numpy_stable(case, oracle):
 def test_sort_pairs_payload(P, nbits, ncols):
     """Stable sort on the low nbits of each key, bits above nbits travelling
     with the key, and payload columns following their keys: against numpy's
-    stable argsort. Key widths from one pass (5, 7) to four (25, 32), with
-    a last pass of 1 to 8 bits. The 22-bit case has 4097 tiles of 8192
+    stable argsort. Key widths from one pass (5, 7) to four (25, 32); the
+    passes split the key evenly (10 bits as 5 + 5, 17 as 6 + 6 + 5, 22 as
+    8 + 7 + 7, 25 as 7 + 6 + 6 + 6). The 22-bit case has 4097 tiles of 8192
     keys, so the per-digit scan over the tiles runs its carry loop twice;
     the 11-bit case fills exactly three tiles."""
     from mlx_nufft_amd import _engine as E
