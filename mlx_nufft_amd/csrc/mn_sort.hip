@@ -175,7 +175,8 @@ __global__ __launch_bounds__(RS_THREADS) void k_radix_hist(const uint32_t *__res
         if (idx < P) atomicAdd(&h[digit_of(kv[i], kmask, shift, dmask)], 1u);
     }
     __syncthreads();
-    hist[(int64_t)threadIdx.x * nblk + tile] = h[threadIdx.x];
+    // rows of the pass's 2^width digits only; the digit scan reads no others
+    if (threadIdx.x <= dmask) hist[(int64_t)threadIdx.x * nblk + tile] = h[threadIdx.x];
 }
 
 struct SortCols {
@@ -215,11 +216,12 @@ __global__ __launch_bounds__(ST_THREADS) void k_radix_scatter(
     const int64_t base = tile * RS_TILE;
     const int nvalid = (int)((P - base) < RS_TILE ? (P - base) : RS_TILE);
     const bool dt = tid < RS_RADIX;  // a thread per digit
+    const bool du = tid <= (int)dmask;  // a digit of this pass (scanned over the tiles)
     {
         // the digit's base (all smaller digits) plus the tiles before this one
-        const uint32_t toff = dt ? offs[(int64_t)tid * nblk + tile] : 0u;
+        const uint32_t toff = du ? offs[(int64_t)tid * nblk + tile] : 0u;
         uint32_t all;
-        const uint32_t ex = block_excl_scan_n<ST_THREADS>(dt ? totals[tid] : 0u, &all);
+        const uint32_t ex = block_excl_scan_n<ST_THREADS>(du ? totals[tid] : 0u, &all);
         if (dt) gbase[tid] = ex + toff;
     }
 #pragma unroll
@@ -561,7 +563,7 @@ int mn_sort_pairs(int64_t P, int key_bits, const uint32_t *key_in, uint32_t *key
         k_radix_hist<<<(unsigned)nblk, RS_THREADS, 0, s>>>(ksrc, P, shift, kmask, dmask, w.hist,
                                                            nblk);
         MN_LAUNCH_CHECK("radix hist");
-        k_digit_scan<<<RS_RADIX, SC_THREADS, 0, s>>>(w.hist, nblk, w.totals);
+        k_digit_scan<<<dmask + 1, SC_THREADS, 0, s>>>(w.hist, nblk, w.totals);
         MN_LAUNCH_CHECK("radix digit scan");
         k_radix_scatter<<<(unsigned)nblk, ST_THREADS, 0, s>>>(ksrc, vsrc, P, shift, kmask, dmask,
                                                              w.hist, w.totals, nblk, kdst, vdst,
