@@ -151,32 +151,60 @@ __global__ __launch_bounds__(SC_THREADS) void k_digit_scan(uint32_t *__restrict_
     if (threadIdx.x == 0) totals[blockIdx.x] = carry;
 }
 
+// Per-tile digit counts. Each wave counts into its own LDS histogram (fewer
+// same-address atomics than one shared by the workgroup); whole tiles of a
+// 16-byte aligned key array are read as 16-byte vectors.
 __global__ __launch_bounds__(RS_THREADS) void k_radix_hist(const uint32_t *__restrict__ keys,
                                                            int64_t P, int shift, uint32_t kmask,
                                                            uint32_t dmask,
                                                            uint32_t *__restrict__ hist,
                                                            int64_t nblk) {
-    __shared__ uint32_t h[RS_RADIX];
-    h[threadIdx.x] = 0;
+    static_assert(RS_THREADS == RS_RADIX, "a thread per digit");
+    constexpr int NW = RS_THREADS / 64;
+    __shared__ uint32_t h[NW][RS_RADIX];
+    const int tid = threadIdx.x, wv = tid >> 6;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) h[w][tid] = 0;
     __syncthreads();
     // tiles XCD-contiguous, as in the scatter: a digit row's entries of
     // neighbouring tiles then leave one L2 as whole lines
     const int64_t tile = xcd_remap(blockIdx.x, nblk);
-    int64_t base = tile * RS_TILE;
-    uint32_t kv[RS_ITEMS];
+    const int64_t base = tile * RS_TILE;
+    const bool vec = base + RS_TILE <= P && (reinterpret_cast<uintptr_t>(keys) & 15) == 0;
+    if (vec) {
+        constexpr int NV = RS_ITEMS / 4;
+        const uint4 *k4 = reinterpret_cast<const uint4 *>(keys + base);
+        uint4 kv[NV];
 #pragma unroll
-    for (int i = 0; i < RS_ITEMS; ++i) {
-        int64_t idx = base + (int64_t)i * RS_THREADS + threadIdx.x;
-        kv[i] = idx < P ? keys[idx] : 0u;
-    }
+        for (int i = 0; i < NV; ++i) kv[i] = k4[i * RS_THREADS + tid];
 #pragma unroll
-    for (int i = 0; i < RS_ITEMS; ++i) {
-        int64_t idx = base + (int64_t)i * RS_THREADS + threadIdx.x;
-        if (idx < P) atomicAdd(&h[digit_of(kv[i], kmask, shift, dmask)], 1u);
+        for (int i = 0; i < NV; ++i) {
+            atomicAdd(&h[wv][digit_of(kv[i].x, kmask, shift, dmask)], 1u);
+            atomicAdd(&h[wv][digit_of(kv[i].y, kmask, shift, dmask)], 1u);
+            atomicAdd(&h[wv][digit_of(kv[i].z, kmask, shift, dmask)], 1u);
+            atomicAdd(&h[wv][digit_of(kv[i].w, kmask, shift, dmask)], 1u);
+        }
+    } else {
+        uint32_t kv[RS_ITEMS];
+#pragma unroll
+        for (int i = 0; i < RS_ITEMS; ++i) {
+            const int64_t idx = base + (int64_t)i * RS_THREADS + tid;
+            kv[i] = idx < P ? keys[idx] : 0u;
+        }
+#pragma unroll
+        for (int i = 0; i < RS_ITEMS; ++i) {
+            const int64_t idx = base + (int64_t)i * RS_THREADS + tid;
+            if (idx < P) atomicAdd(&h[wv][digit_of(kv[i], kmask, shift, dmask)], 1u);
+        }
     }
     __syncthreads();
     // rows of the pass's 2^width digits only; the digit scan reads no others
-    if (threadIdx.x <= dmask) hist[(int64_t)threadIdx.x * nblk + tile] = h[threadIdx.x];
+    if (tid <= (int)dmask) {
+        uint32_t s = 0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) s += h[w][tid];
+        hist[(int64_t)tid * nblk + tile] = s;
+    }
 }
 
 struct SortCols {
