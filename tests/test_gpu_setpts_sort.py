@@ -126,6 +126,30 @@ def test_sort_pairs_payload(P, nbits, ncols):
         assert np.array_equal(o.cpu().numpy(), c[ref])
 
 
+@pytest.mark.parametrize("offset", [1, 3])
+def test_sort_pairs_misaligned_keys(offset):
+    """Keys that start 4 or 12 bytes past a 16-byte boundary: the histogram
+    pass reads whole tiles as 16-byte vectors only from aligned key arrays,
+    and element by element otherwise. Five whole 8192-key tiles and a
+    partial one, against numpy's stable argsort."""
+    from mlx_nufft_amd import _engine as E
+
+    P, nbits = 8192 * 5 + 17, 22
+    print(f"case sort_pairs misaligned offset={offset}", flush=True)
+    rng = np.random.default_rng(40 + offset)
+    key = rng.integers(0, 1 << 32, P, dtype=np.uint64).astype(np.uint32)
+    key[rng.integers(0, P, P // 4)] = key[0]   # ties
+    col = rng.integers(-2**31, 2**31, P, dtype=np.int64).astype(np.int32)
+    padded = np.concatenate([np.zeros(offset, np.uint32), key])
+    kd = torch.from_numpy(padded.view(np.int32)).cuda()[offset:]
+    assert kd.data_ptr() % 16 == 4 * offset
+    skey, perm, outs = E.sort_pairs(kd, nbits, [torch.from_numpy(col).cuda()])
+    ref = np.argsort(key & np.uint32((1 << nbits) - 1), kind="stable")
+    assert np.array_equal(perm.cpu().numpy().view(np.uint32), ref.astype(np.uint32))
+    assert np.array_equal(skey.cpu().numpy().view(np.uint32), key[ref])
+    assert np.array_equal(outs[0].cpu().numpy(), col[ref])
+
+
 @pytest.mark.parametrize("msub", [1024, 7])
 def test_subproblem_table(msub, oracle):
     from mlx_nufft_amd import _engine as E
