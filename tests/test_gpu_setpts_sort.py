@@ -97,13 +97,15 @@ def test_sort_matches_numpy_stable(case, oracle):
                                              (300_001, 23, 3), (1_000_000, 32, 8),
                                              (65_536, 16, 6), (4096 * 8192 + 3, 22, 1),
                                              (50_001, 10, 2), (200_003, 17, 1),
-                                             (100_000, 25, 0), (8192 * 3, 11, 3)])
+                                             (100_000, 25, 0), (8192 * 3, 11, 3),
+                                             (70_001, 9, 1), (1000, 0, 1)])
 def test_sort_pairs_payload(P, nbits, ncols):
     """Stable sort on the low nbits of each key, bits above nbits travelling
     with the key, and payload columns following their keys: against numpy's
     stable argsort. Key widths from one pass (5, 7) to four (25, 32); the
-    passes split the key evenly (10 bits as 5 + 5, 17 as 6 + 6 + 5, 22 as
-    8 + 7 + 7, 25 as 7 + 6 + 6 + 6). The 22-bit case has 4097 tiles of 8192
+    passes split the key evenly (9 bits as 5 + 4, 10 as 5 + 5, 17 as
+    6 + 6 + 5, 22 as 8 + 7 + 7, 25 as 7 + 6 + 6 + 6); 0 bits leave the
+    order unchanged. The 22-bit case has 4097 tiles of 8192
     keys, so the per-digit scan over the tiles runs its carry loop twice;
     the 11-bit case fills exactly three tiles."""
     from mlx_nufft_amd import _engine as E
